@@ -1,0 +1,215 @@
+/*
+ * zipserv.h -- C-ABI of the MI355X (gfx950) ZipServ hot path.
+ *
+ * Every entry point mirrors one reference interface (cited as
+ * file:line relative to the reference checkout) with plain pointers and
+ * sizes: bf16 data is passed as uint16_t bit patterns, streams as
+ * hipStream_t cast to void*.  All device entry points are stream-ordered and
+ * asynchronous; none allocates, synchronises or prints.
+ *
+ * Status codes: ZS_OK (0); negative ZS_E_* for argument / capability errors
+ * detected on the host before any launch; a positive value is a hipError_t
+ * reported by the HIP runtime for a launch.
+ *
+ * Canonical TCA-TBE format (shared by every entry point): M x K bf16 matrix,
+ * M and K multiples of 64, cut into 64x64 global tiles (row-major over
+ * tiles), each into four 16x64 median tiles, each into sixteen 8x8 small
+ * tiles visited as 2x2 groups in column-major order.  Per small tile: three
+ * u64 bit-planes of a 3-bit code (0 = outlier, 1..7 = exponent
+ * start_exp + code), one sign|mantissa byte per in-window element (SM
+ * stream), one raw bf16 per outlier (FULL stream).  Streams are padded to 16
+ * bytes / 8 elements per global tile.  TileOffsets_Global holds
+ * num_global_tiles + 1 (SM, FULL) cumulative pairs, TileOffsets_Median the
+ * 4 per-tile (SM, FULL) starts of each median tile.
+ *
+ * Device SM and FULL buffers must stay readable for ZS_STREAM_SLACK_BYTES
+ * bytes past the end of their streams (the decoder loads aligned 16-byte
+ * windows).  Buffers produced by zs_init_bf16_matrix_triple_bitmap_gpu with
+ * the worst-case sizes of zs_sign_mantissa_capacity / zs_full_capacity
+ * satisfy this.
+ */
+#ifndef ZIPSERV_H
+#define ZIPSERV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ZS_OK 0
+#define ZS_E_INVAL (-1)       /* bad shape, null pointer, bad tile size     */
+#define ZS_E_UNSUPPORTED (-2) /* valid request this build does not handle  */
+#define ZS_E_OVERFLOW (-3)    /* offsets would not fit the int32 format    */
+#define ZS_E_NOMEM (-4)       /* host allocation failed                    */
+
+#define ZS_STREAM_SLACK_BYTES 64
+
+/* KV layouts of a compressed cache (flash.h:19-20). */
+#define ZS_LAYOUT_HEAD_MAJOR 0 /* rows = ((b * Hkv + h) * rows_per_head + t) */
+#define ZS_LAYOUT_TOKEN_MAJOR 1 /* rows = b * batch_stride + t * Hkv + h      */
+
+const char* zs_version(void);
+const char* zs_status_string(int status);
+
+/* ---------------------------------------------------------------------- */
+/* Size queries (no counterpart function in the reference; they state the  */
+/* worst-case allocations of zipserv_decode_attention_ext.cu:177-199 and    */
+/* the size formula of bench_zipserv_gemm_sweep.cu:424-429).                */
+/* ---------------------------------------------------------------------- */
+int64_t zs_num_global_tiles(int M, int K);
+int64_t zs_sign_mantissa_capacity(int M, int K); /* bytes, incl. slack      */
+int64_t zs_full_capacity(int M, int K);          /* bf16 elements, incl. slack */
+/* Compressed size of the GEMM path: SM + 2*FULL + bitmaps + median + global. */
+int64_t zs_compressed_bytes(int M, int K, int64_t total_high_freq, int64_t total_full);
+/* Bytes of Reduction_Workspace needed by zs_bf16_triple_bitmap_mm. */
+int64_t zs_splitk_workspace_bytes(int M, int N, int split_k);
+
+/* ---------------------------------------------------------------------- */
+/* Host codec (CPU)                                                         */
+/* ---------------------------------------------------------------------- */
+
+/* kernel_benchmark/utils.h:189-272 analyzeExponentDistribution_BF16:
+ * window of 7 contiguous exponents; top_exponents[i] = start + i. */
+int zs_analyze_exponents_host(const uint16_t* a, int64_t n, int32_t top_exponents[7]);
+
+/* build/L_API.cuh:53-73 InitBF16MatrixTripleBitmap.  Allocates every output
+ * (release each with zs_host_free); returns the number of global tiles or a
+ * negative status.  Tile sizes must be (8,16,64, 8,64,64). */
+int zs_init_bf16_matrix_triple_bitmap(
+    const uint16_t* A, int M, int K, int tile_M, int tile_M_median, int tile_M_global, int tile_K,
+    int tile_K_median, int tile_K_global, const int32_t* top_exponents, uint8_t** sign_mantissa,
+    uint16_t** compressed_full, uint64_t** bitmap1, uint64_t** bitmap2, uint64_t** bitmap3,
+    int32_t** tile_offsets, int32_t** tile_offsets_median, int32_t** tile_offsets_global,
+    int32_t* max_high_freq_count, int32_t* max_full_count);
+void zs_host_free(void* p);
+
+/* build/L_API.cuh:76-107 InitBF16MatrixTripleBitmap_Reuse: caller buffers
+ * (SM >= M*K bytes, FULL >= M*K elements, temp_sm num_GT*(4096+15) bytes,
+ * temp_full num_GT*(4096+7) elements, gt_* num_GT, *_offsets num_GT+1).
+ * Accepts any 7 distinct exponents. */
+int zs_init_bf16_matrix_triple_bitmap_reuse(
+    const uint16_t* A, int M, int K, int tile_M, int tile_M_median, int tile_M_global, int tile_K,
+    int tile_K_median, int tile_K_global, const int32_t* top_exponents, uint8_t* sign_mantissa,
+    uint16_t* compressed_full, uint64_t* bitmap1, uint64_t* bitmap2, uint64_t* bitmap3,
+    int32_t* tile_offsets, int32_t* tile_offsets_median, int32_t* tile_offsets_global,
+    uint8_t* temp_sm, uint16_t* temp_full, int32_t* gt_hf_count, int32_t* gt_full_count,
+    int32_t* hf_offsets, int32_t* full_offsets, int32_t* max_high_freq_count,
+    int32_t* max_full_count, int32_t* out_total_hf, int32_t* out_total_full);
+
+/* build/L_API.cuh:109-141 InitBF16MatrixTripleBitmap_Reuse_SIMD: same
+ * buffers; the window is taken as [top_exponents[0], top_exponents[0]+6]. */
+int zs_init_bf16_matrix_triple_bitmap_reuse_simd(
+    const uint16_t* A, int M, int K, int tile_M, int tile_M_median, int tile_M_global, int tile_K,
+    int tile_K_median, int tile_K_global, const int32_t* top_exponents, uint8_t* sign_mantissa,
+    uint16_t* compressed_full, uint64_t* bitmap1, uint64_t* bitmap2, uint64_t* bitmap3,
+    int32_t* tile_offsets, int32_t* tile_offsets_median, int32_t* tile_offsets_global,
+    uint8_t* temp_sm, uint16_t* temp_full, int32_t* gt_hf_count, int32_t* gt_full_count,
+    int32_t* hf_offsets, int32_t* full_offsets, int32_t* max_high_freq_count,
+    int32_t* max_full_count, int32_t* out_total_hf, int32_t* out_total_full);
+
+/* ---------------------------------------------------------------------- */
+/* Device codec and kernels (gfx950)                                        */
+/* ---------------------------------------------------------------------- */
+
+/* build/L_API.cuh:38-52 BF16TripleBitmap_Decompress_API: TCA-TBE -> dense
+ * Output[M][K] bf16, bit-exact. */
+int zs_bf16_triple_bitmap_decompress(void* stream, const uint8_t* SignMantissa,
+                                     const uint16_t* CompressedFull, const uint64_t* Bitmap1,
+                                     const uint64_t* Bitmap2, const uint64_t* Bitmap3,
+                                     const int32_t* TileOffsets_Median,
+                                     const int32_t* TileOffsets_Global, int max_high_freq_count,
+                                     int max_full_count, uint8_t start_exp, uint16_t* Output,
+                                     int M_Global, int K_Global);
+
+/* build/L_API.cuh:19-37 BF16TripleBitmap_MM_API: C[N][M] = B[N][K] . W[M][K]^T
+ * with W in TCA-TBE, fp32 accumulation, bf16 output.  Split_K > 1 writes
+ * bf16 partial slabs [Split_K][N][M] into Reduction_Workspace (at least
+ * zs_splitk_workspace_bytes) and sums them in fp32 (Reduction_Kernel.cuh). */
+int zs_bf16_triple_bitmap_mm(void* stream, const uint8_t* SignMantissa,
+                             const uint16_t* CompressedFull, const uint64_t* Bitmap1,
+                             const uint64_t* Bitmap2, const uint64_t* Bitmap3,
+                             const int32_t* TileOffsets_Median, const int32_t* TileOffsets_Global,
+                             int max_high_freq_count, int max_full_count, uint8_t start_exp,
+                             const uint16_t* B, uint16_t* C, int M_Global, int N_Global,
+                             int K_Global, uint16_t* Reduction_Workspace, int Split_K);
+
+/* kernel_benchmark/zipserv_decode_attention_ext.cu:137-153
+ * AnalyzeTopExponentsGPU: 256-bin histogram of d_input (d_exponent_counts,
+ * 256 int32) and the GPU window selection (ext.cu:65-134) into
+ * d_top_exponents[7].  d_done_counter (1 int32) is cleared and unused. */
+int zs_analyze_top_exponents_gpu(void* stream, const uint16_t* d_input, int64_t numel,
+                                 int32_t* d_exponent_counts, int32_t* d_top_exponents,
+                                 int32_t* d_done_counter);
+
+/* build/L_API.cuh:144-165 InitBF16MatrixTripleBitmap_GPU: device encoder
+ * producing the canonical streams.  d_temp_sm / d_temp_full are accepted for
+ * signature parity and may be NULL (the encoder re-reads d_input instead of
+ * staging per-tile streams).  d_hf_offsets / d_full_offsets (num_GT + 1) and
+ * the four scalars are written as in the reference. */
+int zs_init_bf16_matrix_triple_bitmap_gpu(
+    void* stream, const uint16_t* d_input, int M, int K, const int32_t* d_top_exponents,
+    uint8_t* d_sign_mantissa, uint16_t* d_compressed_full, uint64_t* d_bitmap1,
+    uint64_t* d_bitmap2, uint64_t* d_bitmap3, int32_t* d_tile_offsets,
+    int32_t* d_tile_offsets_median, int32_t* d_tile_offsets_global, uint8_t* d_temp_sm,
+    uint16_t* d_temp_full, int32_t* d_gt_hf_count, int32_t* d_gt_full_count,
+    int32_t* d_hf_offsets, int32_t* d_full_offsets, int32_t* d_max_hf_count,
+    int32_t* d_max_full_count, int32_t* d_total_hf, int32_t* d_total_full);
+
+/* ---------------------------------------------------------------------- */
+/* Decode attention over a compressed KV cache                              */
+/* ---------------------------------------------------------------------- */
+
+/* One compressed K or V cache (flash.h:51-68 ZipservCompressedKVParams; the
+ * 12 fields of flash_attn_interface.py:23-36 plus the strides derived by
+ * _normalize_zipserv_kv, flash_attn_interface.py:75-128). */
+typedef struct zs_kv_compressed {
+  const uint8_t* sign_mantissa;
+  const uint16_t* compressed_full;
+  const uint64_t* bitmap1;
+  const uint64_t* bitmap2;
+  const uint64_t* bitmap3;
+  const int32_t* tile_offsets_median;
+  const int32_t* tile_offsets_global;
+  int32_t rows;              /* padded rows of the 2D matrix                 */
+  int32_t cols;              /* padded head_dim (multiple of 64)            */
+  int32_t batch_stride_rows; /* rows / batch                                */
+  int32_t head_stride_rows;  /* batch_stride_rows / num_heads_k             */
+  int32_t max_high_freq_count;
+  int32_t max_full_count;
+  int32_t start_exp;
+  int32_t layout; /* ZS_LAYOUT_*                                           */
+} zs_kv_compressed_t;
+
+/* flash_attn_interface.py:1572-1706 flash_attn_with_kvcache(...,
+ * zipserv_k=, zipserv_v=) -> flash_api.cpp:1346-1520 mha_fwd_kvcache for one
+ * query token (decode): out[b][h] = softmax(scale * q[b][h] . K[b][:L_b][h/G])
+ * . V[b][:L_b][h/G], G = num_heads / num_heads_k, fp32 online softmax.
+ * q, out: [batch][num_heads][head_dim] bf16.  L_b = cache_seqlens[b] (device
+ * int32 [batch]) or seqlen_k when cache_seqlens is NULL.  softmax_lse
+ * (optional, [batch][num_heads] fp32) is the natural-log normaliser.
+ * num_splits = 0 picks a split of the sequence across workgroups; splits > 1
+ * need `workspace` of zs_decode_attention_workspace_bytes bytes. */
+int zs_decode_attention(void* stream, const uint16_t* q, const zs_kv_compressed_t* k,
+                        const zs_kv_compressed_t* v, const int32_t* cache_seqlens, int seqlen_k,
+                        int batch, int num_heads, int num_heads_k, int head_dim,
+                        float softmax_scale, uint16_t* out, float* softmax_lse, void* workspace,
+                        size_t workspace_bytes, int num_splits);
+size_t zs_decode_attention_workspace_bytes(int batch, int num_heads, int head_dim, int seqlen_k,
+                                           int num_splits);
+
+/* The uncompressed comparator (bench_zipserv_decode_attention.py:629-631,
+ * dense flash_attn_with_kvcache): same kernel with K/V read from dense bf16
+ * caches k_cache / v_cache [batch][cache_capacity][num_heads_k][head_dim]. */
+int zs_decode_attention_dense(void* stream, const uint16_t* q, const uint16_t* k_cache,
+                              const uint16_t* v_cache, const int32_t* cache_seqlens,
+                              int seqlen_k, int cache_capacity, int batch, int num_heads,
+                              int num_heads_k, int head_dim, float softmax_scale, uint16_t* out,
+                              float* softmax_lse, void* workspace, size_t workspace_bytes,
+                              int num_splits);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ZIPSERV_H */

@@ -1,0 +1,128 @@
+"""Pins the oracle's GEMM, split-K and decode-attention references against
+numpy float64 math and closed-form special cases."""
+import numpy as np
+import pytest
+
+import oracle as zo
+from zs_testutil import normal_bf16, weights_bf16
+
+
+def test_bf16_rounding_helpers():
+    x = np.array([1.0, 1.00390625, 1.005859375, -2.5, 3.4e38, 1e-40], np.float32)
+    b = zo.f32_to_bf16(x)
+    # 1 + 2^-8 is a tie -> even (1.0); 1 + 1.5*2^-8 rounds up to 1 + 2^-7
+    assert b.tolist()[:4] == [0x3F80, 0x3F80, 0x3F81, 0xC020]
+    for v, bb in zip(x, b):
+        assert zo.lib().zso_f32_to_bf16(float(v)) == int(bb)
+    np.testing.assert_array_equal(zo.bf16_to_f32(np.array([0x3F80, 0xC020], np.uint16)),
+                                  np.array([1.0, -2.5], np.float32))
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 1, 64), (128, 8, 192), (64, 17, 256)])
+def test_gemm_f32_matches_float64(M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    W = weights_bf16(rng, (M, K), outlier_frac=0.01)
+    X = normal_bf16(rng, (N, K))
+    Y = zo.gemm_f32(W, X)
+    ref = zo.bf16_to_f32(X).astype(np.float64) @ zo.bf16_to_f32(W).astype(np.float64).T
+    assert Y.shape == (N, M)
+    np.testing.assert_allclose(Y, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+
+
+def test_gemm_unit_vectors_extract_columns():
+    rng = np.random.default_rng(5)
+    M, K = 64, 128
+    W = weights_bf16(rng, (M, K), outlier_frac=0.05)
+    ks = [0, 1, 63, 64, 127]
+    X = np.zeros((len(ks), K), np.uint16)
+    for i, k in enumerate(ks):
+        X[i, k] = 0x3F80
+    Y = zo.gemm_f32(W, X)
+    for i, k in enumerate(ks):
+        np.testing.assert_array_equal(zo.f32_to_bf16(Y[i]), W[:, k])
+
+
+def test_splitk_one_is_rounded_gemm():
+    rng = np.random.default_rng(9)
+    W = weights_bf16(rng, (64, 256))
+    X = normal_bf16(rng, (4, 256))
+    np.testing.assert_array_equal(zo.gemm_splitk_bf16(W, X, 1), zo.f32_to_bf16(zo.gemm_f32(W, X)))
+
+
+@pytest.mark.parametrize("S", [2, 3, 4])
+def test_splitk_model_double_rounding(S):
+    rng = np.random.default_rng(S)
+    M, N, K = 64, 3, 320  # 5 global-tile columns: uneven split
+    W = weights_bf16(rng, (M, K))
+    X = normal_bf16(rng, (N, K))
+    Y = zo.bf16_to_f32(zo.gemm_splitk_bf16(W, X, S)).astype(np.float64)
+    nk = K // 64
+    avg = (nk - 1) // S + 1
+    w = zo.bf16_to_f32(W).astype(np.float64)
+    x = zo.bf16_to_f32(X).astype(np.float64)
+    parts = []
+    for s in range(S):
+        k0, k1 = s * avg * 64, min((s + 1) * avg, nk) * 64
+        p = x[:, k0:k1] @ w[:, k0:k1].T if k1 > k0 else np.zeros((N, M))
+        parts.append(zo.bf16_to_f32(zo.f32_to_bf16(p.astype(np.float32))).astype(np.float64))
+    ref = sum(parts)
+    np.testing.assert_allclose(Y, ref, rtol=2 ** -7, atol=1e-6)
+
+
+def numpy_attention(q, k, v, seqlens, scale):
+    """Independent vectorised float64 decode attention."""
+    qf = zo.bf16_to_f32(q).astype(np.float64)
+    kf = zo.bf16_to_f32(k).astype(np.float64)
+    vf = zo.bf16_to_f32(v).astype(np.float64)
+    B, H, D = q.shape
+    Hkv = k.shape[2]
+    G = H // Hkv
+    out = np.zeros((B, H, D))
+    lse = np.zeros((B, H))
+    for b in range(B):
+        L = seqlens[b]
+        kk = np.repeat(kf[b, :L], G, axis=1)   # [L, H, D]
+        vv = np.repeat(vf[b, :L], G, axis=1)
+        s = np.einsum("hd,thd->ht", qf[b], kk) * scale
+        mx = s.max(axis=1, keepdims=True)
+        p = np.exp(s - mx)
+        out[b] = np.einsum("ht,thd->hd", p, vv) / p.sum(axis=1, keepdims=True)
+        lse[b] = (mx[:, 0] + np.log(p.sum(axis=1)))
+    return out, lse
+
+
+def test_attention_matches_numpy():
+    rng = np.random.default_rng(2)
+    B, H, Hkv, T, D = 2, 8, 2, 37, 64
+    q = normal_bf16(rng, (B, H, D))
+    k = normal_bf16(rng, (B, T, Hkv, D))
+    v = normal_bf16(rng, (B, T, Hkv, D))
+    sl = np.array([37, 20], np.int32)
+    out, lse = zo.decode_attention_f64(q, k, v, sl)
+    ref, rlse = numpy_attention(q, k, v, sl, 1 / np.sqrt(D))
+    np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(lse, rlse, rtol=1e-12, atol=1e-12)
+
+
+def test_attention_special_cases():
+    rng = np.random.default_rng(4)
+    B, H, Hkv, T, D = 1, 4, 1, 16, 32
+    q = normal_bf16(rng, (B, H, D))
+    v = normal_bf16(rng, (B, T, Hkv, D))
+    # T = 1: output is the single V row for every head, lse = the score
+    k = normal_bf16(rng, (B, T, Hkv, D))
+    out, lse = zo.decode_attention_f64(q, k, v, np.array([1], np.int32))
+    for h in range(H):
+        np.testing.assert_array_equal(out[0, h], zo.bf16_to_f32(v[0, 0, 0]).astype(np.float64))
+    # all-equal scores (K = 0): output is the mean of V, lse = log(T)
+    k0 = np.zeros_like(k)
+    out, lse = zo.decode_attention_f64(q, k0, v)
+    np.testing.assert_allclose(out[0, 0], zo.bf16_to_f32(v[0, :, 0]).astype(np.float64).mean(0), atol=1e-12)
+    np.testing.assert_allclose(lse, np.log(T), atol=1e-12)
+    # one-hot scores: a single key aligned with q dominates
+    qo = np.zeros((B, H, D), np.uint16)
+    qo[:, :, 0] = 0x4480  # 1024
+    ko = np.zeros_like(k)
+    ko[0, 5, 0, 0] = 0x3F80
+    out, _ = zo.decode_attention_f64(qo, ko, v)
+    np.testing.assert_allclose(out[0, 0], zo.bf16_to_f32(v[0, 5, 0]).astype(np.float64), atol=1e-12)

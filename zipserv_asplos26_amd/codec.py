@@ -1,0 +1,376 @@
+"""Host-side mirror of the reference's codec interfaces, over the C-ABI.
+
+* numpy (CPU) entry points mirror build/L_API.cuh's host encoders and
+  kernel_benchmark/utils.h's analyzeExponentDistribution_BF16;
+* torch (GPU) entry points mirror the PyTorch extension
+  kernel_benchmark/zipserv_decode_attention_ext.cpp:81-181
+  (compress_zipserv / decompress_zipserv / decompress_zipserv_into) and the
+  ZipservCompressed record of bench_zipserv_decode_attention.py:49-68, plus
+  zipgemm() over BF16TripleBitmap_MM_API.
+
+Every device call goes through libzipserv.so; nothing here computes on the
+CPU on behalf of a GPU call.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _lib
+from ._lib import check, lib
+
+TILE_ARGS = (8, 16, 64, 8, 64, 64)
+
+
+def _np_ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+# --------------------------------------------------------------------------
+# Host codec (numpy)
+# --------------------------------------------------------------------------
+@dataclass
+class HostCompressed:
+    """Canonical TCA-TBE streams held in numpy arrays (csrc/L_API.cu:314-557)."""
+    sign_mantissa: np.ndarray        # uint8  [total_high_freq]
+    compressed_full: np.ndarray      # uint16 [total_full]
+    bitmap1: np.ndarray              # uint64 [M*K/64]
+    bitmap2: np.ndarray
+    bitmap3: np.ndarray
+    tile_offsets: np.ndarray         # int32 [2*M*K/64]
+    tile_offsets_median: np.ndarray  # int32 [2*M*K/1024]
+    tile_offsets_global: np.ndarray  # int32 [2*(M*K/4096+1)]
+    rows: int
+    cols: int
+    max_high_freq_count: int
+    max_full_count: int
+    start_exp: int
+    top_exponents: list = field(default_factory=list)
+
+    @property
+    def total_high_freq(self) -> int:
+        return int(self.sign_mantissa.size)
+
+    @property
+    def total_full(self) -> int:
+        return int(self.compressed_full.size)
+
+    @property
+    def num_global_tiles(self) -> int:
+        return (self.rows // 64) * (self.cols // 64)
+
+    def compressed_bytes(self) -> int:
+        return int(lib().zs_compressed_bytes(self.rows, self.cols, self.total_high_freq,
+                                             self.total_full))
+
+    def ratio(self) -> float:
+        return 2.0 * self.rows * self.cols / self.compressed_bytes()
+
+
+def analyze_exponents(a: np.ndarray) -> list[int]:
+    """kernel_benchmark/utils.h:189-272 -> 7 contiguous exponents."""
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    top = np.zeros(7, np.int32)
+    check("zs_analyze_exponents_host", lib().zs_analyze_exponents_host(_np_ptr(a), a.size, _np_ptr(top)))
+    return top.tolist()
+
+
+def compress_host(a: np.ndarray, top=None, variant: str = "reuse_simd") -> HostCompressed:
+    """Encode a bf16 [M, K] bit-pattern matrix on the CPU.
+
+    variant: "alloc" (InitBF16MatrixTripleBitmap, L_API.cuh:53),
+             "reuse" (_Reuse, L_API.cuh:76), "reuse_simd" (_Reuse_SIMD, L_API.cuh:109).
+    """
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    if a.ndim != 2:
+        raise ValueError("compress_host expects a 2D bf16 matrix")
+    M, K = a.shape
+    if top is None:
+        top = analyze_exponents(a)
+    topa = np.ascontiguousarray(top, dtype=np.int32)
+    L = lib()
+    mk = M * K
+    ngt = mk // 4096
+    if variant == "alloc":
+        ptrs = [C.c_void_p() for _ in range(8)]
+        mh, mf = C.c_int32(), C.c_int32()
+        rc = L.zs_init_bf16_matrix_triple_bitmap(
+            _np_ptr(a), M, K, *TILE_ARGS, _np_ptr(topa), *[C.byref(p) for p in ptrs],
+            C.byref(mh), C.byref(mf))
+        if rc < 0:
+            check("zs_init_bf16_matrix_triple_bitmap", rc)
+        tog = np.ctypeslib.as_array(C.cast(ptrs[7], C.POINTER(C.c_int32)), (2 * (ngt + 1),)).copy()
+        th, tf = int(tog[-2]), int(tog[-1])
+
+        def grab(p, ctype, n, dt):
+            return np.ctypeslib.as_array(C.cast(p, C.POINTER(ctype)), (n,)).astype(dt, copy=True)
+        out = HostCompressed(
+            sign_mantissa=grab(ptrs[0], C.c_uint8, max(th, 1), np.uint8)[:th],
+            compressed_full=grab(ptrs[1], C.c_uint16, max(tf, 1), np.uint16)[:tf],
+            bitmap1=grab(ptrs[2], C.c_uint64, mk // 64, np.uint64),
+            bitmap2=grab(ptrs[3], C.c_uint64, mk // 64, np.uint64),
+            bitmap3=grab(ptrs[4], C.c_uint64, mk // 64, np.uint64),
+            tile_offsets=grab(ptrs[5], C.c_int32, 2 * (mk // 64), np.int32),
+            tile_offsets_median=grab(ptrs[6], C.c_int32, 2 * (mk // 1024), np.int32),
+            tile_offsets_global=tog, rows=M, cols=K, max_high_freq_count=mh.value,
+            max_full_count=mf.value, start_exp=(int(topa[0]) - 1) & 0xFF, top_exponents=topa.tolist())
+        for p in ptrs:
+            L.zs_host_free(p)
+        return out
+    fn = {"reuse": L.zs_init_bf16_matrix_triple_bitmap_reuse,
+          "reuse_simd": L.zs_init_bf16_matrix_triple_bitmap_reuse_simd}[variant]
+    sm = np.zeros(mk + 16 * ngt + 16, np.uint8)
+    fu = np.zeros(mk + 8 * ngt + 8, np.uint16)
+    b1, b2, b3 = (np.zeros(mk // 64, np.uint64) for _ in range(3))
+    tiles = np.zeros(2 * (mk // 64), np.int32)
+    med = np.zeros(2 * (mk // 1024), np.int32)
+    tog = np.zeros(2 * (ngt + 1), np.int32)
+    tsm = np.zeros(ngt * (4096 + 15) + 16, np.uint8)
+    tfu = np.zeros(ngt * (4096 + 7), np.uint16)
+    ghf, gfu = np.zeros(ngt, np.int32), np.zeros(ngt, np.int32)
+    hoff, foff = np.zeros(ngt + 1, np.int32), np.zeros(ngt + 1, np.int32)
+    mh, mf, th, tf = C.c_int32(), C.c_int32(), C.c_int32(), C.c_int32()
+    rc = fn(_np_ptr(a), M, K, *TILE_ARGS, _np_ptr(topa), _np_ptr(sm), _np_ptr(fu), _np_ptr(b1),
+            _np_ptr(b2), _np_ptr(b3), _np_ptr(tiles), _np_ptr(med), _np_ptr(tog), _np_ptr(tsm),
+            _np_ptr(tfu), _np_ptr(ghf), _np_ptr(gfu), _np_ptr(hoff), _np_ptr(foff),
+            C.byref(mh), C.byref(mf), C.byref(th), C.byref(tf))
+    if rc < 0:
+        check(variant, rc)
+    return HostCompressed(
+        sign_mantissa=sm[: th.value].copy(), compressed_full=fu[: tf.value].copy(),
+        bitmap1=b1, bitmap2=b2, bitmap3=b3, tile_offsets=tiles, tile_offsets_median=med,
+        tile_offsets_global=tog, rows=M, cols=K, max_high_freq_count=mh.value,
+        max_full_count=mf.value, start_exp=(int(topa[0]) - 1) & 0xFF, top_exponents=topa.tolist())
+
+
+# --------------------------------------------------------------------------
+# Device codec (torch tensors on the GPU)
+# --------------------------------------------------------------------------
+def _torch():
+    import torch
+    return torch
+
+
+def _dptr(t) -> int:
+    return 0 if t is None else int(t.data_ptr())
+
+
+def _stream() -> int:
+    torch = _torch()
+    return int(torch.cuda.current_stream().cuda_stream)
+
+
+@dataclass
+class ZipservCompressed:
+    """Device-resident compressed matrix (bench_zipserv_decode_attention.py:49-68).
+
+    sign_mantissa / compressed_full keep ZS_STREAM_SLACK_BYTES of readable slack
+    past total_high_freq / total_full.
+    """
+    sign_mantissa: object
+    compressed_full: object
+    bitmap1: object
+    bitmap2: object
+    bitmap3: object
+    tile_offsets_median: object
+    tile_offsets_global: object
+    rows: int
+    cols: int
+    logical_rows: int
+    logical_cols: int
+    max_high_freq_count: int
+    max_full_count: int
+    start_exp: int
+    total_high_freq: int
+    total_full: int
+    num_global_tiles: int
+    compressed_bytes: int
+    tile_offsets: object = None
+    layout: str = "by_kv_head"
+
+    def ratio(self) -> float:
+        return 2.0 * self.rows * self.cols / self.compressed_bytes
+
+    def streams(self):
+        """The 7 buffers in L_API argument order."""
+        return (self.sign_mantissa, self.compressed_full, self.bitmap1, self.bitmap2,
+                self.bitmap3, self.tile_offsets_median, self.tile_offsets_global)
+
+
+def to_device(h: HostCompressed, device="cuda", logical_rows=None, logical_cols=None) -> ZipservCompressed:
+    """Upload host-compressed streams (with stream slack) to the GPU."""
+    torch = _torch()
+    slack = _lib.ZS_STREAM_SLACK_BYTES
+    sm = np.zeros(h.total_high_freq + slack, np.uint8)
+    sm[: h.total_high_freq] = h.sign_mantissa
+    fu = np.zeros(h.total_full + slack // 2, np.uint16)
+    fu[: h.total_full] = h.compressed_full
+
+    def dev(x):
+        return torch.from_numpy(np.ascontiguousarray(x)).to(device)
+    return ZipservCompressed(
+        sign_mantissa=dev(sm), compressed_full=dev(fu.view(np.int16)).view(torch.bfloat16),
+        bitmap1=dev(h.bitmap1.view(np.int64)), bitmap2=dev(h.bitmap2.view(np.int64)),
+        bitmap3=dev(h.bitmap3.view(np.int64)), tile_offsets_median=dev(h.tile_offsets_median),
+        tile_offsets_global=dev(h.tile_offsets_global), rows=h.rows, cols=h.cols,
+        logical_rows=h.rows if logical_rows is None else logical_rows,
+        logical_cols=h.cols if logical_cols is None else logical_cols,
+        max_high_freq_count=h.max_high_freq_count, max_full_count=h.max_full_count,
+        start_exp=h.start_exp, total_high_freq=h.total_high_freq, total_full=h.total_full,
+        num_global_tiles=h.num_global_tiles, compressed_bytes=h.compressed_bytes(),
+        tile_offsets=dev(h.tile_offsets))
+
+
+def _check_cuda(t, name, dtype=None):
+    torch = _torch()
+    if not (isinstance(t, torch.Tensor) and t.is_cuda):
+        raise ValueError(f"{name} must be a CUDA tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}")
+
+
+def compress_zipserv(input, logical_rows: int | None = None, logical_cols: int | None = None):
+    """zipserv_decode_attention_ext.cpp:81-88 / .cu:157-265 on the GPU.
+
+    Returns [sign_mantissa, compressed_full, bitmap1, bitmap2, bitmap3,
+    tile_offsets_median, tile_offsets_global, meta] where meta is the int64
+    [rows, cols, logical_rows, logical_cols, max_hf, max_full, start_exp,
+    total_hf, total_full, num_global_tiles, comp_bytes] tensor of ext.cu:250-262
+    (comp_bytes uses the inclusive formula of ext.cu:23-33).
+    """
+    torch = _torch()
+    _check_cuda(input, "input", torch.bfloat16)
+    if input.dim() != 2:
+        raise ValueError("input must be 2D")
+    rows, cols = input.shape
+    if rows % 64 or cols % 64:
+        raise ValueError("rows and cols must be padded to multiples of 64")
+    L = lib()
+    dev = input.device
+    mk = rows * cols
+    ngt = mk // 4096
+    i32 = dict(dtype=torch.int32, device=dev)
+    sm = torch.empty(int(L.zs_sign_mantissa_capacity(rows, cols)), dtype=torch.uint8, device=dev)
+    fu = torch.empty(int(L.zs_full_capacity(rows, cols)), dtype=torch.bfloat16, device=dev)
+    b1, b2, b3 = (torch.empty(mk // 64, dtype=torch.int64, device=dev) for _ in range(3))
+    tiles = torch.empty(2 * (mk // 64), **i32)
+    med = torch.empty(2 * (mk // 1024), **i32)
+    tog = torch.empty(2 * (ngt + 1), **i32)
+    ghf, gfu = torch.empty(ngt, **i32), torch.empty(ngt, **i32)
+    hoff, foff = torch.empty(ngt + 1, **i32), torch.empty(ngt + 1, **i32)
+    top = torch.empty(7, **i32)
+    counts = torch.empty(256, **i32)
+    done = torch.empty(4, **i32)
+    scal = torch.empty(4, **i32)
+    st = _stream()
+    check("zs_analyze_top_exponents_gpu",
+          L.zs_analyze_top_exponents_gpu(st, _dptr(input), mk, _dptr(counts), _dptr(top), _dptr(done)))
+    check("zs_init_bf16_matrix_triple_bitmap_gpu",
+          L.zs_init_bf16_matrix_triple_bitmap_gpu(
+              st, _dptr(input), rows, cols, _dptr(top), _dptr(sm), _dptr(fu), _dptr(b1),
+              _dptr(b2), _dptr(b3), _dptr(tiles), _dptr(med), _dptr(tog), None, None,
+              _dptr(ghf), _dptr(gfu), _dptr(hoff), _dptr(foff), _dptr(scal[0:]),
+              _dptr(scal[1:]), _dptr(scal[2:]), _dptr(scal[3:])))
+    host = torch.cat([scal, top[:1]]).cpu().tolist()  # synchronises, as ext.cu:234-245
+    max_hf, max_full, total_hf, total_full, top0 = host
+    # The slack past the streams is zeroed so every byte a decoder may touch is defined.
+    sm[total_hf:].zero_()
+    fu[total_full:].zero_()
+    start_exp = top0 - 1
+    inclusive = (total_hf + 2 * total_full + (mk // 64) * 3 * 8 + (mk // 64) * 2 * 4
+                 + (mk // 1024) * 2 * 4 + (ngt + 1) * 2 * 4 + 7 * 4)
+    meta = torch.tensor([rows, cols, rows if logical_rows is None else logical_rows,
+                         cols if logical_cols is None else logical_cols, max_hf, max_full,
+                         start_exp, total_hf, total_full, ngt, inclusive], dtype=torch.int64)
+    return [sm, fu, b1, b2, b3, med, tog, meta]
+
+
+def make_zipserv_compressed(parts, layout: str = "by_kv_head") -> ZipservCompressed:
+    """bench_zipserv_decode_attention.py:375-405 make_zipserv_compressed_from_parts."""
+    sm, fu, b1, b2, b3, med, tog, meta = parts
+    m = meta.tolist()
+    rows, cols = int(m[0]), int(m[1])
+    return ZipservCompressed(
+        sign_mantissa=sm, compressed_full=fu, bitmap1=b1, bitmap2=b2, bitmap3=b3,
+        tile_offsets_median=med, tile_offsets_global=tog, rows=rows, cols=cols,
+        logical_rows=int(m[2]), logical_cols=int(m[3]), max_high_freq_count=int(m[4]),
+        max_full_count=int(m[5]), start_exp=int(m[6]), total_high_freq=int(m[7]),
+        total_full=int(m[8]), num_global_tiles=int(m[9]),
+        compressed_bytes=int(lib().zs_compressed_bytes(rows, cols, int(m[7]), int(m[8]))),
+        layout=layout)
+
+
+def compress(input, logical_rows=None, logical_cols=None, layout="by_kv_head") -> ZipservCompressed:
+    return make_zipserv_compressed(compress_zipserv(input, logical_rows, logical_cols), layout)
+
+
+def decompress_zipserv_into(output, sign_mantissa, compressed_full, bitmap1, bitmap2, bitmap3,
+                            tile_offsets_median, tile_offsets_global, rows, cols,
+                            max_high_freq_count, max_full_count, start_exp):
+    """zipserv_decode_attention_ext.cpp:144-175 -> BF16TripleBitmap_Decompress_API."""
+    torch = _torch()
+    _check_cuda(output, "output", torch.bfloat16)
+    if tuple(output.shape) != (rows, cols):
+        raise ValueError("output shape must be (rows, cols)")
+    for name, t in (("sign_mantissa", sign_mantissa), ("compressed_full", compressed_full),
+                    ("bitmap1", bitmap1), ("bitmap2", bitmap2), ("bitmap3", bitmap3),
+                    ("tile_offsets_median", tile_offsets_median),
+                    ("tile_offsets_global", tile_offsets_global)):
+        _check_cuda(t, name)
+    check("zs_bf16_triple_bitmap_decompress",
+          lib().zs_bf16_triple_bitmap_decompress(
+              _stream(), _dptr(sign_mantissa), _dptr(compressed_full), _dptr(bitmap1),
+              _dptr(bitmap2), _dptr(bitmap3), _dptr(tile_offsets_median),
+              _dptr(tile_offsets_global), int(max_high_freq_count), int(max_full_count),
+              int(start_exp) & 0xFF, _dptr(output), int(rows), int(cols)))
+    return output
+
+
+def decompress_zipserv(sign_mantissa, compressed_full, bitmap1, bitmap2, bitmap3,
+                       tile_offsets_median, tile_offsets_global, rows, cols,
+                       max_high_freq_count, max_full_count, start_exp):
+    """zipserv_decode_attention_ext.cpp:90-142."""
+    torch = _torch()
+    out = torch.empty((rows, cols), dtype=torch.bfloat16, device=sign_mantissa.device)
+    return decompress_zipserv_into(out, sign_mantissa, compressed_full, bitmap1, bitmap2, bitmap3,
+                                   tile_offsets_median, tile_offsets_global, rows, cols,
+                                   max_high_freq_count, max_full_count, start_exp)
+
+
+def decompress(c: ZipservCompressed, out=None):
+    torch = _torch()
+    if out is None:
+        out = torch.empty((c.rows, c.cols), dtype=torch.bfloat16, device=c.sign_mantissa.device)
+    return decompress_zipserv_into(out, *c.streams(), c.rows, c.cols, c.max_high_freq_count,
+                                   c.max_full_count, c.start_exp)
+
+
+def splitk_workspace(c: ZipservCompressed, n: int, split_k: int):
+    torch = _torch()
+    nbytes = int(lib().zs_splitk_workspace_bytes(c.rows, n, split_k))
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes // 2, dtype=torch.bfloat16, device=c.sign_mantissa.device)
+
+
+def zipgemm(c: ZipservCompressed, x, split_k: int = 1, out=None, workspace=None):
+    """Y[N, M] = X[N, K] . W[M, K]^T (build/L_API.cuh:19-37 BF16TripleBitmap_MM_API)."""
+    torch = _torch()
+    _check_cuda(x, "x", torch.bfloat16)
+    if x.dim() != 2 or x.shape[1] != c.cols:
+        raise ValueError(f"x must be [N, {c.cols}]")
+    n = x.shape[0]
+    if out is None:
+        out = torch.empty((n, c.rows), dtype=torch.bfloat16, device=x.device)
+    if split_k > 1 and workspace is None:
+        workspace = splitk_workspace(c, n, split_k)
+    check("zs_bf16_triple_bitmap_mm",
+          lib().zs_bf16_triple_bitmap_mm(
+              _stream(), *[_dptr(t) for t in c.streams()], c.max_high_freq_count,
+              c.max_full_count, c.start_exp & 0xFF, _dptr(x), _dptr(out), c.rows, n, c.cols,
+              _dptr(workspace), split_k))
+    return out
