@@ -114,10 +114,11 @@ def test_zipgemm_matches_oracle(torch_cuda, M, K, N):
     np.testing.assert_allclose(y, ref, rtol=1e-2, atol=1e-2 * np.abs(ref).max())
 
 
-@pytest.mark.parametrize("split_k", [2, 3, 4])
-def test_zipgemm_splitk(torch_cuda, split_k):
-    rng = np.random.default_rng(split_k)
-    M, K, N = 128, 320, 24
+@pytest.mark.parametrize("split_k,N", [(2, 24), (3, 24), (4, 24), (2, 1), (4, 16), (2, 64),
+                                       (3, 100), (5, 128)])
+def test_zipgemm_splitk(torch_cuda, split_k, N):
+    rng = np.random.default_rng(split_k * 1000 + N)
+    M, K = 128, 320
     W = weights_bf16(rng, (M, K), outlier_frac=0.01)
     X = normal_bf16(rng, (N, K))
     c = upload(zo.compress(W))
@@ -127,6 +128,20 @@ def test_zipgemm_splitk(torch_cuda, split_k):
     assert rel_err(y, zo.gemm_f32(W, X)) <= 1e-2
     model = zo.bf16_to_f32(zo.gemm_splitk_bf16(W, X, split_k))
     assert rel_err(y, model) <= 1e-2
+
+
+@pytest.mark.parametrize("M,K,N,split_k", [(256, 2048, 16, 4), (192, 4096, 8, 8), (512, 1024, 32, 2),
+                                           (128, 64 * 70, 1, 3)])
+def test_zipgemm_splitk_long_slices(torch_cuda, M, K, N, split_k):
+    """Slices longer than the 64-tile offset chunk and heavy outliers."""
+    rng = np.random.default_rng(M + K + N + split_k)
+    W = weights_bf16(rng, (M, K), outlier_frac=0.05)
+    X = normal_bf16(rng, (N, K))
+    c = upload(zo.compress(W))
+    Y = zs.zipgemm(c, to_torch_bf16(X), split_k=split_k)
+    y = zo.bf16_to_f32(from_torch_bf16(Y))
+    assert rel_err(y, zo.gemm_f32(W, X)) <= 1e-2
+    assert rel_err(y, zo.bf16_to_f32(zo.gemm_splitk_bf16(W, X, split_k))) <= 1e-2
 
 
 def test_zipgemm_unit_vectors_exact(torch_cuda):

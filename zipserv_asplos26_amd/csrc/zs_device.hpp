@@ -31,24 +31,31 @@ constexpr int kWave = 64;
 //   e2[v] lane j = bit_j(v) << 8
 //   e3[v] lane j = bit_j(v) << 9
 // so e1[b1] + e2[b2] + e3[b3] = (start_exp + code_j) << 7 = the exponent field.
-//   sel[v] dword d = v_perm selector bytes [r_2d, r_2d, r_2d+1, r_2d+1], r_j =
-//   number of set bits of v below j (rank of position j in the SM window).
+// Indexed by the in-window mask v = b1|b2|b3:
+//   sel[v]  dword d = v_perm selector bytes [r_2d, r_2d, r_2d+1, r_2d+1],
+//           r_j = set bits of v below j (rank of position j in the SM window);
+//   osel[v] dword d = v_perm selector bytes picking outlier k_j = j - r_j from
+//           a 4-value FULL window (bytes 2k, 2k+1), for the outlier lanes;
+//   omsk[v] dword d = 0xFFFF in the 16-bit lanes that are outliers.
 struct DecodeTables {
   uint4 e1[256];
   uint4 e2[256];
   uint4 e3[256];
   uint4 sel[256];
+  uint4 osel[256];
+  uint4 omsk[256];
 };
 
 __device__ __forceinline__ void build_decode_tables(DecodeTables& T, int start_exp, int tid,
                                                     int nthreads) {
   for (int v = tid; v < 256; v += nthreads) {
-    uint32_t e1[4], e2[4], e3[4], s[4];
-    uint32_t r[8];
+    uint32_t e1[4], e2[4], e3[4], s[4], os[4], om[4];
+    uint32_t r[8], k[8];
     uint32_t rank = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       r[j] = rank;
+      k[j] = j - rank;
       rank += (v >> j) & 1;
     }
 #pragma unroll
@@ -58,29 +65,32 @@ __device__ __forceinline__ void build_decode_tables(DecodeTables& T, int start_e
       e2[d] = (lo << 8) | (hi << 24);
       e3[d] = (lo << 9) | (hi << 25);
       s[d] = r[2 * d] | (r[2 * d] << 8) | (r[2 * d + 1] << 16) | (r[2 * d + 1] << 24);
+      const uint32_t klo = k[2 * d] & 3, khi = k[2 * d + 1] & 3;
+      os[d] = (2 * klo) | ((2 * klo + 1) << 8) | ((2 * khi) << 16) | ((2 * khi + 1) << 24);
+      om[d] = (lo ? 0u : 0xFFFFu) | (hi ? 0u : 0xFFFF0000u);
     }
     T.e1[v] = make_uint4(e1[0], e1[1], e1[2], e1[3]);
     T.e2[v] = make_uint4(e2[0], e2[1], e2[2], e2[3]);
     T.e3[v] = make_uint4(e3[0], e3[1], e3[2], e3[3]);
     T.sel[v] = make_uint4(s[0], s[1], s[2], s[3]);
+    T.osel[v] = make_uint4(os[0], os[1], os[2], os[3]);
+    T.omsk[v] = make_uint4(om[0], om[1], om[2], om[3]);
   }
 }
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
 // Inclusive prefix sum over the 64 lanes of a wave: Hillis-Steele inside
-// each 16-lane DPP row (row_shr 1,2,4,8), then the three row totals are
-// folded in with readlane.
+// each 16-lane DPP row (row_shr 1,2,4,8), then row_bcast:15 adds row 0's
+// total into row 1 and row 2's into row 3, and row_bcast:31 adds the total of
+// rows 0-1 into rows 2-3.
 __device__ __forceinline__ int wave_inclusive_scan(int x) {
   x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
   x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
   x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
   x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
-  const int t0 = __builtin_amdgcn_readlane(x, 15);
-  const int t1 = __builtin_amdgcn_readlane(x, 31);
-  const int t2 = __builtin_amdgcn_readlane(x, 47);
-  const int row = lane_id() >> 4;
-  x += (row > 0 ? t0 : 0) + (row > 1 ? t1 : 0) + (row > 2 ? t2 : 0);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
   return x;
 }
 
@@ -135,52 +145,176 @@ __device__ __forceinline__ RowRef load_half_median(const Streams& s, int64_t bm_
   return r;
 }
 
-// Decodes the lane's 8 elements into 4 dwords (element 2d in the low half of
-// dword d).  In-window elements: v_perm gathers sign|mantissa bytes from an
-// aligned 12-byte SM window, v_bfi merges the exponent field from the LDS
-// tables.  Outliers are patched from the FULL stream in position order.
-__device__ __forceinline__ u32x4 decode_row(const Streams& s, const DecodeTables& T,
-                                            const RowRef& r) {
-  const uint4 x1 = T.e1[r.b1];
-  const uint4 x2 = T.e2[r.b2];
-  const uint4 x3 = T.e3[r.b3];
-  const uint4 sel = T.sel[r.ind];
-  const int64_t a = r.sm_off & ~(int64_t)3;
-  const uint32_t sh = (uint32_t)(r.sm_off & 3);
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(s.sm + a);
-  const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
+// In-window part of a row decode: gathers the lane's sign|mantissa bytes from
+// a 12-byte SM window (w0..w2, starting `sh` bytes before the row's first
+// byte) with v_perm and merges the exponent field from the LDS tables with
+// v_bfi.  Outlier positions hold garbage until patched.
+__device__ __forceinline__ u32x4 decode_inwindow(const DecodeTables& T, uint32_t b1, uint32_t b2,
+                                                 uint32_t b3, uint32_t ind, uint32_t w0,
+                                                 uint32_t w1, uint32_t w2, uint32_t sh) {
+  const uint4 x1 = T.e1[b1];
+  const uint4 x2 = T.e2[b2];
+  const uint4 x3 = T.e3[b3];
+  const uint4 sel = T.sel[ind];
   const uint32_t s0 = __builtin_amdgcn_alignbyte(w1, w0, sh);
   const uint32_t s1 = __builtin_amdgcn_alignbyte(w2, w1, sh);
-  u32x4 o;
-  o[0] = __builtin_amdgcn_perm(s1, s0, sel.x);
-  o[1] = __builtin_amdgcn_perm(s1, s0, sel.y);
-  o[2] = __builtin_amdgcn_perm(s1, s0, sel.z);
-  o[3] = __builtin_amdgcn_perm(s1, s0, sel.w);
   const uint32_t msk = 0x807F807Fu;
-  o[0] = (o[0] & msk) | ((x1.x + x2.x + x3.x) & ~msk);
-  o[1] = (o[1] & msk) | ((x1.y + x2.y + x3.y) & ~msk);
-  o[2] = (o[2] & msk) | ((x1.z + x2.z + x3.z) & ~msk);
-  o[3] = (o[3] & msk) | ((x1.w + x2.w + x3.w) & ~msk);
+  u32x4 o;
+  o[0] = (__builtin_amdgcn_perm(s1, s0, sel.x) & msk) | ((x1.x + x2.x + x3.x) & ~msk);
+  o[1] = (__builtin_amdgcn_perm(s1, s0, sel.y) & msk) | ((x1.y + x2.y + x3.y) & ~msk);
+  o[2] = (__builtin_amdgcn_perm(s1, s0, sel.z) & msk) | ((x1.z + x2.z + x3.z) & ~msk);
+  o[3] = (__builtin_amdgcn_perm(s1, s0, sel.w) & msk) | ((x1.w + x2.w + x3.w) & ~msk);
+  return o;
+}
+
+// Merges the first four outliers of a row into `o` branch-free: g0/g1 hold
+// FULL values k = 0,1 / 2,3 of the row; v_perm places value k_j under each
+// outlier lane and v_bfi keeps it only there.
+__device__ __forceinline__ void merge_outliers4(const DecodeTables& T, uint32_t ind, uint32_t g0,
+                                                uint32_t g1, u32x4& o) {
+  const uint4 os = T.osel[ind];
+  const uint4 om = T.omsk[ind];
+  o[0] = (__builtin_amdgcn_perm(g1, g0, os.x) & om.x) | (o[0] & ~om.x);
+  o[1] = (__builtin_amdgcn_perm(g1, g0, os.y) & om.y) | (o[1] & ~om.y);
+  o[2] = (__builtin_amdgcn_perm(g1, g0, os.z) & om.z) | (o[2] & ~om.z);
+  o[3] = (__builtin_amdgcn_perm(g1, g0, os.w) & om.w) | (o[3] & ~om.w);
+}
+
+// Writes the k-th outlier value v of the row into position j (0..7).
+__device__ __forceinline__ void patch_outlier(u32x4& o, int j, uint32_t v) {
+  const uint32_t shj = (j & 1) * 16;
+  const uint32_t keep = ~(0xFFFFu << shj);
+  const uint32_t ins = v << shj;
+  const int d = j >> 1;
+  o[0] = d == 0 ? ((o[0] & keep) | ins) : o[0];
+  o[1] = d == 1 ? ((o[1] & keep) | ins) : o[1];
+  o[2] = d == 2 ? ((o[2] & keep) | ins) : o[2];
+  o[3] = d == 3 ? ((o[3] & keep) | ins) : o[3];
+}
+
+// Patches the row's outliers (positions = set bits of fm, in order) from a
+// FULL window held in registers: q0..q2 are the 3 dwords starting at the
+// 4-byte-aligned address at or below the row's first outlier, `odd` says
+// whether that outlier is the high half of q0.  Covers up to 5 outliers
+// (6 - odd halfwords); returns the bits of fm still unpatched.
+__device__ __forceinline__ uint32_t patch_outliers_window(u32x4& o, uint32_t fm, uint32_t q0,
+                                                          uint32_t q1, uint32_t q2, int odd) {
+  int hw = odd;
+  while (fm && hw < 6) {
+    const uint32_t d = hw < 2 ? q0 : (hw < 4 ? q1 : q2);
+    patch_outlier(o, __builtin_ctz(fm), (d >> ((hw & 1) * 16)) & 0xFFFFu);
+    fm &= fm - 1;
+    ++hw;
+  }
+  return fm;
+}
+
+// Decodes the lane's 8 elements into 4 dwords (element 2d in the low half of
+// dword d) straight from the global streams.  Outliers are patched from the
+// FULL stream in position order.
+__device__ __forceinline__ u32x4 decode_row(const Streams& s, const DecodeTables& T,
+                                            const RowRef& r) {
+  const int64_t a = r.sm_off & ~(int64_t)3;
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(s.sm + a);
+  u32x4 o = decode_inwindow(T, r.b1, r.b2, r.b3, r.ind, w[0], w[1], w[2],
+                            (uint32_t)(r.sm_off & 3));
   uint32_t fm = (~r.ind) & 0xFFu;
   if (fm) {
     const uint16_t* f = s.full + r.full_off;
     int k = 0;
     while (fm) {
-      const int j = __builtin_ctz(fm);
-      const uint32_t v = f[k];
-      const uint32_t shj = (j & 1) * 16;
-      const uint32_t keep = ~(0xFFFFu << shj);
-      const uint32_t ins = v << shj;
-      const int d = j >> 1;
-      o[0] = d == 0 ? ((o[0] & keep) | ins) : o[0];
-      o[1] = d == 1 ? ((o[1] & keep) | ins) : o[1];
-      o[2] = d == 2 ? ((o[2] & keep) | ins) : o[2];
-      o[3] = d == 3 ? ((o[3] & keep) | ins) : o[3];
+      patch_outlier(o, __builtin_ctz(fm), f[k]);
       fm &= fm - 1;
       ++k;
     }
   }
   return o;
+}
+
+// Decodes both half median tiles (16 rows x 32 columns each) of one staged
+// median tile with their dependency chains interleaved.
+//   bm     : 3 bitmap planes, plane p at bm + p * plane_stride, rows of half h
+//            at byte 64 * h (+ lane)
+//   smb    : SM bytes, the median tile's first one at offset `msm`
+//   fub    : FULL elements, the median tile's first one at element `mf`
+//   gfull  : the same FULL stream in global memory, used when `direct`
+// Returns the two MFMA A operands.
+struct HalfDec {
+  uint32_t b1, b2, b3, ind;
+  int excl, incl;
+};
+
+__device__ __forceinline__ void decode_median_pair(const DecodeTables& T, const uint8_t* bm,
+                                                   int plane_stride, const uint8_t* smb, int msm,
+                                                   const uint16_t* fub, int mf, bool direct,
+                                                   const uint16_t* gfull, u32x4& o0, u32x4& o1) {
+  const int l = lane_id();
+  HalfDec d[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    d[h].b1 = bm[64 * h + l];
+    d[h].b2 = bm[plane_stride + 64 * h + l];
+    d[h].b3 = bm[2 * plane_stride + 64 * h + l];
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    d[h].ind = d[h].b1 | d[h].b2 | d[h].b3;
+    const int n = __builtin_popcount(d[h].ind);
+    d[h].incl = wave_inclusive_scan(n);
+    d[h].excl = d[h].incl - n;
+  }
+  const int tot0 = __builtin_amdgcn_readlane(d[0].incl, 63);
+  u32x4 o[2];
+  int fo[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int smo = msm + (h ? tot0 : 0) + d[h].excl;
+    fo[h] = mf + (h ? 512 - tot0 : 0) + 8 * l - d[h].excl;
+    const uint32_t* wp = reinterpret_cast<const uint32_t*>(smb + (smo & ~3));
+    o[h] = decode_inwindow(T, d[h].b1, d[h].b2, d[h].b3, d[h].ind, wp[0], wp[1], wp[2],
+                           (uint32_t)(smo & 3));
+  }
+  if (!direct) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t* fw = reinterpret_cast<const uint32_t*>(
+          reinterpret_cast<const uint8_t*>(fub) + ((2 * fo[h]) & ~3));
+      const uint32_t fsh = (uint32_t)((2 * fo[h]) & 3);
+      const uint32_t q0 = fw[0], q1 = fw[1], q2 = fw[2];
+      merge_outliers4(T, d[h].ind, __builtin_amdgcn_alignbyte(q1, q0, fsh),
+                      __builtin_amdgcn_alignbyte(q2, q1, fsh), o[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      // Rows with more than four outliers (rare) patch the rest one by one.
+      uint32_t rest = (~d[h].ind) & 0xFFu;
+      rest &= rest - 1;
+      rest &= rest - 1;
+      rest &= rest - 1;
+      rest &= rest - 1;
+      if (rest) {
+        int k = 4;
+        while (rest) {
+          patch_outlier(o[h], __builtin_ctz(rest), fub[fo[h] + k]);
+          rest &= rest - 1;
+          ++k;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t fm = (~d[h].ind) & 0xFFu;
+      int k = 0;
+      while (fm) {
+        patch_outlier(o[h], __builtin_ctz(fm), gfull[fo[h] + k]);
+        fm &= fm - 1;
+        ++k;
+      }
+    }
+  }
+  o0 = o[0];
+  o1 = o[1];
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {

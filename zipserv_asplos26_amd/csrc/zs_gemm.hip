@@ -5,10 +5,11 @@
 //   * decompress: one workgroup (4 waves) per 64x64 global tile (grid-stride),
 //     wave w = median tile w; each lane stores its 8 decoded bf16 as 16 bytes.
 //   * ZipGEMM: one workgroup per 16-row band x split-K slice x 16*NB output
-//     columns; its 4 waves take interleaved global-tile columns of the slice
-//     and the decoded A fragment feeds v_mfma_f32_16x16x32_bf16 against
-//     16-byte X loads (B operand lane l: column l%16, the same 8 k as A).
-//     The 4 partial accumulators are summed through LDS.
+//     columns; its waves take interleaved global-tile columns of the slice,
+//     stage each median tile through a wave-private LDS double buffer, and
+//     feed the decoded A fragment to v_mfma_f32_16x16x32_bf16 against 16-byte
+//     X loads (B operand lane l: column l%16, the same 8 k as A).  The
+//     per-wave partial accumulators are tree-summed through LDS.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -45,17 +46,131 @@ __global__ __launch_bounds__(256) void decompress_kernel(Streams s, int start_ex
   }
 }
 
-template <int NB>
-__global__ __launch_bounds__(256) void gemm_kernel(Streams s, int start_exp, const uint16_t* X,
-                                                   uint16_t* Y, int M, int N, int K,
-                                                   int kb_per_split) {
-  __shared__ DecodeTables T;
-  __shared__ f32x4 red[3][NB][64];
+// ---------------------------------------------------------------------------
+// ZipGEMM.  A workgroup of WAVES waves owns one 16-row band (one median tile
+// row of the global-tile grid) x one split-K slice x 16*NB output columns.
+// Wave w streams global-tile columns kb0+w, kb0+w+WAVES, ... of the slice.
+// For each one it copies the median tile's bitmap planes (3 x 128 B), its SM
+// bytes and its FULL elements with 16-byte loads into a wave-private,
+// double-buffered LDS stage -- the load addresses depend only on the tile
+// offsets, so the copy of tile j+2 is in flight while tile j is decoded --
+// and decodes each half median tile from LDS into one MFMA A operand.
+// ---------------------------------------------------------------------------
+constexpr int kStBm = 0;                     // 3 x 128 B bitmap planes
+constexpr int kStSm = 384;                   // SM bytes from the 16-aligned start
+constexpr int kStSmBytes = 1056;             // 65 chunks used + read-window slack
+constexpr int kStFull = kStSm + kStSmBytes;  // FULL elements from the 8-aligned start
+constexpr int kFullChunks = 33;              // staged outliers: up to 264 per median tile
+constexpr int kStBytes = kStFull + kFullChunks * 16 + 16;  // + window-read slack
+
+struct StageRegs {
+  u32x4 sm;    // SM chunk l (16 bytes) of the median tile
+  u32x4 misc;  // lanes 0..23 bitmap chunks, 24..56 FULL chunks, 57 SM chunk 64
+};
+struct StageMeta {
+  int sm_rel;    // first SM byte of the median tile relative to the stage copy
+  int full_rel;  // first FULL element relative to the stage copy
+  int fa0;       // stream offset of the stage copy's first FULL element
+  int full_direct;  // outliers did not fit the stage: read them from global
+};
+
+// Stream offsets of one median tile: first SM byte, first FULL element, and
+// the first ones after it (the next median tile's start, or the next global
+// tile's padded start for the last median tile).
+struct TileOff {
+  int hf0, f0, hf1, f1;
+};
+
+// Vector-loads the offsets of up to 64 median tiles (lane i -> tile i) so the
+// pipeline reads them with readlane instead of waiting on scalar loads.
+__device__ __forceinline__ TileOff load_tile_offsets(const Streams& s, int g, int m, bool valid) {
+  TileOff t{0, 0, 0, 0};
+  if (valid) {
+    const int t0 = s.tog[2 * g], tf0 = s.tog[2 * g + 1];
+    const int mb = 2 * (4 * g + m);
+    t.hf0 = t0 + s.tom[mb];
+    t.f0 = tf0 + s.tom[mb + 1];
+    if (m < 3) {
+      t.hf1 = t0 + s.tom[mb + 2];
+      t.f1 = tf0 + s.tom[mb + 3];
+    } else {
+      t.hf1 = s.tog[2 * g + 2];
+      t.f1 = s.tog[2 * g + 3];
+    }
+  }
+  return t;
+}
+
+__device__ __forceinline__ TileOff tile_off_at(const TileOff& v, int i) {
+  TileOff t;
+  t.hf0 = __builtin_amdgcn_readlane(v.hf0, i);
+  t.f0 = __builtin_amdgcn_readlane(v.f0, i);
+  t.hf1 = __builtin_amdgcn_readlane(v.hf1, i);
+  t.f1 = __builtin_amdgcn_readlane(v.f1, i);
+  return t;
+}
+
+// `bm_lane` is this lane's bitmap plane (lanes 0-7: plane 1, 8-15: plane 2,
+// 16-23: plane 3), chosen once per kernel.
+__device__ __forceinline__ void stage_issue(const Streams& s, const uint8_t* bm_lane, int g, int m,
+                                            const TileOff& o, StageRegs& r, StageMeta& mt) {
+  const int l = lane_id();
+  const int a0 = o.hf0 & ~15;
+  const int nch = min((o.hf1 - a0 + 15) >> 4, 65);
+  const int fa0 = o.f0 & ~7;
+  const int nfc = (o.f1 - fa0 + 7) >> 3;
+  mt.sm_rel = o.hf0 - a0;
+  mt.full_rel = o.f0 - fa0;
+  mt.fa0 = fa0;
+  mt.full_direct = nfc > kFullChunks;
+  // Every lane issues exactly two 16-byte loads (addresses clamped to valid
+  // data when the lane has nothing to fetch) so the number of loads in flight
+  // is the same on every path and the waits stay precise.
+  r.sm = *reinterpret_cast<const u32x4*>(s.sm + a0 + (l < nch ? 16 * l : 0));
+  const uint8_t* mp = bm_lane + 512 * g + 128 * m + 16 * (l & 7);
+  if (l >= 24) {
+    if (l < 24 + kFullChunks) {
+      if (l - 24 < nfc && nfc <= kFullChunks)
+        mp = reinterpret_cast<const uint8_t*>(s.full + fa0 + 8 * (l - 24));
+    } else if (l == 24 + kFullChunks && nch > 64) {
+      mp = s.sm + a0 + 1024;
+    }
+  }
+  r.misc = *reinterpret_cast<const u32x4*>(mp);
+}
+
+__device__ __forceinline__ void stage_write(uint8_t* st, const StageRegs& r) {
+  const int l = lane_id();
+  *reinterpret_cast<u32x4*>(st + kStSm + 16 * l) = r.sm;
+  if (l < 24)
+    *reinterpret_cast<u32x4*>(st + kStBm + 16 * l) = r.misc;
+  else if (l < 24 + kFullChunks)
+    *reinterpret_cast<u32x4*>(st + kStFull + 16 * (l - 24)) = r.misc;
+  else if (l == 24 + kFullChunks)
+    *reinterpret_cast<u32x4*>(st + kStSm + 1024) = r.misc;
+}
+
+template <int NB, int WAVES>
+struct GemmSmem {
+  static constexpr int kMain = (int)sizeof(DecodeTables) + WAVES * 3 * kStBytes;
+  static constexpr int kRed = (WAVES / 2) * NB * 64 * 16;
+  static constexpr int kBytes = kMain > kRed ? kMain : kRed;
+};
+
+template <int NB, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void gemm_kernel(Streams s, int start_exp,
+                                                          const uint16_t* X, uint16_t* Y, int M,
+                                                          int N, int K, int kb_per_split) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[GemmSmem<NB, WAVES>::kBytes];
+  DecodeTables& T = *reinterpret_cast<DecodeTables*>(smem);
   build_decode_tables(T, start_exp, threadIdx.x, blockDim.x);
   __syncthreads();
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
+  uint8_t* stage0 = smem + sizeof(DecodeTables) + w * 3 * kStBytes;
+  uint8_t* stage1 = stage0 + kStBytes;
+  uint8_t* stage2 = stage1 + kStBytes;
   const int band = blockIdx.x;  // 16-row band
   const int gm = band >> 2, m = band & 3;
   const int split = blockIdx.y;
@@ -63,6 +178,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(Streams s, int start_exp, con
   const int KT = K >> 6;
   const int kb0 = split * kb_per_split;
   const int kb1 = min(kb0 + kb_per_split, KT);
+  const int cnt = kb1 - kb0 > w ? (kb1 - kb0 - w + WAVES - 1) / WAVES : 0;
 
   const uint16_t* xrow[NB];
 #pragma unroll
@@ -74,43 +190,295 @@ __global__ __launch_bounds__(256) void gemm_kernel(Streams s, int start_exp, con
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int gk = kb0 + w; gk < kb1; gk += 4) {
-    const int64_t g = (int64_t)gm * KT + gk;
-    int64_t smb = (int64_t)s.tog[2 * g] + s.tom[2 * (4 * g + m)];
-    int64_t fb = (int64_t)s.tog[2 * g + 1] + s.tom[2 * (4 * g + m) + 1];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      int tot;
-      const RowRef r = load_half_median(s, 512 * g + 128 * m + 64 * h, smb, fb, tot);
-      const bf16x8 a = as_bf16x8(decode_row(s, T, r));
-      smb += tot;
-      fb += 512 - tot;
-      const int kk = gk * 64 + h * 32;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(xrow[nb] + kk);
-        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[nb], 0, 0, 0);
-      }
+  // Software pipeline over this wave's tiles, in chunks of 64 (one tile's
+  // offsets per lane, read back with readlane).  Register sets rotate by
+  // unrolling, so every register name is static; every step issues the same
+  // loads, and tile indices past the chunk end are clamped to its last tile
+  // (a discarded re-read).
+  // Lanes 24..63 use plane 3 as their in-bounds default bitmap address.
+  const uint8_t* bm_lane = l < 8 ? s.bm1 : (l < 16 ? s.bm2 : s.bm3);
+  for (int c0 = 0; c0 < cnt; c0 += 64) {
+    const int n = min(cnt - c0, 64);
+    const int last = n - 1;
+    const TileOff offs = load_tile_offsets(s, gm * KT + kb0 + w + (c0 + l) * WAVES, m, l < n);
+    // A tile's compressed data is fetched three tiles ahead (register sets
+    // R0..R2); tile j+1 is written to the next LDS stage while tile j is
+    // decoded.  X fragments ride in the same ring for narrow batches
+    // (kXRing); wider ones fetch X one tile ahead to stay within 256 VGPRs.
+    constexpr bool kXRing = NB <= 2;
+    StageRegs R0, R1, R2;
+    StageMeta M0, M1, M2;
+    bf16x8 X0[2][NB], X1[2][NB], X2[2][NB], xc[2][NB], xn[2][NB];
+#define ZS_TILE(J) (gm * KT + kb0 + w + (c0 + (J)) * WAVES)
+#define ZS_LOADX(J, DST)                                                            \
+  {                                                                                 \
+    const int kk_ = (kb0 + w + (c0 + (J)) * WAVES) * 64;                            \
+    _Pragma("unroll") for (int h_ = 0; h_ < 2; ++h_)                                \
+      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_)                          \
+        DST[h_][nb_] = *reinterpret_cast<const bf16x8*>(xrow[nb_] + kk_ + 32 * h_); \
+  }
+#define ZS_ISSUE(J, R, MT, XD)                                                      \
+  {                                                                                 \
+    stage_issue(s, bm_lane, ZS_TILE(J), m, tile_off_at(offs, (J)), R, MT);          \
+    if constexpr (kXRing) ZS_LOADX(J, XD);                                          \
+  }
+#define ZS_STEP(J, CUR, NXT, RC, MC, XC, RN)                                             \
+  {                                                                                      \
+    const StageMeta cm_ = MC;                                                            \
+    _Pragma("unroll") for (int h_ = 0; h_ < 2; ++h_)                                     \
+      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_)                               \
+        xc[h_][nb_] = kXRing ? XC[h_][nb_] : xn[h_][nb_];                                \
+    stage_write(NXT, RN);                                                                \
+    ZS_ISSUE(min((J) + 3, last), RC, MC, XC);                                            \
+    if constexpr (!kXRing) ZS_LOADX(min((J) + 1, last), xn);                             \
+    if ((J) < n) {                                                                       \
+      u32x4 a0_, a1_;                                                                    \
+      decode_median_pair(T, CUR + kStBm, 128, CUR + kStSm, cm_.sm_rel,                   \
+                         reinterpret_cast<const uint16_t*>(CUR + kStFull), cm_.full_rel, \
+                         cm_.full_direct, s.full + cm_.fa0, a0_, a1_);                   \
+      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                             \
+        acc[nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0_), xc[0][nb_],   \
+                                                           acc[nb_], 0, 0, 0);           \
+        acc[nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1_), xc[1][nb_],   \
+                                                           acc[nb_], 0, 0, 0);           \
+      }                                                                                  \
+    }                                                                                    \
+  }
+    ZS_ISSUE(0, R0, M0, X0);
+    ZS_ISSUE(min(1, last), R1, M1, X1);
+    ZS_ISSUE(min(2, last), R2, M2, X2);
+    if constexpr (!kXRing) ZS_LOADX(0, xn);
+    stage_write(stage0, R0);
+    // Period-3 body (3 register sets x 3 LDS stages) without early exits:
+    // steps past the end only repeat the clamped loads and skip the decode.
+    for (int j = 0; j < n; j += 3) {
+      ZS_STEP(j, stage0, stage1, R0, M0, X0, R1);
+      ZS_STEP(j + 1, stage1, stage2, R1, M1, X1, R2);
+      ZS_STEP(j + 2, stage2, stage0, R2, M2, X2, R0);
     }
+#undef ZS_STEP
+#undef ZS_LOADX
+#undef ZS_ISSUE
+#undef ZS_TILE
   }
 
-  if (w > 0) {
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) red[w - 1][nb][l] = acc[nb];
-  }
+  // Deterministic tree reduction of the WAVES partial accumulators in LDS.
   __syncthreads();
+  f32x4* red = reinterpret_cast<f32x4*>(smem);
+#pragma unroll
+  for (int half = WAVES / 2; half >= 1; half /= 2) {
+    if (w >= half && w < 2 * half) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) red[((w - half) * NB + nb) * 64 + l] = acc[nb];
+    }
+    __syncthreads();
+    if (w < half) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[nb] += red[(w * NB + nb) * 64 + l];
+    }
+    __syncthreads();
+  }
   if (w == 0) {
     uint16_t* out = Y + (int64_t)split * M * N;
     const int mrow = band * 16 + 4 * (l >> 4);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      f32x4 v = acc[nb] + red[0][nb][l] + red[1][nb][l] + red[2][nb][l];
+      const f32x4 v = acc[nb];
       const int n = n0 + nb * 16 + (l & 15);
       if (n < N) {
         const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
         const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
         *reinterpret_cast<uint2*>(out + (int64_t)n * M + mrow) = make_uint2(lo, hi);
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// ZipGEMM, 64-row variant.  A workgroup of 4 waves owns one 64-row band (a
+// row of global tiles) x one K slice x 16*NB output columns; wave w owns
+// median tile w of every global tile.  The 256 threads copy each global tile
+// (bitmap planes 3 x 512 B, its SM bytes from the 16-aligned tile start, its
+// FULL elements) into a 3-deep LDS ring with two unconditional 16-byte loads
+// per thread, three tiles ahead; one barrier per tile publishes a stage.  The
+// tile's streams are contiguous in HBM and every wave reuses the same X
+// columns, so this variant reads long runs and a quarter of the X traffic.
+// ---------------------------------------------------------------------------
+constexpr int kGtBm = 0;                    // 3 planes x 512 B
+constexpr int kGtSm = 1536;                 // 258 chunks (<= 4111 bytes)
+constexpr int kGtSmBytes = 4128 + 32;       // + read-window slack
+constexpr int kGtFull = kGtSm + kGtSmBytes;  // up to 64 chunks of FULL
+constexpr int kGtFullChunks = 64;
+constexpr int kGtBytes = kGtFull + kGtFullChunks * 16 + 16;
+
+struct GtRegs {
+  u32x4 a, b;
+};
+struct GtMeta {
+  int fg0;          // first FULL element of the global tile
+  int full_direct;  // FULL segment larger than the stage: decode reads global
+};
+struct GtOff {
+  int sm0, f0, sm1, f1;  // stream offsets of the tile and of the next one
+  int msm, mf;           // this wave's median-tile start inside the tile
+};
+
+__device__ __forceinline__ GtOff load_gt_offsets(const Streams& s, int g, int m, bool valid) {
+  GtOff t{0, 0, 0, 0, 0, 0};
+  if (valid) {
+    t.sm0 = s.tog[2 * g];
+    t.f0 = s.tog[2 * g + 1];
+    t.sm1 = s.tog[2 * g + 2];
+    t.f1 = s.tog[2 * g + 3];
+    t.msm = s.tom[2 * (4 * g + m)];
+    t.mf = s.tom[2 * (4 * g + m) + 1];
+  }
+  return t;
+}
+
+// Source pointers of one thread's two loads for global tile g.  Role of
+// thread t for load b: t < 96 bitmap chunk, 96..159 FULL chunk, 160..161 SM
+// chunks 256..257, others a clamped re-read of SM chunk 0.
+__device__ __forceinline__ void gt_issue(const Streams& s, int t, const uint8_t* bm_thread,
+                                         int g, int sm0, int sm1, int f0, int f1, GtRegs& r,
+                                         GtMeta& mt) {
+  const int nsm = (sm1 - sm0 + 15) >> 4;  // <= 257
+  const int nfc = (f1 - f0 + 7) >> 3;
+  mt.fg0 = f0;
+  mt.full_direct = nfc > kGtFullChunks;
+  r.a = *reinterpret_cast<const u32x4*>(s.sm + sm0 + (t < nsm ? 16 * t : 0));
+  const uint8_t* pb = s.sm + sm0;
+  if (t < 96) {
+    pb = bm_thread + 512 * g + 16 * (t & 31);
+  } else if (t < 160) {
+    if (t - 96 < nfc && nfc <= kGtFullChunks)
+      pb = reinterpret_cast<const uint8_t*>(s.full + f0 + 8 * (t - 96));
+  } else if (t < 162) {
+    if (t + 96 < nsm) pb = s.sm + sm0 + 16 * (t + 96);
+  }
+  r.b = *reinterpret_cast<const u32x4*>(pb);
+}
+
+__device__ __forceinline__ void gt_write(uint8_t* st, int t, const GtRegs& r) {
+  *reinterpret_cast<u32x4*>(st + kGtSm + 16 * t) = r.a;
+  if (t < 96)
+    *reinterpret_cast<u32x4*>(st + kGtBm + 512 * (t >> 5) + 16 * (t & 31)) = r.b;
+  else if (t < 160)
+    *reinterpret_cast<u32x4*>(st + kGtFull + 16 * (t - 96)) = r.b;
+  else if (t < 162)
+    *reinterpret_cast<u32x4*>(st + kGtSm + 16 * (t + 96)) = r.b;
+}
+
+template <int NB>
+struct Gemm64Smem {
+  static constexpr int kBytes = (int)sizeof(DecodeTables) + 3 * kGtBytes;
+};
+
+template <int NB>
+__global__ __launch_bounds__(256) void gemm64_kernel(Streams s, int start_exp, const uint16_t* X,
+                                                     uint16_t* Y, int M, int N, int K,
+                                                     int kb_per_split) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[Gemm64Smem<NB>::kBytes];
+  DecodeTables& T = *reinterpret_cast<DecodeTables*>(smem);
+  build_decode_tables(T, start_exp, threadIdx.x, blockDim.x);
+  uint8_t* stg0 = smem + sizeof(DecodeTables);
+  uint8_t* stg1 = stg0 + kGtBytes;
+  uint8_t* stg2 = stg1 + kGtBytes;
+
+  const int t = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // median tile of this wave
+  const int l = lane_id();
+  const int gm = blockIdx.x;
+  const int split = blockIdx.y;
+  const int n0 = blockIdx.z * NB * 16;
+  const int KT = K >> 6;
+  const int kb0 = split * kb_per_split;
+  const int n = max(0, min(kb0 + kb_per_split, KT) - kb0);  // tiles of this slice
+
+  const uint16_t* xrow[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int col = min(n0 + nb * 16 + (l & 15), N - 1);
+    xrow[nb] = X + (int64_t)col * K + 8 * (l >> 4);
+  }
+  f32x4 acc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Threads 0..95 load bitmap chunks: plane t/32.
+  const uint8_t* bm_thread = t < 32 ? s.bm1 : (t < 64 ? s.bm2 : s.bm3);
+
+  for (int c0 = 0; c0 < n; c0 += 64) {
+    const int cn = min(n - c0, 64);
+    const int last = cn - 1;
+    const GtOff offs = load_gt_offsets(s, gm * KT + kb0 + c0 + l, w, l < cn);
+    GtRegs R0, R1, R2;
+    GtMeta M0, M1, M2;
+    bf16x8 X0[2][NB], X1[2][NB], X2[2][NB], xc[2][NB];
+    // Tile i's offsets sit in lane i of every wave; the loaders need the
+    // tile's stream bounds, the decoders their own median's start.
+#define ZS_G(J) (gm * KT + kb0 + c0 + (J))
+#define ZS_GISSUE(J, R, MT, XD)                                                          \
+  {                                                                                      \
+    const int jj_ = (J);                                                                 \
+    gt_issue(s, t, bm_thread, ZS_G(jj_), __builtin_amdgcn_readlane(offs.sm0, jj_),       \
+             __builtin_amdgcn_readlane(offs.sm1, jj_),                                   \
+             __builtin_amdgcn_readlane(offs.f0, jj_),                                    \
+             __builtin_amdgcn_readlane(offs.f1, jj_), R, MT);                            \
+    const int kk_ = (kb0 + c0 + jj_) * 64;                                               \
+    _Pragma("unroll") for (int h_ = 0; h_ < 2; ++h_)                                     \
+      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_)                               \
+        XD[h_][nb_] = *reinterpret_cast<const bf16x8*>(xrow[nb_] + kk_ + 32 * h_);       \
+  }
+#define ZS_GSTEP(J, CUR, NXT, RC, MC, XC, RN)                                            \
+  {                                                                                      \
+    const GtMeta cm_ = MC;                                                               \
+    _Pragma("unroll") for (int h_ = 0; h_ < 2; ++h_)                                     \
+      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) xc[h_][nb_] = XC[h_][nb_];    \
+    gt_write(NXT, t, RN);                                                                \
+    ZS_GISSUE(min((J) + 3, last), RC, MC, XC);                                           \
+    __syncthreads();                                                                     \
+    if ((J) < cn) {                                                                      \
+      const int msm_ = __builtin_amdgcn_readlane(offs.msm, (J));                         \
+      const int mf_ = __builtin_amdgcn_readlane(offs.mf, (J));                           \
+      u32x4 a0_, a1_;                                                                    \
+      decode_median_pair(T, CUR + kGtBm + 128 * w, 512, CUR + kGtSm, msm_,               \
+                         reinterpret_cast<const uint16_t*>(CUR + kGtFull), mf_,          \
+                         cm_.full_direct, s.full + cm_.fg0, a0_, a1_);                   \
+      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                             \
+        acc[nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0_), xc[0][nb_],   \
+                                                           acc[nb_], 0, 0, 0);           \
+        acc[nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1_), xc[1][nb_],   \
+                                                           acc[nb_], 0, 0, 0);           \
+      }                                                                                  \
+    }                                                                                    \
+  }
+    if (cn > 0) {
+      ZS_GISSUE(0, R0, M0, X0);
+      ZS_GISSUE(min(1, last), R1, M1, X1);
+      ZS_GISSUE(min(2, last), R2, M2, X2);
+      __syncthreads();  // decode tables built; previous chunk's stages drained
+      gt_write(stg0, t, R0);
+      for (int j = 0; j < cn; j += 3) {
+        ZS_GSTEP(j, stg0, stg1, R0, M0, X0, R1);
+        ZS_GSTEP(j + 1, stg1, stg2, R1, M1, X1, R2);
+        ZS_GSTEP(j + 2, stg2, stg0, R2, M2, X2, R0);
+      }
+    }
+#undef ZS_GSTEP
+#undef ZS_GISSUE
+#undef ZS_G
+  }
+
+  uint16_t* out = Y + (int64_t)split * M * N;
+  const int mrow = gm * 64 + w * 16 + 4 * (l >> 4);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const f32x4 v = acc[nb];
+    const int col = n0 + nb * 16 + (l & 15);
+    if (col < N) {
+      const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+      const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
+      *reinterpret_cast<uint2*>(out + (int64_t)col * M + mrow) = make_uint2(lo, hi);
     }
   }
 }
@@ -163,8 +531,19 @@ static int status_of(hipError_t e) { return e == hipSuccess ? ZS_OK : (int)e; }
 template <int NB>
 static hipError_t launch_gemm(hipStream_t st, const Streams& s, int start_exp, const uint16_t* X,
                               uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split) {
+  constexpr int kWaves = NB <= 4 ? 8 : 4;
   dim3 grid(M / 16, split_k, (N + NB * 16 - 1) / (NB * 16));
-  hipLaunchKernelGGL(gemm_kernel<NB>, grid, dim3(256), 0, st, s, start_exp, X, Y, M, N, K,
+  hipLaunchKernelGGL((gemm_kernel<NB, kWaves>), grid, dim3(kWaves * 64), 0, st, s, start_exp, X,
+                     Y, M, N, K, kb_per_split);
+  return hipGetLastError();
+}
+
+template <int NB>
+static hipError_t launch_gemm64(hipStream_t st, const Streams& s, int start_exp,
+                                const uint16_t* X, uint16_t* Y, int M, int N, int K, int split_k,
+                                int kb_per_split) {
+  dim3 grid(M / 64, split_k, (N + NB * 16 - 1) / (NB * 16));
+  hipLaunchKernelGGL((gemm64_kernel<NB>), grid, dim3(256), 0, st, s, start_exp, X, Y, M, N, K,
                      kb_per_split);
   return hipGetLastError();
 }
@@ -232,7 +611,16 @@ extern "C" int zs_bf16_triple_bitmap_mm(void* stream, const uint8_t* sm, const u
   uint16_t* out = split_k == 1 ? C : ws;
   const int nb = (N + 15) / 16;
   hipError_t e;
-  if (nb <= 1) e = launch_gemm<1>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
+  // A split-K launch has enough workgroups to use the 64-row tile kernel
+  // (long contiguous reads, X shared by the four median tiles); a single
+  // slice keeps 16-row bands so that small M still fills the GPU.
+  const bool wide = split_k > 1 && nb <= 8;
+  if (wide) {
+    if (nb <= 1) e = launch_gemm64<1>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
+    else if (nb <= 2) e = launch_gemm64<2>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
+    else if (nb <= 4) e = launch_gemm64<4>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
+    else e = launch_gemm64<8>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
+  } else if (nb <= 1) e = launch_gemm<1>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
   else if (nb <= 2) e = launch_gemm<2>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
   else if (nb <= 3) e = launch_gemm<3>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
   else if (nb <= 4) e = launch_gemm<4>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
