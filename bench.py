@@ -32,6 +32,7 @@ SHAPES = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate", 14336, 4096), ("up", 
           ("down", 4096, 14336)]
 NS = [1, 8, 16, 32, 64, 128]
 HBM_PEAK_GBS = 8000.0
+CALIB_BYTES = 256 << 20
 
 
 def parse():
@@ -45,6 +46,30 @@ def parse():
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--reps", type=int, default=20, help="graph replays per (shape, N) in the per-kernel timing")
     return ap.parse_args()
+
+
+def kernel_name(N):
+    """Instantiation of zs::gemm_kernel that zs_bf16_triple_bitmap_mm picks for
+    split-K 1 at batch N (ceil(N/16) column blocks of 16, rounded up to a
+    compiled width; 8 waves per workgroup up to 4 blocks, else 4)."""
+    nb = (N + 15) // 16
+    nb = next(w for w in (1, 2, 3, 4, 6, 8, 16) if w >= nb) if nb <= 16 else 16
+    return f"zs::gemm_kernel<{nb}, {8 if nb <= 4 else 4}>"
+
+
+def traffic_from_profile(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a copy kernel of
+    known size); None when the summary has no line for this kernel."""
+    path = os.path.join(ROOT, "profiles", "zs_gemm_kernel_pmc_llama3-8b_sweep.md")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch") and f"`{kernel}`" in line:
+                return {"bytes_per_launch": int(line.rsplit(":", 1)[1].strip()),
+                        "source": os.path.relpath(path, ROOT)}
+    return None
 
 
 def make_layer(torch, zs, gen, dev):
@@ -136,6 +161,15 @@ def main():
         enc_t += time.perf_counter() - t1
         enc_bytes += 2 * M * K
 
+    # Calibration kernel for HBM counters: an elementwise negation of 256 MiB
+    # (reads and writes exactly CALIB_BYTES each); rocprofv3 --pmc runs of this
+    # script scale FETCH_SIZE / WRITE_SIZE of the GEMM kernels by its reading.
+    ca = torch.empty(CALIB_BYTES // 2, device=dev, dtype=torch.bfloat16).fill_(1.0)
+    cb = torch.empty_like(ca)
+    torch.neg(ca, out=cb)
+    torch.cuda.synchronize()
+    del ca, cb
+
     stream = torch.cuda.Stream()
 
     def capture(fn):
@@ -200,7 +234,8 @@ def main():
             alg = comp + 2 * N * K + 2 * N * M
             sum_alg_bytes += alg
             sum_kernel_s += tz
-            row = {"shape": name, "M": M, "K": K, "N": N, "zip_us": round(tz * 1e6, 2),
+            row = {"shape": name, "M": M, "K": K, "N": N, "kernel": kernel_name(N),
+                   "zip_us": round(tz * 1e6, 3), "alg_bytes": alg,
                    "eff_TBps": round(2 * M * K / tz / 1e12, 3),
                    "comp_TBps": round(alg / tz / 1e12, 3)}
             if not args.no_dense:
@@ -213,7 +248,22 @@ def main():
             per.append(row)
 
     ratio = sum(2 * M * K for _, M, K in SHAPES) / sum(c.compressed_bytes for _, _, _, _, c in layers[0])
-    achieved = sum_alg_bytes / sum_kernel_s / 1e9
+    # Per-kernel roll-up: launches of one instantiation, its average launch
+    # time and average algorithmic bytes; the dominant one carries the roofline.
+    kernels = {}
+    for row in per:
+        k = kernels.setdefault(kernel_name(row["N"]), {"launches": 0, "time_s": 0.0, "alg_bytes": 0.0})
+        k["launches"] += 1
+        k["time_s"] += row["zip_us"] * 1e-6
+        k["alg_bytes"] += row["alg_bytes"]
+    for k in kernels.values():
+        k["avg_us"] = round(k["time_s"] / k["launches"] * 1e6, 3)
+        k["avg_alg_bytes"] = int(k["alg_bytes"] / k["launches"])
+        k["achieved_GBps"] = round(k["alg_bytes"] / k["time_s"] / 1e9, 1)
+    dominant = max(kernels, key=lambda n: kernels[n]["time_s"])
+    dk = kernels[dominant]
+    achieved = dk["alg_bytes"] / dk["time_s"] / 1e9
+    traffic = traffic_from_profile(dominant)
     out = {
         "metric": METRIC,
         "value": round(value, 4),
@@ -246,10 +296,15 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "zs::gemm_kernel",
-            "algorithmic_bytes": "comp_bytes(W) + 2*N*K + 2*N*M per launch, summed over the 30 launches of a step",
+            "traffic": None if traffic is None else traffic["bytes_per_launch"],
+            "kernel": dominant,
+            "avg_launch_us": dk["avg_us"],
+            "alg_bytes_per_launch": dk["avg_alg_bytes"],
+            "algorithmic_bytes": "comp_bytes(W) + 2*N*K + 2*N*M per launch, averaged over the "
+                                 "launches of this instantiation in one step",
+            "traffic_source": None if traffic is None else traffic["source"],
         },
+        "kernels": kernels,
         "per_launch": per,
         "setup_s": round(setup_s, 2),
     }
