@@ -1,18 +1,487 @@
-// zs_attention.hip -- decode attention over compressed / dense KV (gfx950).
+// zs_attention.hip -- single-token (decode) GQA attention over a KV cache held
+// in the TCA-TBE format, and the same kernel over a dense bf16 cache (gfx950).
+//
+// Work unit: one wave per (batch b, KV head h, sequence split).  The wave walks
+// its token range 16 tokens (one median-tile row band) at a time in four steps
+//   K0: decode K median tile, dims 0..63   -> S^T += K q^T  (2 x mfma 16x16x32)
+//   K1: decode K median tile, dims 64..127 -> S^T complete; online softmax
+//   V0: decode V median tile, dims 0..63   -> O^T += V^T P^T (4 x mfma 16x16x16)
+//   V1: decode V median tile, dims 64..127 -> O^T += V^T P^T (4 x mfma 16x16x16)
+// S^T is tokens x heads: the decoded K fragment (lane l: token l%16, dims
+// 8*(l/16)..+7) is the A operand as is and q (lane l: head l%16) the B operand.
+// Its accumulator layout (lane l: head l%16, tokens 4*(l/16)+r) is exactly the
+// B operand P^T of the 16x16x16 product, and the A operand V^T (lane l: dim
+// l%16, tokens 4*(l/16)+j) comes from the decoded V tile written row-major to
+// LDS and read back with ds_read_b64_tr_b16.  The O^T accumulator keeps head
+// l%16 in lane l, the same lanes that hold that head's running max and sum.
+//
+// The median tiles are prefetched four steps ahead into registers and staged
+// through a wave-private LDS double buffer (zs_stage.hpp), as in ZipGEMM.
+// Splits write unnormalised partials (O, m, l) that attn_combine_kernel merges.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cmath>
+
 #include "../../include/zipserv.h"
+#include "zs_device.hpp"
+#include "zs_stage.hpp"
 
-extern "C" size_t zs_decode_attention_workspace_bytes(int, int, int, int, int) { return 0; }
+namespace zs {
 
-extern "C" int zs_decode_attention(void*, const uint16_t*, const zs_kv_compressed_t*,
-                                   const zs_kv_compressed_t*, const int32_t*, int, int, int, int,
-                                   int, float, uint16_t*, float*, void*, size_t, int) {
-  return ZS_E_UNSUPPORTED;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kHeadDim = 128;
+constexpr int kAttnWaves = 4;
+constexpr int kVRow = 160;                  // LDS row pitch of the V tile (bytes)
+constexpr int kVBytes = 16 * kVRow;         // 16 tokens x 64 dims (+ pad)
+constexpr int kAttnWaveLds = 2 * kStBytes + kVBytes;
+
+struct AttnParams {
+  Streams k, v;                 // compressed caches (compressed kernel)
+  const uint16_t* kd;           // dense caches [B][cap][Hkv][D] (dense kernel)
+  const uint16_t* vd;
+  int k_start, v_start;         // start_exp of K and V
+  int k_bsr, k_hsr, v_bsr, v_hsr;  // batch / head strides in rows (compressed)
+  int cap;                      // dense cache capacity (tokens)
+  const uint16_t* q;            // [B][H][D]
+  uint16_t* out;                // [B][H][D]
+  float* lse;                   // [B][H] or null
+  float* ws_o;                  // [B][H][splits][D]   (splits > 1)
+  float* ws_ml;                 // [B][H][splits][2]
+  const int32_t* seqlens;       // [B] or null
+  int seqlen_k, batch, heads, heads_k, group, splits, chunk;
+  float scale_log2;             // softmax_scale * log2(e)
+};
+
+__device__ __forceinline__ void build_e1(uint4* e1, int start_exp, int tid, int nthreads) {
+  for (int v = tid; v < 256; v += nthreads) {
+    uint32_t w[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t lo = (v >> (2 * d)) & 1, hi = (v >> (2 * d + 1)) & 1;
+      w[d] = ((uint32_t)(start_exp + lo) << 7) | ((uint32_t)(start_exp + hi) << 23);
+    }
+    e1[v] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
 }
 
-extern "C" int zs_decode_attention_dense(void*, const uint16_t*, const uint16_t*, const uint16_t*,
-                                         const int32_t*, int, int, int, int, int, int, float,
-                                         uint16_t*, float*, void*, size_t, int) {
-  return ZS_E_UNSUPPORTED;
+__device__ __forceinline__ float wave_max16(float x) {
+  // max over lanes l, l^16, l^32, l^48 (the four row groups)
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ __forceinline__ float wave_sum16(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const __bf16 ha = (__bf16)a, hb = (__bf16)b;
+  return (uint32_t)__builtin_bit_cast(unsigned short, ha) |
+         ((uint32_t)__builtin_bit_cast(unsigned short, hb) << 16);
+}
+
+// Median tile `med` (16 tokens) of the wave's range, column tile c, of K or V:
+// global tile index in the compressed 2D matrix (2 column tiles of 64).
+__device__ __forceinline__ int kv_tile(int rowbase, int med, int c) {
+  return ((rowbase >> 6) + (med >> 2)) * 2 + c;
+}
+
+template <bool kDense>
+__global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnParams p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t attn_smem[];
+  DecodeTables& T = *reinterpret_cast<DecodeTables*>(attn_smem);
+  uint4* e1v = reinterpret_cast<uint4*>(attn_smem + sizeof(DecodeTables));
+  if constexpr (!kDense) {
+    build_decode_tables(T, p.k_start, threadIdx.x, blockDim.x);
+    build_e1(e1v, p.v_start, threadIdx.x, blockDim.x);
+  }
+  __syncthreads();
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = lane_id();
+  const int item = blockIdx.x * kAttnWaves + w;
+  if (item >= p.batch * p.heads_k * p.splits) return;
+  const int sp = item % p.splits;
+  const int h = (item / p.splits) % p.heads_k;
+  const int b = item / (p.splits * p.heads_k);
+  int L = p.seqlen_k;
+  if (p.seqlens) L = min(L, __builtin_amdgcn_readfirstlane(p.seqlens[b]));
+  L = max(L, 0);
+  const int t0 = sp * p.chunk;
+  const int t1 = min(t0 + p.chunk, L);
+  const int nmed = t1 > t0 ? (t1 - t0 + 15) >> 4 : 0;
+
+  uint8_t* wl = attn_smem + (kDense ? 0 : sizeof(DecodeTables) + 256 * 16) + w * kAttnWaveLds;
+  uint8_t* stage0 = wl;
+  uint8_t* stage1 = wl + kStBytes;
+  uint8_t* vbuf = wl + 2 * kStBytes;
+
+  // q^T fragments (B operand): lane l -> head l%16 of this KV group, dims
+  // 32c + 8*(l/16) .. +7.  Heads past the group read head 0 and are dropped.
+  const int g = l & 15;
+  const int qh = h * p.group + (g < p.group ? g : 0);
+  const uint16_t* qrow = p.q + ((int64_t)b * p.heads + qh) * kHeadDim + 8 * (l >> 4);
+  bf16x8 Q[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) Q[c] = *reinterpret_cast<const bf16x8*>(qrow + 32 * c);
+
+  f32x4 O[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 S = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint32_t pb0 = 0, pb1 = 0;  // P^T of the current 16 tokens, bf16 pairs
+
+  // tr16 read address of the V tile: token 4*(l/16) + (l%16)/4, dim 4*(l%4)
+  // (+16 per 16-dim block) -> lane gets V[4*(l/16)+j][16*blk + l%16], j=0..3.
+  const int vtr = (4 * (l >> 4) + ((l & 15) >> 2)) * kVRow + 8 * (l & 3);
+  // ds_write of the decoded half h: token l%16, dims 32h + 8*(l/16).
+  const int vwr = (l & 15) * kVRow + 16 * (l >> 4);
+
+  const int k_rowbase = kDense ? 0 : b * p.k_bsr + h * p.k_hsr + t0;
+  const int v_rowbase = kDense ? 0 : b * p.v_bsr + h * p.v_hsr + t0;
+  const uint8_t* bmk = l < 8 ? p.k.bm1 : (l < 16 ? p.k.bm2 : p.k.bm3);
+  const uint8_t* bmv = l < 8 ? p.v.bm1 : (l < 16 ? p.v.bm2 : p.v.bm3);
+
+  // Dense rows: token of lane l in median `med`, clamped to the valid range.
+  auto dense_row = [&](const uint16_t* base, int med) -> const uint16_t* {
+    const int t = min(t0 + 16 * med + (l & 15), L - 1);
+    return base + (((int64_t)b * p.cap + t) * p.heads_k + h) * kHeadDim + 8 * (l >> 4);
+  };
+
+  // One step: consume the fragments (a0, a1) of step type TY (0 = K0, 1 = K1,
+  // 2 = V0, 3 = V1) for median `med`.
+  auto consume = [&](int TY, int med, u32x4 a0, u32x4 a1) {
+    if (TY < 2) {
+      if (TY == 0) S = f32x4{0.f, 0.f, 0.f, 0.f};
+      S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0), Q[2 * TY], S, 0, 0, 0);
+      S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1), Q[2 * TY + 1], S, 0, 0, 0);
+      if (TY == 1) {
+        // online softmax over this median's 16 tokens (log2 domain)
+        const int tb = t0 + 16 * med + 4 * (l >> 4);
+        float s[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          s[r] = (tb + r < t1) ? S[r] * p.scale_log2 : -INFINITY;
+          mx = fmaxf(mx, s[r]);
+        }
+        mx = wave_max16(mx);
+        const float m_new = fmaxf(m_run, mx);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        float pr[4], ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          pr[r] = __builtin_amdgcn_exp2f(s[r] - m_use);
+          ps += pr[r];
+        }
+        ps = wave_sum16(ps);
+        l_run = l_run * alpha + ps;
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) O[i] *= alpha;
+        }
+        m_run = m_new;
+        pb0 = pack_bf16x2(pr[0], pr[1]);
+        pb1 = pack_bf16x2(pr[2], pr[3]);
+      }
+    } else {
+      // V^T P^T for the 64 dims of this column tile, via the LDS transpose
+      *reinterpret_cast<u32x4*>(vbuf + vwr) = a0;
+      *reinterpret_cast<u32x4*>(vbuf + vwr + 64) = a1;
+      const v4i16 pbv = __builtin_bit_cast(v4i16, (uint2){pb0, pb1});
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        const v4i16 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4i16*)(vbuf + vtr + 32 * blk));
+        const int oi = 4 * (TY - 2) + blk;
+        O[oi] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pbv, O[oi], 0, 0, 0);
+      }
+    }
+  };
+
+  if (nmed > 0) {
+    const int nstep = 4 * nmed;
+    const int last = nstep - 1;
+    if constexpr (kDense) {
+      // Fragments fetched four steps ahead straight into registers.
+      u32x4 A0[4], A1[4];
+      auto fetch = [&](int j, u32x4& x0, u32x4& x1) {
+        const int ty = j & 3, med = j >> 2;
+        const uint16_t* r = dense_row(ty < 2 ? p.kd : p.vd, med) + 64 * (ty & 1);
+        x0 = *reinterpret_cast<const u32x4*>(r);
+        x1 = *reinterpret_cast<const u32x4*>(r + 32);
+      };
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fetch(i, A0[i], A1[i]);  // nstep >= 4
+      for (int j = 0; j < nstep; j += 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const u32x4 a0 = A0[i], a1 = A1[i];
+          const int jn = j + 4 + i;
+          fetch(jn <= last ? jn : ((last & ~3) | i), A0[i], A1[i]);
+          consume(i, (j >> 2), a0, a1);
+        }
+      }
+    } else {
+      // Offsets of up to 64 steps at a time (lane i -> step c0 + i).
+      for (int c0 = 0; c0 < nstep; c0 += 64) {
+        const int n = min(nstep - c0, 64);
+        const int lastc = n - 1;
+        TileOff offs{0, 0, 0, 0};
+        {
+          const int j = c0 + min(l, lastc);
+          const int ty = j & 3, med = j >> 2;
+          const Streams& st = ty < 2 ? p.k : p.v;
+          const int gt = kv_tile(ty < 2 ? k_rowbase : v_rowbase, med, ty & 1);
+          offs = load_tile_offsets(st, gt, med & 3, true);
+        }
+        StageRegs R0, R1, R2, R3;
+        StageMeta M0, M1, M2, M3;
+        // step index within the chunk -> (type, median) of the whole range
+// Step type I (0..3) is a literal at every use, so the K / V choice is static.
+#define ZA_ISSUE(J, I, R, MT)                                                          \
+  {                                                                                    \
+    const int jj_ = (J);                                                               \
+    const int med_ = (c0 + jj_) >> 2;                                                  \
+    stage_issue((I) < 2 ? p.k : p.v, (I) < 2 ? bmk : bmv,                              \
+                kv_tile((I) < 2 ? k_rowbase : v_rowbase, med_, (I) & 1), med_ & 3,     \
+                tile_off_at(offs, jj_), R, MT);                                        \
+  }
+        // Clamp keeps the step type of the slot (c0 and n are multiples of 4).
+#define ZA_CLAMP(J, I) ((J) <= lastc ? (J) : ((lastc & ~3) | (I)))
+#define ZA_STEP(J, I, CUR, NXT, RC, MC, RN)                                            \
+  {                                                                                    \
+    const StageMeta cm_ = MC;                                                          \
+    stage_write(NXT, RN);                                                              \
+    ZA_ISSUE(ZA_CLAMP((J) + 4, I), I, RC, MC);                                            \
+    const Streams& st_ = (I) < 2 ? p.k : p.v;                                          \
+    u32x4 a0_, a1_;                                                                    \
+    decode_median_pair(T, (I) < 2 ? T.e1 : e1v, CUR + kStBm, 128, CUR + kStSm,         \
+                       cm_.sm_rel, reinterpret_cast<const uint16_t*>(CUR + kStFull),   \
+                       cm_.full_rel, cm_.full_direct, st_.full + cm_.fa0, a0_, a1_);   \
+    consume((I), (c0 + (J)) >> 2, a0_, a1_);                                           \
+  }
+        ZA_ISSUE(0, 0, R0, M0);  // n >= 4: a chunk holds whole medians
+        ZA_ISSUE(1, 1, R1, M1);
+        ZA_ISSUE(2, 2, R2, M2);
+        ZA_ISSUE(3, 3, R3, M3);
+        stage_write(stage0, R0);
+        for (int j = 0; j < n; j += 4) {
+          ZA_STEP(j, 0, stage0, stage1, R0, M0, R1);
+          ZA_STEP(j + 1, 1, stage1, stage0, R1, M1, R2);
+          ZA_STEP(j + 2, 2, stage0, stage1, R2, M2, R3);
+          ZA_STEP(j + 3, 3, stage1, stage0, R3, M3, R0);
+        }
+#undef ZA_STEP
+#undef ZA_CLAMP
+#undef ZA_ISSUE
+      }
+    }
+  }
+
+  // Results: lane l holds head g = l%16, dims 16*i + 4*(l/16) + r of O[i].
+  const int head = h * p.group + g;
+  const bool own = g < p.group;
+  const int d0 = 4 * (l >> 4);
+  if (p.splits == 1) {
+    if (own) {
+      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+      uint16_t* orow = p.out + ((int64_t)b * p.heads + head) * kHeadDim + d0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint2 v;
+        v.x = pack_bf16x2(O[i][0] * inv, O[i][1] * inv);
+        v.y = pack_bf16x2(O[i][2] * inv, O[i][3] * inv);
+        *reinterpret_cast<uint2*>(orow + 16 * i) = v;
+      }
+      if (p.lse && l < 16)
+        p.lse[(int64_t)b * p.heads + head] =
+            l_run > 0.f ? (m_run + __log2f(l_run)) * 0.6931471805599453f : -INFINITY;
+    }
+  } else if (own) {
+    const int64_t slot = ((int64_t)b * p.heads + head) * p.splits + sp;
+    float* wo = p.ws_o + slot * kHeadDim + d0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<f32x4*>(wo + 16 * i) = O[i];
+    if (l < 16) {
+      p.ws_ml[2 * slot] = m_run;
+      p.ws_ml[2 * slot + 1] = l_run;
+    }
+  }
+}
+
+// Merges the split partials of one (batch, head): 128 threads, one per dim.
+__global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(AttnParams p) {
+  const int bh = blockIdx.x;
+  const int d = threadIdx.x;
+  const float* ml = p.ws_ml + (int64_t)bh * p.splits * 2;
+  float m = -INFINITY;
+  for (int s = 0; s < p.splits; ++s) m = fmaxf(m, ml[2 * s]);
+  const float m_use = m == -INFINITY ? 0.f : m;
+  float lsum = 0.f, acc = 0.f;
+  const float* wo = p.ws_o + (int64_t)bh * p.splits * kHeadDim + d;
+  for (int s = 0; s < p.splits; ++s) {
+    const float sc = ml[2 * s + 1] > 0.f ? __builtin_amdgcn_exp2f(ml[2 * s] - m_use) : 0.f;
+    lsum += ml[2 * s + 1] * sc;
+    acc += wo[(int64_t)s * kHeadDim] * sc;
+  }
+  const float v = lsum > 0.f ? acc / lsum : 0.f;
+  p.out[(int64_t)bh * kHeadDim + d] = (uint16_t)f32_to_bf16_bits(v);
+  if (p.lse && d == 0)
+    p.lse[bh] = lsum > 0.f ? (m + __log2f(lsum)) * 0.6931471805599453f : -INFINITY;
+}
+
+static int attn_auto_splits(int batch, int heads_k, int seqlen_k) {
+  // Aim for about 2048 waves; at least 256 tokens per split.
+  const int units = std::max(1, batch * heads_k);
+  const int max_splits = std::max(1, (seqlen_k + 255) / 256);
+  return std::min(max_splits, std::max(1, (2048 + units - 1) / units));
+}
+
+static int attn_chunk(int seqlen_k, int splits) {
+  const int blocks = (seqlen_k + 63) / 64;
+  return ((blocks + splits - 1) / splits) * 64;
+}
+
+static size_t attn_ws_bytes(int batch, int heads, int splits) {
+  if (splits <= 1) return 0;
+  return (size_t)batch * heads * splits * (kHeadDim + 2) * sizeof(float);
+}
+
+template <bool kDense>
+static int attn_launch(hipStream_t st, AttnParams& p, void* workspace, size_t ws_bytes) {
+  if (p.splits > 1) {
+    if (!workspace || ws_bytes < attn_ws_bytes(p.batch, p.heads, p.splits)) return ZS_E_INVAL;
+    p.ws_o = reinterpret_cast<float*>(workspace);
+    p.ws_ml = p.ws_o + (size_t)p.batch * p.heads * p.splits * kHeadDim;
+  }
+  const int items = p.batch * p.heads_k * p.splits;
+  const int grid = (items + kAttnWaves - 1) / kAttnWaves;
+  const size_t lds = (kDense ? 0 : sizeof(DecodeTables) + 256 * 16) +
+                     (size_t)kAttnWaves * kAttnWaveLds;
+  hipLaunchKernelGGL(attn_kernel<kDense>, dim3(grid), dim3(kAttnWaves * 64), lds, st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  if (p.splits > 1) {
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(p.batch * p.heads), dim3(kHeadDim), 0, st, p);
+    e = hipGetLastError();
+  }
+  return e == hipSuccess ? ZS_OK : (int)e;
+}
+
+static int attn_common_checks(int batch, int heads, int heads_k, int head_dim, int seqlen_k,
+                              int num_splits, const void* q, const void* out) {
+  if (!q || !out || batch <= 0 || heads <= 0 || heads_k <= 0 || seqlen_k < 0 || num_splits < 0)
+    return ZS_E_INVAL;
+  if (heads % heads_k) return ZS_E_INVAL;
+  if (head_dim != kHeadDim || heads / heads_k > 16) return ZS_E_UNSUPPORTED;
+  return ZS_OK;
+}
+
+}  // namespace zs
+
+using namespace zs;
+
+extern "C" size_t zs_decode_attention_workspace_bytes(int batch, int num_heads, int head_dim,
+                                                      int seqlen_k, int num_splits) {
+  if (batch <= 0 || num_heads <= 0 || head_dim != kHeadDim || seqlen_k < 0) return 0;
+  // num_splits == 0 asks for the automatic choice; its size is bounded by
+  // the split count of a single KV head.
+  const int splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, 1, seqlen_k);
+  return attn_ws_bytes(batch, num_heads, splits);
+}
+
+extern "C" int zs_decode_attention(void* stream, const uint16_t* q, const zs_kv_compressed_t* k,
+                                   const zs_kv_compressed_t* v, const int32_t* cache_seqlens,
+                                   int seqlen_k, int batch, int num_heads, int num_heads_k,
+                                   int head_dim, float softmax_scale, uint16_t* out,
+                                   float* softmax_lse, void* workspace, size_t workspace_bytes,
+                                   int num_splits) {
+  int stc = attn_common_checks(batch, num_heads, num_heads_k, head_dim, seqlen_k, num_splits, q,
+                               out);
+  if (stc != ZS_OK) return stc;
+  if (!k || !v) return ZS_E_INVAL;
+  const zs_kv_compressed_t* kv[2] = {k, v};
+  for (const zs_kv_compressed_t* c : kv) {
+    if (!c->sign_mantissa || !c->compressed_full || !c->bitmap1 || !c->bitmap2 ||
+        !c->bitmap3 || !c->tile_offsets_median || !c->tile_offsets_global)
+      return ZS_E_INVAL;
+    if (c->layout != ZS_LAYOUT_HEAD_MAJOR) return ZS_E_UNSUPPORTED;
+    if (c->cols != kHeadDim || c->rows <= 0 || (c->rows % 64)) return ZS_E_INVAL;
+    if (c->head_stride_rows <= 0 || (c->head_stride_rows % 64) ||
+        c->batch_stride_rows != num_heads_k * c->head_stride_rows ||
+        (int64_t)c->batch_stride_rows * batch > c->rows || c->head_stride_rows < seqlen_k)
+      return ZS_E_INVAL;
+    if (c->start_exp < 0 || c->start_exp > 255) return ZS_E_INVAL;
+  }
+  AttnParams p{};
+  auto streams = [](const zs_kv_compressed_t* c) {
+    Streams s;
+    s.sm = c->sign_mantissa;
+    s.full = c->compressed_full;
+    s.bm1 = reinterpret_cast<const uint8_t*>(c->bitmap1);
+    s.bm2 = reinterpret_cast<const uint8_t*>(c->bitmap2);
+    s.bm3 = reinterpret_cast<const uint8_t*>(c->bitmap3);
+    s.tom = c->tile_offsets_median;
+    s.tog = c->tile_offsets_global;
+    return s;
+  };
+  p.k = streams(k);
+  p.v = streams(v);
+  p.k_start = k->start_exp;
+  p.v_start = v->start_exp;
+  p.k_bsr = k->batch_stride_rows;
+  p.k_hsr = k->head_stride_rows;
+  p.v_bsr = v->batch_stride_rows;
+  p.v_hsr = v->head_stride_rows;
+  p.q = q;
+  p.out = out;
+  p.lse = softmax_lse;
+  p.seqlens = cache_seqlens;
+  p.seqlen_k = seqlen_k;
+  p.batch = batch;
+  p.heads = num_heads;
+  p.heads_k = num_heads_k;
+  p.group = num_heads / num_heads_k;
+  p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k);
+  p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
+  p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
+  p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  return attn_launch<false>((hipStream_t)stream, p, workspace, workspace_bytes);
+}
+
+extern "C" int zs_decode_attention_dense(void* stream, const uint16_t* q, const uint16_t* k_cache,
+                                         const uint16_t* v_cache, const int32_t* cache_seqlens,
+                                         int seqlen_k, int cache_capacity, int batch,
+                                         int num_heads, int num_heads_k, int head_dim,
+                                         float softmax_scale, uint16_t* out, float* softmax_lse,
+                                         void* workspace, size_t workspace_bytes,
+                                         int num_splits) {
+  int stc = attn_common_checks(batch, num_heads, num_heads_k, head_dim, seqlen_k, num_splits, q,
+                               out);
+  if (stc != ZS_OK) return stc;
+  if (!k_cache || !v_cache || cache_capacity < seqlen_k) return ZS_E_INVAL;
+  AttnParams p{};
+  p.kd = k_cache;
+  p.vd = v_cache;
+  p.cap = cache_capacity;
+  p.q = q;
+  p.out = out;
+  p.lse = softmax_lse;
+  p.seqlens = cache_seqlens;
+  p.seqlen_k = seqlen_k;
+  p.batch = batch;
+  p.heads = num_heads;
+  p.heads_k = num_heads_k;
+  p.group = num_heads / num_heads_k;
+  p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k);
+  p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
+  p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
+  p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  return attn_launch<true>((hipStream_t)stream, p, workspace, workspace_bytes);
 }

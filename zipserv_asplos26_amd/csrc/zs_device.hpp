@@ -148,11 +148,14 @@ __device__ __forceinline__ RowRef load_half_median(const Streams& s, int64_t bm_
 // In-window part of a row decode: gathers the lane's sign|mantissa bytes from
 // a 12-byte SM window (w0..w2, starting `sh` bytes before the row's first
 // byte) with v_perm and merges the exponent field from the LDS tables with
-// v_bfi.  Outlier positions hold garbage until patched.
-__device__ __forceinline__ u32x4 decode_inwindow(const DecodeTables& T, uint32_t b1, uint32_t b2,
-                                                 uint32_t b3, uint32_t ind, uint32_t w0,
-                                                 uint32_t w1, uint32_t w2, uint32_t sh) {
-  const uint4 x1 = T.e1[b1];
+// v_bfi.  `e1` is the plane-1 table holding the start_exp bias (T.e1, or a
+// second table for a matrix with another window).  Outlier positions hold
+// garbage until patched.
+__device__ __forceinline__ u32x4 decode_inwindow(const DecodeTables& T, const uint4* e1,
+                                                 uint32_t b1, uint32_t b2, uint32_t b3,
+                                                 uint32_t ind, uint32_t w0, uint32_t w1,
+                                                 uint32_t w2, uint32_t sh) {
+  const uint4 x1 = e1[b1];
   const uint4 x2 = T.e2[b2];
   const uint4 x3 = T.e3[b3];
   const uint4 sel = T.sel[ind];
@@ -216,7 +219,7 @@ __device__ __forceinline__ u32x4 decode_row(const Streams& s, const DecodeTables
                                             const RowRef& r) {
   const int64_t a = r.sm_off & ~(int64_t)3;
   const uint32_t* w = reinterpret_cast<const uint32_t*>(s.sm + a);
-  u32x4 o = decode_inwindow(T, r.b1, r.b2, r.b3, r.ind, w[0], w[1], w[2],
+  u32x4 o = decode_inwindow(T, T.e1, r.b1, r.b2, r.b3, r.ind, w[0], w[1], w[2],
                             (uint32_t)(r.sm_off & 3));
   uint32_t fm = (~r.ind) & 0xFFu;
   if (fm) {
@@ -241,10 +244,11 @@ __device__ __forceinline__ u32x4 decode_row(const Streams& s, const DecodeTables
 // Returns the two MFMA A operands.
 struct HalfDec {
   uint32_t b1, b2, b3, ind;
-  int excl, incl;
+  int n, excl, incl;
 };
 
-__device__ __forceinline__ void decode_median_pair(const DecodeTables& T, const uint8_t* bm,
+__device__ __forceinline__ void decode_median_pair(const DecodeTables& T, const uint4* e1,
+                                                   const uint8_t* bm,
                                                    int plane_stride, const uint8_t* smb, int msm,
                                                    const uint16_t* fub, int mf, bool direct,
                                                    const uint16_t* gfull, u32x4& o0, u32x4& o1) {
@@ -259,9 +263,9 @@ __device__ __forceinline__ void decode_median_pair(const DecodeTables& T, const 
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     d[h].ind = d[h].b1 | d[h].b2 | d[h].b3;
-    const int n = __builtin_popcount(d[h].ind);
-    d[h].incl = wave_inclusive_scan(n);
-    d[h].excl = d[h].incl - n;
+    d[h].n = __builtin_popcount(d[h].ind);
+    d[h].incl = wave_inclusive_scan(d[h].n);
+    d[h].excl = d[h].incl - d[h].n;
   }
   const int tot0 = __builtin_amdgcn_readlane(d[0].incl, 63);
   u32x4 o[2];
@@ -271,7 +275,7 @@ __device__ __forceinline__ void decode_median_pair(const DecodeTables& T, const 
     const int smo = msm + (h ? tot0 : 0) + d[h].excl;
     fo[h] = mf + (h ? 512 - tot0 : 0) + 8 * l - d[h].excl;
     const uint32_t* wp = reinterpret_cast<const uint32_t*>(smb + (smo & ~3));
-    o[h] = decode_inwindow(T, d[h].b1, d[h].b2, d[h].b3, d[h].ind, wp[0], wp[1], wp[2],
+    o[h] = decode_inwindow(T, e1, d[h].b1, d[h].b2, d[h].b3, d[h].ind, wp[0], wp[1], wp[2],
                            (uint32_t)(smo & 3));
   }
   if (!direct) {
@@ -286,13 +290,14 @@ __device__ __forceinline__ void decode_median_pair(const DecodeTables& T, const 
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      // Rows with more than four outliers (rare) patch the rest one by one.
-      uint32_t rest = (~d[h].ind) & 0xFFu;
-      rest &= rest - 1;
-      rest &= rest - 1;
-      rest &= rest - 1;
-      rest &= rest - 1;
-      if (rest) {
+      // Rows with more than four outliers (fewer than four in-window
+      // elements; rare) patch the rest one by one.
+      if (d[h].n < 4) {
+        uint32_t rest = (~d[h].ind) & 0xFFu;
+        rest &= rest - 1;
+        rest &= rest - 1;
+        rest &= rest - 1;
+        rest &= rest - 1;
         int k = 4;
         while (rest) {
           patch_outlier(o[h], __builtin_ctz(rest), fub[fo[h] + k]);

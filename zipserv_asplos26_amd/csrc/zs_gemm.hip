@@ -16,6 +16,7 @@
 
 #include "../../include/zipserv.h"
 #include "zs_device.hpp"
+#include "zs_stage.hpp"
 
 namespace zs {
 
@@ -56,100 +57,6 @@ __global__ __launch_bounds__(256) void decompress_kernel(Streams s, int start_ex
 // offsets, so the copy of tile j+2 is in flight while tile j is decoded --
 // and decodes each half median tile from LDS into one MFMA A operand.
 // ---------------------------------------------------------------------------
-constexpr int kStBm = 0;                     // 3 x 128 B bitmap planes
-constexpr int kStSm = 384;                   // SM bytes from the 16-aligned start
-constexpr int kStSmBytes = 1056;             // 65 chunks used + read-window slack
-constexpr int kStFull = kStSm + kStSmBytes;  // FULL elements from the 8-aligned start
-constexpr int kFullChunks = 33;              // staged outliers: up to 264 per median tile
-constexpr int kStBytes = kStFull + kFullChunks * 16 + 16;  // + window-read slack
-
-struct StageRegs {
-  u32x4 sm;    // SM chunk l (16 bytes) of the median tile
-  u32x4 misc;  // lanes 0..23 bitmap chunks, 24..56 FULL chunks, 57 SM chunk 64
-};
-struct StageMeta {
-  int sm_rel;    // first SM byte of the median tile relative to the stage copy
-  int full_rel;  // first FULL element relative to the stage copy
-  int fa0;       // stream offset of the stage copy's first FULL element
-  int full_direct;  // outliers did not fit the stage: read them from global
-};
-
-// Stream offsets of one median tile: first SM byte, first FULL element, and
-// the first ones after it (the next median tile's start, or the next global
-// tile's padded start for the last median tile).
-struct TileOff {
-  int hf0, f0, hf1, f1;
-};
-
-// Vector-loads the offsets of up to 64 median tiles (lane i -> tile i) so the
-// pipeline reads them with readlane instead of waiting on scalar loads.
-__device__ __forceinline__ TileOff load_tile_offsets(const Streams& s, int g, int m, bool valid) {
-  TileOff t{0, 0, 0, 0};
-  if (valid) {
-    const int t0 = s.tog[2 * g], tf0 = s.tog[2 * g + 1];
-    const int mb = 2 * (4 * g + m);
-    t.hf0 = t0 + s.tom[mb];
-    t.f0 = tf0 + s.tom[mb + 1];
-    if (m < 3) {
-      t.hf1 = t0 + s.tom[mb + 2];
-      t.f1 = tf0 + s.tom[mb + 3];
-    } else {
-      t.hf1 = s.tog[2 * g + 2];
-      t.f1 = s.tog[2 * g + 3];
-    }
-  }
-  return t;
-}
-
-__device__ __forceinline__ TileOff tile_off_at(const TileOff& v, int i) {
-  TileOff t;
-  t.hf0 = __builtin_amdgcn_readlane(v.hf0, i);
-  t.f0 = __builtin_amdgcn_readlane(v.f0, i);
-  t.hf1 = __builtin_amdgcn_readlane(v.hf1, i);
-  t.f1 = __builtin_amdgcn_readlane(v.f1, i);
-  return t;
-}
-
-// `bm_lane` is this lane's bitmap plane (lanes 0-7: plane 1, 8-15: plane 2,
-// 16-23: plane 3), chosen once per kernel.
-__device__ __forceinline__ void stage_issue(const Streams& s, const uint8_t* bm_lane, int g, int m,
-                                            const TileOff& o, StageRegs& r, StageMeta& mt) {
-  const int l = lane_id();
-  const int a0 = o.hf0 & ~15;
-  const int nch = min((o.hf1 - a0 + 15) >> 4, 65);
-  const int fa0 = o.f0 & ~7;
-  const int nfc = (o.f1 - fa0 + 7) >> 3;
-  mt.sm_rel = o.hf0 - a0;
-  mt.full_rel = o.f0 - fa0;
-  mt.fa0 = fa0;
-  mt.full_direct = nfc > kFullChunks;
-  // Every lane issues exactly two 16-byte loads (addresses clamped to valid
-  // data when the lane has nothing to fetch) so the number of loads in flight
-  // is the same on every path and the waits stay precise.
-  r.sm = *reinterpret_cast<const u32x4*>(s.sm + a0 + (l < nch ? 16 * l : 0));
-  const uint8_t* mp = bm_lane + 512 * g + 128 * m + 16 * (l & 7);
-  if (l >= 24) {
-    if (l < 24 + kFullChunks) {
-      if (l - 24 < nfc && nfc <= kFullChunks)
-        mp = reinterpret_cast<const uint8_t*>(s.full + fa0 + 8 * (l - 24));
-    } else if (l == 24 + kFullChunks && nch > 64) {
-      mp = s.sm + a0 + 1024;
-    }
-  }
-  r.misc = *reinterpret_cast<const u32x4*>(mp);
-}
-
-__device__ __forceinline__ void stage_write(uint8_t* st, const StageRegs& r) {
-  const int l = lane_id();
-  *reinterpret_cast<u32x4*>(st + kStSm + 16 * l) = r.sm;
-  if (l < 24)
-    *reinterpret_cast<u32x4*>(st + kStBm + 16 * l) = r.misc;
-  else if (l < 24 + kFullChunks)
-    *reinterpret_cast<u32x4*>(st + kStFull + 16 * (l - 24)) = r.misc;
-  else if (l == 24 + kFullChunks)
-    *reinterpret_cast<u32x4*>(st + kStSm + 1024) = r.misc;
-}
-
 template <int NB, int WAVES>
 struct GemmSmem {
   static constexpr int kMain = (int)sizeof(DecodeTables) + WAVES * 3 * kStBytes;
@@ -233,7 +140,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(Streams s, int start_e
     if constexpr (!kXRing) ZS_LOADX(min((J) + 1, last), xn);                             \
     if ((J) < n) {                                                                       \
       u32x4 a0_, a1_;                                                                    \
-      decode_median_pair(T, CUR + kStBm, 128, CUR + kStSm, cm_.sm_rel,                   \
+      decode_median_pair(T, T.e1, CUR + kStBm, 128, CUR + kStSm, cm_.sm_rel,                   \
                          reinterpret_cast<const uint16_t*>(CUR + kStFull), cm_.full_rel, \
                          cm_.full_direct, s.full + cm_.fa0, a0_, a1_);                   \
       _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                             \
@@ -441,7 +348,7 @@ __global__ __launch_bounds__(256) void gemm64_kernel(Streams s, int start_exp, c
       const int msm_ = __builtin_amdgcn_readlane(offs.msm, (J));                         \
       const int mf_ = __builtin_amdgcn_readlane(offs.mf, (J));                           \
       u32x4 a0_, a1_;                                                                    \
-      decode_median_pair(T, CUR + kGtBm + 128 * w, 512, CUR + kGtSm, msm_,               \
+      decode_median_pair(T, T.e1, CUR + kGtBm + 128 * w, 512, CUR + kGtSm, msm_,               \
                          reinterpret_cast<const uint16_t*>(CUR + kGtFull), mf_,          \
                          cm_.full_direct, s.full + cm_.fg0, a0_, a1_);                   \
       _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                             \
