@@ -158,6 +158,51 @@ int zs_init_bf16_matrix_triple_bitmap_gpu(
     int32_t* d_max_full_count, int32_t* d_total_hf, int32_t* d_total_full);
 
 /* ---------------------------------------------------------------------- */
+/* CDNA4 re-tiled layout (this library's device layout; no counterpart in   */
+/* the reference).  A lossless rearrangement of the canonical streams with  */
+/* the same size: one fixed 1408-byte record per 16x64 tile (record r =     */
+/* band * K/64 + kt) holding every element's sign|mantissa byte and the    */
+/* three code bit-planes in MFMA-lane order, plus a stream of outlier       */
+/* exponent bytes ((exponent - start_exp) mod 256) with num_records + 1    */
+/* int32 cumulative offsets.  `fixed` and `exps` must be 16-byte aligned    */
+/* and `exps` must keep ZS_STREAM_SLACK_BYTES readable bytes past its end.  */
+/* ---------------------------------------------------------------------- */
+int64_t zs_retiled_num_records(int M, int K);
+int64_t zs_retiled_fixed_bytes(int M, int K);
+/* bf16 -> re-tiled, two phases: count + scan (d_counts: num_records int32,
+ * d_eoff: num_records + 1, d_total: 1 int64 = number of outlier bytes),
+ * then emit once the caller has sized d_exps.  d_top_exponents is the window
+ * from zs_analyze_top_exponents_gpu (start_exp = top[0] - 1). */
+int zs_compress_retiled_count_gpu(void* stream, const uint16_t* d_input, int M, int K,
+                                  const int32_t* d_top_exponents, int32_t* d_counts,
+                                  int32_t* d_eoff, int64_t* d_total);
+int zs_compress_retiled_emit_gpu(void* stream, const uint16_t* d_input, int M, int K,
+                                 const int32_t* d_top_exponents, const int32_t* d_eoff,
+                                 uint8_t* d_fixed, uint8_t* d_exps);
+/* Canonical TCA-TBE streams -> re-tiled, same two phases (window start_exp). */
+int zs_retile_triple_bitmap_count_gpu(void* stream, const uint8_t* SignMantissa,
+                                      const uint16_t* CompressedFull, const uint64_t* Bitmap1,
+                                      const uint64_t* Bitmap2, const uint64_t* Bitmap3,
+                                      const int32_t* TileOffsets_Median,
+                                      const int32_t* TileOffsets_Global, int M, int K,
+                                      int32_t* d_counts, int32_t* d_eoff, int64_t* d_total);
+int zs_retile_triple_bitmap_emit_gpu(void* stream, const uint8_t* SignMantissa,
+                                     const uint16_t* CompressedFull, const uint64_t* Bitmap1,
+                                     const uint64_t* Bitmap2, const uint64_t* Bitmap3,
+                                     const int32_t* TileOffsets_Median,
+                                     const int32_t* TileOffsets_Global, uint8_t start_exp, int M,
+                                     int K, const int32_t* d_eoff, uint8_t* d_fixed,
+                                     uint8_t* d_exps);
+/* Decompress / ZipGEMM over the re-tiled layout: same results as
+ * zs_bf16_triple_bitmap_decompress / zs_bf16_triple_bitmap_mm on the
+ * canonical streams it was built from (same split-K semantics). */
+int zs_retiled_decompress(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
+                          const int32_t* d_eoff, uint8_t start_exp, uint16_t* out, int M, int K);
+int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
+                  const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B, uint16_t* C, int M,
+                  int N, int K, uint16_t* Reduction_Workspace, int Split_K);
+
+/* ---------------------------------------------------------------------- */
 /* Decode attention over a compressed KV cache                              */
 /* ---------------------------------------------------------------------- */
 

@@ -53,6 +53,9 @@ def lib():
         L.zso_gemm_splitk_bf16.argtypes = [p, p, C.c_int, C.c_int, C.c_int, C.c_int, p]
         L.zso_decode_attention_f64.argtypes = [p, p, p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                                p, C.c_double, p, p]
+        L.zso_compress_retiled.restype = C.c_int64
+        L.zso_compress_retiled.argtypes = [p, C.c_int, C.c_int, C.c_int, p, p, p]
+        L.zso_decompress_retiled.argtypes = [p, p, p, C.c_int, C.c_int, C.c_int, p]
         _lib = L
     return _lib
 
@@ -247,3 +250,46 @@ def decode_attention_f64(q, k, v, seqlens=None, scale=None):
     lib().zso_decode_attention_f64(_ptr(q), _ptr(k), _ptr(v), B, H, Hkv, T, D,
                                    None if sl is None else _ptr(sl), float(scale), _ptr(out), _ptr(lse))
     return out, lse
+
+
+REC_BYTES = 1408
+
+
+@dataclass
+class Retiled:
+    """This build's CDNA4 re-tiled layout (no reference counterpart): fixed
+    1408-byte records per 16x64 tile + outlier exponent stream."""
+    fixed: np.ndarray   # uint8 [num_records * 1408]
+    exps: np.ndarray    # uint8 [num_outliers]
+    eoff: np.ndarray    # int32 [num_records + 1]
+    start_exp: int
+    rows: int
+    cols: int
+
+    def compressed_bytes(self) -> int:
+        return self.fixed.size + self.exps.size + 4 * self.eoff.size
+
+
+def compress_retiled(a: np.ndarray, start_exp: int) -> Retiled:
+    """bf16 [M, K] -> re-tiled layout under window start `start_exp`."""
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    M, K = a.shape
+    nrec = (M // 16) * (K // 64)
+    fixed = np.zeros(nrec * REC_BYTES, np.uint8)
+    exps = np.zeros(M * K, np.uint8)
+    eoff = np.zeros(nrec + 1, np.int32)
+    n = lib().zso_compress_retiled(_ptr(a), M, K, int(start_exp), _ptr(fixed), _ptr(exps), _ptr(eoff))
+    return Retiled(fixed, exps[:n].copy(), eoff, int(start_exp) & 0xFF, M, K)
+
+
+def retile(e: Encoded) -> Retiled:
+    """Canonical streams -> re-tiled layout (decode, then re-pack under the same window)."""
+    return compress_retiled(decompress(e), e.start_exp)
+
+
+def decompress_retiled(r: Retiled) -> np.ndarray:
+    out = np.zeros((r.rows, r.cols), np.uint16)
+    ex = np.ascontiguousarray(r.exps) if r.exps.size else np.zeros(1, np.uint8)
+    lib().zso_decompress_retiled(_ptr(r.fixed), _ptr(ex), _ptr(r.eoff), r.start_exp, r.rows,
+                                 r.cols, _ptr(out))
+    return out

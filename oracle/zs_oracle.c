@@ -600,3 +600,76 @@ void zso_decode_attention_f64(const uint16_t* q, const uint16_t* k, const uint16
         }
     free(s);
 }
+
+/* ------------------------------------------------------------------------ */
+/* Re-tiled device layout (see zs_oracle.h).                                 */
+/* ------------------------------------------------------------------------ */
+static inline int64_t zso_rec_elem(int M, int K, int64_t r, int h, int l, int i, int* row, int* col) {
+    const int KT = K / 64;
+    const int64_t band = r / KT, kt = r % KT;
+    (void)M;
+    *row = (int)(band * 16 + (l & 15));
+    *col = (int)(kt * 64 + 32 * h + 8 * (l >> 4) + i);
+    return (int64_t)(*row) * K + *col;
+}
+
+int64_t zso_compress_retiled(const uint16_t* a, int M, int K, int start_exp, uint8_t* fixed,
+                             uint8_t* exps, int32_t* eoff) {
+    const int64_t nrec = (int64_t)(M / 16) * (K / 64);
+    int64_t nout = 0;
+    const unsigned st = (unsigned)start_exp & 0xFFu;
+    eoff[0] = 0;
+    for (int64_t r = 0; r < nrec; ++r) {
+        uint8_t* f = fixed + r * ZSO_REC_BYTES;
+        unsigned B[64][2][3];
+        memset(B, 0, sizeof(B));
+        for (int h = 0; h < 2; ++h)          /* outliers in (h, l, i) order */
+            for (int l = 0; l < 64; ++l)
+                for (int i = 0; i < 8; ++i) {
+                    int row, col;
+                    const uint16_t v = a[zso_rec_elem(M, K, r, h, l, i, &row, &col)];
+                    const unsigned e = (v >> 7) & 0xFFu;
+                    const unsigned d = (e - st) & 0xFFu;
+                    const unsigned code = (d >= 1 && d <= 7) ? d : 0;
+                    f[16 * l + 8 * h + i] = (uint8_t)(((v >> 8) & 0x80u) | (v & 0x7Fu));
+                    for (int p = 0; p < 3; ++p) B[l][h][p] |= ((code >> p) & 1u) << i;
+                    if (code == 0) exps[nout++] = (uint8_t)d;
+                }
+        for (int l = 0; l < 64; ++l) {
+            const uint32_t w32 = B[l][0][0] | (B[l][0][1] << 8) | (B[l][0][2] << 16) | (B[l][1][0] << 24);
+            const uint16_t w16 = (uint16_t)(B[l][1][1] | (B[l][1][2] << 8));
+            memcpy(f + 1024 + 4 * l, &w32, 4);
+            memcpy(f + 1280 + 2 * l, &w16, 2);
+        }
+        eoff[r + 1] = (int32_t)nout;
+    }
+    return nout;
+}
+
+void zso_decompress_retiled(const uint8_t* fixed, const uint8_t* exps, const int32_t* eoff,
+                            int start_exp, int M, int K, uint16_t* out) {
+    const int64_t nrec = (int64_t)(M / 16) * (K / 64);
+    const unsigned st = (unsigned)start_exp & 0xFFu;
+    for (int64_t r = 0; r < nrec; ++r) {
+        const uint8_t* f = fixed + r * ZSO_REC_BYTES;
+        int64_t k = eoff[r];
+        for (int h = 0; h < 2; ++h)
+            for (int l = 0; l < 64; ++l) {
+                uint32_t w32;
+                uint16_t w16;
+                memcpy(&w32, f + 1024 + 4 * l, 4);
+                memcpy(&w16, f + 1280 + 2 * l, 2);
+                const unsigned b1 = h ? (w32 >> 24) : (w32 & 0xFFu);
+                const unsigned b2 = h ? (w16 & 0xFFu) : ((w32 >> 8) & 0xFFu);
+                const unsigned b3 = h ? (unsigned)(w16 >> 8) : ((w32 >> 16) & 0xFFu);
+                for (int i = 0; i < 8; ++i) {
+                    const unsigned code = ((b1 >> i) & 1u) | (((b2 >> i) & 1u) << 1) | (((b3 >> i) & 1u) << 2);
+                    const unsigned s = f[16 * l + 8 * h + i];
+                    const unsigned e = code ? ((st + code) & 0xFFu) : ((st + exps[k++]) & 0xFFu);
+                    int row, col;
+                    out[zso_rec_elem(M, K, r, h, l, i, &row, &col)] =
+                        (uint16_t)(((s & 0x80u) << 8) | (e << 7) | (s & 0x7Fu));
+                }
+            }
+    }
+}

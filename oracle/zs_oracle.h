@@ -92,3 +92,26 @@ void zso_decode_attention_f64(const uint16_t* q, const uint16_t* k, const uint16
 }
 #endif
 #endif
+
+/* ------------------------------------------------------------------------ */
+/* CDNA4 re-tiled device layout (this build's own layout; no counterpart in  */
+/* the reference).  A lossless rearrangement of the canonical streams:       */
+/* record r = band*(K/64) + kt covers rows 16*band..+15, cols 64*kt..+63.    */
+/* Element (h, l, i) of a record (half h < 2, lane l < 64, i < 8) is row     */
+/* 16*band + l%16, col 64*kt + 32*h + 8*(l/16) + i.  Fixed part, 1408 B per  */
+/* record: byte 16*l + 8*h + i = sign|mantissa byte of (h,l,i); bytes        */
+/* 1024 + 4*l.. = u32 (B1(0,l) | B2(0,l)<<8 | B3(0,l)<<16 | B1(1,l)<<24);    */
+/* bytes 1280 + 2*l.. = u16 (B2(1,l) | B3(1,l)<<8), Bp(h,l) bit i = bit p-1  */
+/* of the 3-bit code of (h,l,i) (0 = outlier, else exponent start+code).     */
+/* Exponent stream: for each outlier, in (h, l, i) order, the byte           */
+/* (exponent - start_exp) mod 256, at exps[eoff[r] + k]; eoff has           */
+/* num_records + 1 cumulative entries.                                       */
+/* ------------------------------------------------------------------------ */
+#define ZSO_REC_BYTES 1408
+/* bf16 -> re-tiled layout for window start `start_exp` (in-window iff
+ * (exponent - start_exp) mod 256 in 1..7, the canonical rule for the
+ * contiguous window top[i] = start_exp + 1 + i). Returns the outlier count. */
+int64_t zso_compress_retiled(const uint16_t* a, int M, int K, int start_exp, uint8_t* fixed,
+                             uint8_t* exps, int32_t* eoff);
+void zso_decompress_retiled(const uint8_t* fixed, const uint8_t* exps, const int32_t* eoff,
+                            int start_exp, int M, int K, uint16_t* out);

@@ -9,20 +9,25 @@ from ._lib import LIB_PATH, ZipServError, build, lib  # noqa: F401
 from .codec import (  # noqa: F401
     HostCompressed,
     ZipservCompressed,
+    ZipservRetiled,
     analyze_exponents,
     compress,
     compress_host,
+    compress_retiled,
     compress_zipserv,
     decompress,
+    decompress_retiled,
     decompress_zipserv,
     decompress_zipserv_into,
     make_zipserv_compressed,
+    retile,
     to_device,
     zipgemm,
 )
 
 __all__ = [
     "LIB_PATH", "ZipServError", "build", "lib", "HostCompressed", "ZipservCompressed",
+    "ZipservRetiled", "compress_retiled", "decompress_retiled", "retile",
     "analyze_exponents", "compress", "compress_host", "compress_zipserv", "decompress",
     "decompress_zipserv", "decompress_zipserv_into", "make_zipserv_compressed", "to_device",
     "zipgemm",

@@ -53,6 +53,17 @@ SIGNATURES = {
     "zs_analyze_top_exponents_gpu": (C.c_int, [_p, _p, _i64, _p, _p, _p]),
     "zs_init_bf16_matrix_triple_bitmap_gpu": (
         C.c_int, [_p, _p, C.c_int, C.c_int, _p] + [_p] * 8 + [_p] * 2 + [_p] * 4 + [_p] * 4),
+    "zs_retiled_num_records": (C.c_int64, [C.c_int, C.c_int]),
+    "zs_retiled_fixed_bytes": (C.c_int64, [C.c_int, C.c_int]),
+    "zs_compress_retiled_count_gpu": (C.c_int, [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p]),
+    "zs_compress_retiled_emit_gpu": (C.c_int, [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p]),
+    "zs_retile_triple_bitmap_count_gpu": (
+        C.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, C.c_int, C.c_int, _p, _p, _p]),
+    "zs_retile_triple_bitmap_emit_gpu": (
+        C.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, C.c_uint8, C.c_int, C.c_int, _p, _p, _p]),
+    "zs_retiled_decompress": (C.c_int, [_p, _p, _p, _p, C.c_uint8, _p, C.c_int, C.c_int]),
+    "zs_retiled_mm": (C.c_int, [_p, _p, _p, _p, C.c_uint8, _p, _p, C.c_int, C.c_int, C.c_int,
+                                _p, C.c_int]),
     "zs_decode_attention": (
         C.c_int, [_p, _p, _p, _p, _p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                   _p, _p, _p, C.c_size_t, C.c_int]),

@@ -190,6 +190,10 @@ class ZipservCompressed:
     tile_offsets: object = None
     layout: str = "by_kv_head"
 
+    @property
+    def device(self):
+        return self.sign_mantissa.device
+
     def ratio(self) -> float:
         return 2.0 * self.rows * self.cols / self.compressed_bytes
 
@@ -349,16 +353,126 @@ def decompress(c: ZipservCompressed, out=None):
                                    c.max_full_count, c.start_exp)
 
 
-def splitk_workspace(c: ZipservCompressed, n: int, split_k: int):
+def splitk_workspace(c, n: int, split_k: int):
     torch = _torch()
     nbytes = int(lib().zs_splitk_workspace_bytes(c.rows, n, split_k))
     if nbytes == 0:
         return None
-    return torch.empty(nbytes // 2, dtype=torch.bfloat16, device=c.sign_mantissa.device)
+    return torch.empty(nbytes // 2, dtype=torch.bfloat16, device=c.device)
 
 
-def zipgemm(c: ZipservCompressed, x, split_k: int = 1, out=None, workspace=None):
-    """Y[N, M] = X[N, K] . W[M, K]^T (build/L_API.cuh:19-37 BF16TripleBitmap_MM_API)."""
+# ---------------------------------------------------------------------------
+# CDNA4 re-tiled layout (the library's device layout; see include/zipserv.h)
+# ---------------------------------------------------------------------------
+@dataclass
+class ZipservRetiled:
+    """Device-resident re-tiled matrix: fixed 1408-byte records per 16x64 tile
+    (sign|mantissa bytes and code bit-planes in MFMA lane order) + outlier
+    exponent bytes with per-record offsets.  Same content and size as the
+    canonical streams, laid out for contiguous per-band streaming."""
+    fixed: object          # uint8 [num_records * 1408]
+    exps: object           # uint8 [num_outliers + slack]
+    eoff: object           # int32 [num_records + 1]
+    rows: int
+    cols: int
+    logical_rows: int
+    logical_cols: int
+    start_exp: int
+    num_outliers: int
+    compressed_bytes: int
+    layout: str = "by_kv_head"
+
+    @property
+    def device(self):
+        return self.fixed.device
+
+    def ratio(self) -> float:
+        return 2.0 * self.rows * self.cols / self.compressed_bytes
+
+
+def _retiled_alloc(rows, cols, total, dev):
+    torch = _torch()
+    nrec = rows // 16 * (cols // 64)
+    fixed = torch.empty(nrec * 1408, dtype=torch.uint8, device=dev)
+    exps = torch.zeros(int(total) + _lib.ZS_STREAM_SLACK_BYTES, dtype=torch.uint8, device=dev)
+    return fixed, exps, nrec
+
+
+def compress_retiled(input, logical_rows=None, logical_cols=None, layout="by_kv_head") -> ZipservRetiled:
+    """bf16 [rows, cols] on the GPU -> re-tiled layout (window chosen on the GPU
+    with the rule of zipserv_decode_attention_ext.cu:35-135)."""
+    torch = _torch()
+    _check_cuda(input, "input", torch.bfloat16)
+    if input.dim() != 2:
+        raise ValueError("input must be 2D")
+    rows, cols = input.shape
+    if rows % 64 or cols % 64:
+        raise ValueError("rows and cols must be padded to multiples of 64")
+    L = lib()
+    dev = input.device
+    i32 = dict(dtype=torch.int32, device=dev)
+    nrec = rows // 16 * (cols // 64)
+    top, counts, done = torch.empty(7, **i32), torch.empty(256, **i32), torch.empty(4, **i32)
+    cnt, eoff = torch.empty(nrec, **i32), torch.empty(nrec + 1, **i32)
+    total = torch.empty(1, dtype=torch.int64, device=dev)
+    st = _stream()
+    check("zs_analyze_top_exponents_gpu",
+          L.zs_analyze_top_exponents_gpu(st, _dptr(input), rows * cols, _dptr(counts), _dptr(top),
+                                         _dptr(done)))
+    check("zs_compress_retiled_count_gpu",
+          L.zs_compress_retiled_count_gpu(st, _dptr(input), rows, cols, _dptr(top), _dptr(cnt),
+                                          _dptr(eoff), _dptr(total)))
+    tot, top0 = int(total.item()), int(top[0].item())  # synchronises (sizes the stream)
+    if tot > 2**31 - 1:
+        raise OverflowError("outlier count exceeds the int32 offsets")
+    fixed, exps, _ = _retiled_alloc(rows, cols, tot, dev)
+    check("zs_compress_retiled_emit_gpu",
+          L.zs_compress_retiled_emit_gpu(st, _dptr(input), rows, cols, _dptr(top), _dptr(eoff),
+                                         _dptr(fixed), _dptr(exps)))
+    return ZipservRetiled(fixed, exps, eoff, rows, cols,
+                          rows if logical_rows is None else logical_rows,
+                          cols if logical_cols is None else logical_cols,
+                          (top0 - 1) & 0xFF, tot, nrec * 1408 + tot + 4 * (nrec + 1), layout)
+
+
+def retile(c: ZipservCompressed) -> ZipservRetiled:
+    """Canonical device streams -> re-tiled layout (same window, same bytes as
+    compress_retiled under that window)."""
+    torch = _torch()
+    L = lib()
+    dev = c.sign_mantissa.device
+    i32 = dict(dtype=torch.int32, device=dev)
+    nrec = c.rows // 16 * (c.cols // 64)
+    cnt, eoff = torch.empty(nrec, **i32), torch.empty(nrec + 1, **i32)
+    total = torch.empty(1, dtype=torch.int64, device=dev)
+    st = _stream()
+    ptrs = [_dptr(t) for t in c.streams()]
+    check("zs_retile_triple_bitmap_count_gpu",
+          L.zs_retile_triple_bitmap_count_gpu(st, *ptrs, c.rows, c.cols, _dptr(cnt), _dptr(eoff),
+                                              _dptr(total)))
+    tot = int(total.item())
+    fixed, exps, _ = _retiled_alloc(c.rows, c.cols, tot, dev)
+    check("zs_retile_triple_bitmap_emit_gpu",
+          L.zs_retile_triple_bitmap_emit_gpu(st, *ptrs, c.start_exp & 0xFF, c.rows, c.cols,
+                                             _dptr(eoff), _dptr(fixed), _dptr(exps)))
+    return ZipservRetiled(fixed, exps, eoff, c.rows, c.cols, c.logical_rows, c.logical_cols,
+                          c.start_exp & 0xFF, tot, nrec * 1408 + tot + 4 * (nrec + 1), c.layout)
+
+
+def decompress_retiled(r: ZipservRetiled, out=None):
+    torch = _torch()
+    if out is None:
+        out = torch.empty((r.rows, r.cols), dtype=torch.bfloat16, device=r.device)
+    _check_cuda(out, "out", torch.bfloat16)
+    check("zs_retiled_decompress",
+          lib().zs_retiled_decompress(_stream(), _dptr(r.fixed), _dptr(r.exps), _dptr(r.eoff),
+                                      r.start_exp & 0xFF, _dptr(out), r.rows, r.cols))
+    return out
+
+
+def zipgemm(c, x, split_k: int = 1, out=None, workspace=None):
+    """Y[N, M] = X[N, K] . W[M, K]^T (build/L_API.cuh:19-37 BF16TripleBitmap_MM_API).
+    `c` is a ZipservCompressed (canonical streams) or a ZipservRetiled."""
     torch = _torch()
     _check_cuda(x, "x", torch.bfloat16)
     if x.dim() != 2 or x.shape[1] != c.cols:
@@ -368,6 +482,12 @@ def zipgemm(c: ZipservCompressed, x, split_k: int = 1, out=None, workspace=None)
         out = torch.empty((n, c.rows), dtype=torch.bfloat16, device=x.device)
     if split_k > 1 and workspace is None:
         workspace = splitk_workspace(c, n, split_k)
+    if isinstance(c, ZipservRetiled):
+        check("zs_retiled_mm",
+              lib().zs_retiled_mm(_stream(), _dptr(c.fixed), _dptr(c.exps), _dptr(c.eoff),
+                                  c.start_exp & 0xFF, _dptr(x), _dptr(out), c.rows, n, c.cols,
+                                  _dptr(workspace), split_k))
+        return out
     check("zs_bf16_triple_bitmap_mm",
           lib().zs_bf16_triple_bitmap_mm(
               _stream(), *[_dptr(t) for t in c.streams()], c.max_high_freq_count,

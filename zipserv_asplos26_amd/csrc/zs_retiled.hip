@@ -1,0 +1,610 @@
+// zs_retiled.hip -- the CDNA4 re-tiled layout on gfx950: encoders (from bf16
+// and from canonical TCA-TBE streams), decompress and ZipGEMM.
+//
+// The layout (zs_rdecode.hpp) stores each 16 x 64 tile as one fixed 1408-byte
+// record whose bytes each lane loads straight into the registers it decodes
+// from (16 B sign|mantissa + 4 B + 2 B bit-planes), plus a per-record run of
+// outlier exponent bytes.  A workgroup streams consecutive records of one
+// 16-row band, so HBM sees long contiguous runs; only the outlier bytes pass
+// through LDS.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "../../include/zipserv.h"
+#include "zs_device.hpp"
+#include "zs_rdecode.hpp"
+
+namespace zs {
+
+// ---------------------------------------------------------------------------
+// Encoders.  One wave per record (grid-stride); lane l gathers its 2 x 8
+// elements (one 16-byte load per half) from the bf16 matrix.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ const uint16_t* rec_src(const uint16_t* a, int K, int64_t rec, int h) {
+  const int KT = K >> 6;
+  const int64_t band = rec / KT, kt = rec % KT;
+  const int l = lane_id();
+  return a + (band * 16 + (l & 15)) * (int64_t)K + kt * 64 + 32 * h + 8 * (l >> 4);
+}
+
+// Plane bytes of 8 elements from their exponents (window start st).
+__device__ __forceinline__ void classify8(u32x4 v, uint32_t st, uint32_t& b1, uint32_t& b2,
+                                          uint32_t& b3) {
+  b1 = b2 = b3 = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t x = (v[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+    const uint32_t d = (((x >> 7) & 0xFFu) - st) & 0xFFu;
+    const uint32_t c = (d >= 1 && d <= 7) ? d : 0u;
+    b1 |= (c & 1u) << i;
+    b2 |= ((c >> 1) & 1u) << i;
+    b3 |= ((c >> 2) & 1u) << i;
+  }
+}
+
+__device__ __forceinline__ int wave_sum(int x) {
+  const int incl = wave_inclusive_scan(x);
+  return __builtin_amdgcn_readlane(incl, 63);
+}
+
+__global__ __launch_bounds__(256) void rcount_kernel(const uint16_t* a, int M, int K,
+                                                     const int32_t* top, int32_t* counts) {
+  const uint32_t st = (uint32_t)(top[0] - 1) & 0xFFu;
+  const int64_t nrec = (int64_t)(M >> 4) * (K >> 6);
+  const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t rec = wid; rec < nrec; rec += nw) {
+    int n = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t b1, b2, b3;
+      classify8(*reinterpret_cast<const u32x4*>(rec_src(a, K, rec, h)), st, b1, b2, b3);
+      n += 8 - __builtin_popcount(b1 | b2 | b3);
+    }
+    n = wave_sum(n);
+    if (lane_id() == 0) counts[rec] = n;
+  }
+}
+
+// Same count from canonical bit-planes (record = median tile m of GT g).
+__global__ __launch_bounds__(256) void rcount_canon_kernel(Streams s, int M, int K,
+                                                           int32_t* counts) {
+  const int KT = K >> 6;
+  const int64_t nrec = (int64_t)(M >> 4) * KT;
+  const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  const int l = lane_id();
+  for (int64_t rec = wid; rec < nrec; rec += nw) {
+    const int64_t band = rec / KT, kt = rec % KT;
+    const int64_t g = (band >> 2) * KT + kt;
+    const int64_t bb = 512 * g + 128 * (band & 3) + l;
+    int n = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      n += 8 - __builtin_popcount(s.bm1[bb + 64 * h] | s.bm2[bb + 64 * h] | s.bm3[bb + 64 * h]);
+    n = wave_sum(n);
+    if (l == 0) counts[rec] = n;
+  }
+}
+
+// Exclusive scan of the per-record counts into eoff (n + 1 entries) by one
+// workgroup of 1024 threads; *total receives the sum (64-bit).
+__global__ __launch_bounds__(1024) void rscan_kernel(const int32_t* counts, int64_t n,
+                                                     int32_t* eoff, int64_t* total) {
+  __shared__ int64_t part[1024];
+  const int t = threadIdx.x;
+  const int64_t per = (n + 1023) / 1024;
+  const int64_t b = std::min<int64_t>(n, t * per), e = std::min<int64_t>(n, b + per);
+  int64_t s = 0;
+  for (int64_t i = b; i < e; ++i) s += counts[i];
+  part[t] = s;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int64_t v = t >= off ? part[t - off] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  int64_t run = part[t] - s;
+  for (int64_t i = b; i < e; ++i) {
+    eoff[i] = (int32_t)run;
+    run += counts[i];
+  }
+  if (t == 1023) {
+    eoff[n] = (int32_t)part[1023];
+    *total = part[1023];
+  }
+}
+
+// Writes one record from the lane's 16 bf16 values and plane bytes.
+__device__ __forceinline__ void emit_record(uint8_t* fixed, uint8_t* exps, int64_t rec,
+                                            int64_t ebase, uint32_t st, const u32x4 v[2],
+                                            const uint32_t b[2][3]) {
+  const int l = lane_id();
+  u32x4 sm;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t x = (v[h][(4 * q + j) >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+        w |= (((x >> 8) & 0x80u) | (x & 0x7Fu)) << (8 * j);
+      }
+      sm[2 * h + q] = w;
+    }
+  const uint32_t p32 = b[0][0] | (b[0][1] << 8) | (b[0][2] << 16) | (b[1][0] << 24);
+  const uint32_t p16 = b[1][1] | (b[1][2] << 8);
+  uint8_t* f = fixed + rec * kRecBytes;
+  *reinterpret_cast<u32x4*>(f + 16 * l) = sm;
+  *reinterpret_cast<uint32_t*>(f + kRecP32 + 4 * l) = p32;
+  *reinterpret_cast<uint16_t*>(f + kRecP16 + 2 * l) = (uint16_t)p16;
+  int rank0, rank1;
+  r_ranks(p32, p16, rank0, rank1);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint32_t fm = ~(b[h][0] | b[h][1] | b[h][2]) & 0xFFu;
+    int64_t o = ebase + (h ? rank1 : rank0);
+    while (fm) {
+      const int i = __builtin_ctz(fm);
+      fm &= fm - 1;
+      const uint32_t x = (v[h][i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+      exps[o++] = (uint8_t)((((x >> 7) & 0xFFu) - st) & 0xFFu);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void remit_kernel(const uint16_t* a, int M, int K,
+                                                    const int32_t* top, const int32_t* eoff,
+                                                    uint8_t* fixed, uint8_t* exps) {
+  const uint32_t st = (uint32_t)(top[0] - 1) & 0xFFu;
+  const int64_t nrec = (int64_t)(M >> 4) * (K >> 6);
+  const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t rec = wid; rec < nrec; rec += nw) {
+    u32x4 v[2];
+    uint32_t b[2][3];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v[h] = *reinterpret_cast<const u32x4*>(rec_src(a, K, rec, h));
+      classify8(v[h], st, b[h][0], b[h][1], b[h][2]);
+    }
+    emit_record(fixed, exps, rec, eoff[rec], st, v, b);
+  }
+}
+
+// From canonical streams: each median tile is decoded (global-memory decoder,
+// bit-exact) and re-packed; its plane bytes are the canonical bitmap bytes.
+__global__ __launch_bounds__(256) void remit_canon_kernel(Streams s, int start_exp, int M, int K,
+                                                          const int32_t* eoff, uint8_t* fixed,
+                                                          uint8_t* exps) {
+  __shared__ DecodeTables T;
+  build_decode_tables(T, start_exp, threadIdx.x, blockDim.x);
+  __syncthreads();
+  const int KT = K >> 6;
+  const int64_t nrec = (int64_t)(M >> 4) * KT;
+  const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t rec = wid; rec < nrec; rec += nw) {
+    const int64_t band = rec / KT, kt = rec % KT;
+    const int64_t g = (band >> 2) * KT + kt;
+    const int m = (int)(band & 3);
+    int64_t smb = (int64_t)s.tog[2 * g] + s.tom[2 * (4 * g + m)];
+    int64_t fb = (int64_t)s.tog[2 * g + 1] + s.tom[2 * (4 * g + m) + 1];
+    u32x4 v[2];
+    uint32_t b[2][3];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      int tot;
+      const RowRef r = load_half_median(s, 512 * g + 128 * m + 64 * h, smb, fb, tot);
+      v[h] = decode_row(s, T, r);
+      b[h][0] = r.b1;
+      b[h][1] = r.b2;
+      b[h][2] = r.b3;
+      smb += tot;
+      fb += 512 - tot;
+    }
+    emit_record(fixed, exps, rec, eoff[rec], (uint32_t)start_exp & 0xFFu, v, b);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Record fetch: the fixed part straight into registers, the outlier bytes as
+// up to 64 16-byte chunks (lane l: chunk l) bound for a wave-private LDS stage.
+// A record with more than 64 chunks of outliers is decoded from global memory.
+// ---------------------------------------------------------------------------
+struct RStage {
+  RecRegs r;
+  u32x4 ex;
+};
+struct RMeta {
+  int e0;    // first outlier byte of the record (stream offset)
+  int rel;   // e0 - first staged byte
+  int nch;   // staged chunks (> kExpChunks: decode from global memory)
+};
+
+__device__ __forceinline__ void r_issue(const uint8_t* fixed, const uint8_t* exps, int64_t rec,
+                                        int e0, int e1, RStage& s, RMeta& mt) {
+  const int l = lane_id();
+  const uint8_t* f = fixed + rec * kRecBytes;
+  s.r.sm = *reinterpret_cast<const u32x4*>(f + 16 * l);
+  s.r.p32 = *reinterpret_cast<const uint32_t*>(f + kRecP32 + 4 * l);
+  s.r.p16 = *reinterpret_cast<const uint16_t*>(f + kRecP16 + 2 * l);
+  const int ea0 = e0 & ~15;
+  const int nch = (e1 - ea0 + 15) >> 4;
+  mt.e0 = e0;
+  mt.rel = e0 - ea0;
+  mt.nch = nch;
+  s.ex = *reinterpret_cast<const u32x4*>(exps + ea0 + (l < nch ? 16 * l : 0));
+}
+
+__device__ __forceinline__ void r_stage(uint8_t* st, const RStage& s, const RMeta& mt) {
+  const int l = lane_id();
+  if (l < mt.nch) *reinterpret_cast<u32x4*>(st + 16 * l) = s.ex;
+}
+
+__device__ __forceinline__ void r_decode_staged(const RTables& T, const RStage& s,
+                                                const RMeta& mt, const uint8_t* st,
+                                                const uint8_t* exps, u32x4& o0, u32x4& o1) {
+  if (mt.nch <= kExpChunks)
+    r_decode(T, T.e1, s.r, st, mt.rel, o0, o1);
+  else
+    r_decode(T, T.e1, s.r, exps + mt.e0, 0, o0, o1);
+}
+
+// ---------------------------------------------------------------------------
+// Decompress: 4 waves per workgroup, one record per wave step (grid-stride).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rdecompress_kernel(const uint8_t* fixed,
+                                                          const uint8_t* exps,
+                                                          const int32_t* eoff, int start_exp,
+                                                          uint16_t* out, int M, int K) {
+  __shared__ RTables T;
+  __shared__ __attribute__((aligned(16))) uint8_t stg[4][kExpStage];
+  build_r_tables(T, start_exp, threadIdx.x, blockDim.x);
+  __syncthreads();
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = lane_id();
+  const int KT = K >> 6;
+  const int64_t nrec = (int64_t)(M >> 4) * KT;
+  for (int64_t rec = (int64_t)blockIdx.x * 4 + w; rec < nrec; rec += (int64_t)gridDim.x * 4) {
+    RStage s;
+    RMeta mt;
+    r_issue(fixed, exps, rec, eoff[rec], eoff[rec + 1], s, mt);
+    r_stage(stg[w], s, mt);
+    u32x4 o0, o1;
+    r_decode_staged(T, s, mt, stg[w], exps, o0, o1);
+    const int64_t band = rec / KT, kt = rec % KT;
+    uint16_t* dst = out + (band * 16 + (l & 15)) * (int64_t)K + kt * 64 + 8 * (l >> 4);
+    *reinterpret_cast<u32x4*>(dst) = o0;
+    *reinterpret_cast<u32x4*>(dst + 32) = o1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// ZipGEMM over the re-tiled layout.  Workgroup = WAVES waves on one 16-row
+// band x one split-K slice x 16*NB output columns; wave w takes K tiles
+// kb0+w, kb0+w+WAVES, ...  Records are fetched three tiles ahead into a
+// register ring, their outlier bytes staged one tile ahead.
+// ---------------------------------------------------------------------------
+template <int NB, int WAVES>
+struct RGemmSmem {
+  static constexpr int kMain = (int)sizeof(RTables) + WAVES * 3 * kExpStage;
+  static constexpr int kRed = (WAVES / 2) * NB * 64 * 16;
+  static constexpr int kBytes = kMain > kRed ? kMain : kRed;
+};
+
+template <int NB, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
+                                                           const uint8_t* exps,
+                                                           const int32_t* eoff, int start_exp,
+                                                           const uint16_t* X, uint16_t* Y, int M,
+                                                           int N, int K, int kb_per_split) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[RGemmSmem<NB, WAVES>::kBytes];
+  RTables& T = *reinterpret_cast<RTables*>(smem);
+  build_r_tables(T, start_exp, threadIdx.x, blockDim.x);
+  __syncthreads();
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = lane_id();
+  uint8_t* stage0 = smem + sizeof(RTables) + w * 3 * kExpStage;
+  uint8_t* stage1 = stage0 + kExpStage;
+  uint8_t* stage2 = stage1 + kExpStage;
+  const int band = blockIdx.x;
+  const int split = blockIdx.y;
+  const int n0 = blockIdx.z * NB * 16;
+  const int KT = K >> 6;
+  const int kb0 = split * kb_per_split;
+  const int kb1 = min(kb0 + kb_per_split, KT);
+  const int cnt = kb1 - kb0 > w ? (kb1 - kb0 - w + WAVES - 1) / WAVES : 0;
+  const int64_t rec0 = (int64_t)band * KT + kb0 + w;  // record of this wave's tile 0
+
+  const uint16_t* xrow[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int n = min(n0 + nb * 16 + (l & 15), N - 1);
+    xrow[nb] = X + (int64_t)n * K + 8 * (l >> 4);
+  }
+  f32x4 acc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int c0 = 0; c0 < cnt; c0 += 64) {
+    const int n = min(cnt - c0, 64);
+    const int last = n - 1;
+    // lane i: outlier offsets of tile c0 + i (clamped to the chunk)
+    const int64_t ri = rec0 + (int64_t)(c0 + min(l, last)) * WAVES;
+    const int oe0 = eoff[ri], oe1 = eoff[ri + 1];
+    constexpr bool kXRing = NB <= 2;
+    RStage R0, R1, R2;
+    RMeta M0, M1, M2;
+    bf16x8 X0[2][NB], X1[2][NB], X2[2][NB], xc[2][NB], xn[2][NB];
+#define RZ_LOADX(J, DST)                                                            \
+  {                                                                                 \
+    const int kk_ = (kb0 + w + (c0 + (J)) * WAVES) * 64;                            \
+    _Pragma("unroll") for (int h_ = 0; h_ < 2; ++h_)                                \
+      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_)                          \
+        DST[h_][nb_] = *reinterpret_cast<const bf16x8*>(xrow[nb_] + kk_ + 32 * h_); \
+  }
+#define RZ_ISSUE(J, R, MT, XD)                                                      \
+  {                                                                                 \
+    const int j_ = (J);                                                             \
+    r_issue(fixed, exps, rec0 + (int64_t)(c0 + j_) * WAVES,                         \
+            __builtin_amdgcn_readlane(oe0, j_), __builtin_amdgcn_readlane(oe1, j_), \
+            R, MT);                                                                 \
+    if constexpr (kXRing) RZ_LOADX(j_, XD);                                         \
+  }
+#define RZ_STEP(J, CUR, NXT, RC, MC, XC, RN, MN)                                         \
+  {                                                                                      \
+    const RStage cs_ = RC;                                                               \
+    const RMeta cm_ = MC;                                                                \
+    _Pragma("unroll") for (int h_ = 0; h_ < 2; ++h_)                                     \
+      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_)                               \
+        xc[h_][nb_] = kXRing ? XC[h_][nb_] : xn[h_][nb_];                                \
+    r_stage(NXT, RN, MN);                                                                \
+    RZ_ISSUE(min((J) + 3, last), RC, MC, XC);                                            \
+    if constexpr (!kXRing) RZ_LOADX(min((J) + 1, last), xn);                             \
+    if ((J) < n) {                                                                       \
+      u32x4 a0_, a1_;                                                                    \
+      r_decode_staged(T, cs_, cm_, CUR, exps, a0_, a1_);                                 \
+      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                             \
+        acc[nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0_), xc[0][nb_],   \
+                                                           acc[nb_], 0, 0, 0);           \
+        acc[nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1_), xc[1][nb_],   \
+                                                           acc[nb_], 0, 0, 0);           \
+      }                                                                                  \
+    }                                                                                    \
+  }
+    RZ_ISSUE(0, R0, M0, X0);
+    RZ_ISSUE(min(1, last), R1, M1, X1);
+    RZ_ISSUE(min(2, last), R2, M2, X2);
+    if constexpr (!kXRing) RZ_LOADX(0, xn);
+    r_stage(stage0, R0, M0);
+    for (int j = 0; j < n; j += 3) {
+      RZ_STEP(j, stage0, stage1, R0, M0, X0, R1, M1);
+      RZ_STEP(j + 1, stage1, stage2, R1, M1, X1, R2, M2);
+      RZ_STEP(j + 2, stage2, stage0, R2, M2, X2, R0, M0);
+    }
+#undef RZ_STEP
+#undef RZ_ISSUE
+#undef RZ_LOADX
+  }
+
+  // Deterministic tree reduction of the WAVES partial accumulators in LDS.
+  __syncthreads();
+  f32x4* red = reinterpret_cast<f32x4*>(smem);
+#pragma unroll
+  for (int half = WAVES / 2; half >= 1; half /= 2) {
+    if (w >= half && w < 2 * half) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) red[((w - half) * NB + nb) * 64 + l] = acc[nb];
+    }
+    __syncthreads();
+    if (w < half) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[nb] += red[(w * NB + nb) * 64 + l];
+    }
+    __syncthreads();
+  }
+  if (w == 0) {
+    uint16_t* out = Y + (int64_t)split * M * N;
+    const int mrow = band * 16 + 4 * (l >> 4);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const f32x4 v = acc[nb];
+      const int n = n0 + nb * 16 + (l & 15);
+      if (n < N) {
+        const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+        const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
+        *reinterpret_cast<uint2*>(out + (int64_t)n * M + mrow) = make_uint2(lo, hi);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void rsplitk_reduce_kernel(uint16_t* C, const uint16_t* WS,
+                                                             int64_t mn, int split_k) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i >= mn) return;
+  if (i + 8 <= mn) {
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < split_k; ++k) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(WS + k * mn + i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        s[2 * j] += bf16_bits_to_f32(v[j] & 0xFFFFu);
+        s[2 * j + 1] += bf16_bits_to_f32(v[j] >> 16);
+      }
+    }
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = f32_to_bf16_bits(s[2 * j]) | (f32_to_bf16_bits(s[2 * j + 1]) << 16);
+    *reinterpret_cast<u32x4*>(C + i) = o;
+  } else {
+    for (int64_t e = i; e < mn; ++e) {
+      float s = 0.f;
+      for (int k = 0; k < split_k; ++k) s += bf16_bits_to_f32(WS[k * mn + e]);
+      C[e] = (uint16_t)f32_to_bf16_bits(s);
+    }
+  }
+}
+
+static int r_grid(int64_t nrec, int waves_per_block) {
+  const int64_t blocks = (nrec + waves_per_block - 1) / waves_per_block;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, 256 * 64));
+}
+
+template <int NB>
+static hipError_t launch_rgemm(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
+                               const int32_t* eoff, int start_exp, const uint16_t* X,
+                               uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split) {
+  constexpr int kWaves = NB <= 4 ? 8 : 4;
+  dim3 grid(M / 16, split_k, (N + NB * 16 - 1) / (NB * 16));
+  hipLaunchKernelGGL((rgemm_kernel<NB, kWaves>), grid, dim3(kWaves * 64), 0, st, fixed, exps,
+                     eoff, start_exp, X, Y, M, N, K, kb_per_split);
+  return hipGetLastError();
+}
+
+static int status_of(hipError_t e) { return e == hipSuccess ? ZS_OK : (int)e; }
+
+static bool shape_ok(int M, int K) { return M > 0 && K > 0 && M % 64 == 0 && K % 64 == 0; }
+
+}  // namespace zs
+
+using namespace zs;
+
+extern "C" int64_t zs_retiled_num_records(int M, int K) {
+  if (!shape_ok(M, K)) return ZS_E_INVAL;
+  return (int64_t)(M / 16) * (K / 64);
+}
+
+extern "C" int64_t zs_retiled_fixed_bytes(int M, int K) {
+  if (!shape_ok(M, K)) return ZS_E_INVAL;
+  return (int64_t)(M / 16) * (K / 64) * kRecBytes;
+}
+
+extern "C" int zs_compress_retiled_count_gpu(void* stream, const uint16_t* d_input, int M, int K,
+                                             const int32_t* d_top_exponents, int32_t* d_counts,
+                                             int32_t* d_eoff, int64_t* d_total) {
+  if (!shape_ok(M, K) || !d_input || !d_top_exponents || !d_counts || !d_eoff || !d_total)
+    return ZS_E_INVAL;
+  if ((reinterpret_cast<uintptr_t>(d_input) & 15) != 0) return ZS_E_INVAL;
+  const int64_t nrec = (int64_t)(M / 16) * (K / 64);
+  if (nrec + 1 > INT32_MAX) return ZS_E_OVERFLOW;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(rcount_kernel, dim3(r_grid(nrec, 4)), dim3(256), 0, st, d_input, M, K,
+                     d_top_exponents, d_counts);
+  hipLaunchKernelGGL(rscan_kernel, dim3(1), dim3(1024), 0, st, d_counts, nrec, d_eoff, d_total);
+  return status_of(hipGetLastError());
+}
+
+extern "C" int zs_compress_retiled_emit_gpu(void* stream, const uint16_t* d_input, int M, int K,
+                                            const int32_t* d_top_exponents, const int32_t* d_eoff,
+                                            uint8_t* d_fixed, uint8_t* d_exps) {
+  if (!shape_ok(M, K) || !d_input || !d_top_exponents || !d_eoff || !d_fixed || !d_exps)
+    return ZS_E_INVAL;
+  if ((reinterpret_cast<uintptr_t>(d_input) & 15) || (reinterpret_cast<uintptr_t>(d_fixed) & 15))
+    return ZS_E_INVAL;
+  const int64_t nrec = (int64_t)(M / 16) * (K / 64);
+  hipLaunchKernelGGL(remit_kernel, dim3(r_grid(nrec, 4)), dim3(256), 0, (hipStream_t)stream,
+                     d_input, M, K, d_top_exponents, d_eoff, d_fixed, d_exps);
+  return status_of(hipGetLastError());
+}
+
+static Streams canon_streams(const uint8_t* sm, const uint16_t* full, const uint64_t* b1,
+                             const uint64_t* b2, const uint64_t* b3, const int32_t* tom,
+                             const int32_t* tog) {
+  Streams s;
+  s.sm = sm;
+  s.full = full;
+  s.bm1 = reinterpret_cast<const uint8_t*>(b1);
+  s.bm2 = reinterpret_cast<const uint8_t*>(b2);
+  s.bm3 = reinterpret_cast<const uint8_t*>(b3);
+  s.tom = tom;
+  s.tog = tog;
+  return s;
+}
+
+extern "C" int zs_retile_triple_bitmap_count_gpu(void* stream, const uint8_t* sm,
+                                                 const uint16_t* full, const uint64_t* b1,
+                                                 const uint64_t* b2, const uint64_t* b3,
+                                                 const int32_t* tom, const int32_t* tog, int M,
+                                                 int K, int32_t* d_counts, int32_t* d_eoff,
+                                                 int64_t* d_total) {
+  if (!shape_ok(M, K) || !sm || !full || !b1 || !b2 || !b3 || !tom || !tog || !d_counts ||
+      !d_eoff || !d_total)
+    return ZS_E_INVAL;
+  const int64_t nrec = (int64_t)(M / 16) * (K / 64);
+  if (nrec + 1 > INT32_MAX) return ZS_E_OVERFLOW;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(rcount_canon_kernel, dim3(r_grid(nrec, 4)), dim3(256), 0, st,
+                     canon_streams(sm, full, b1, b2, b3, tom, tog), M, K, d_counts);
+  hipLaunchKernelGGL(rscan_kernel, dim3(1), dim3(1024), 0, st, d_counts, nrec, d_eoff, d_total);
+  return status_of(hipGetLastError());
+}
+
+extern "C" int zs_retile_triple_bitmap_emit_gpu(void* stream, const uint8_t* sm,
+                                                const uint16_t* full, const uint64_t* b1,
+                                                const uint64_t* b2, const uint64_t* b3,
+                                                const int32_t* tom, const int32_t* tog,
+                                                uint8_t start_exp, int M, int K,
+                                                const int32_t* d_eoff, uint8_t* d_fixed,
+                                                uint8_t* d_exps) {
+  if (!shape_ok(M, K) || !sm || !full || !b1 || !b2 || !b3 || !tom || !tog || !d_eoff ||
+      !d_fixed || !d_exps)
+    return ZS_E_INVAL;
+  if (reinterpret_cast<uintptr_t>(d_fixed) & 15) return ZS_E_INVAL;
+  const int64_t nrec = (int64_t)(M / 16) * (K / 64);
+  hipLaunchKernelGGL(remit_canon_kernel, dim3(r_grid(nrec, 4)), dim3(256), 0,
+                     (hipStream_t)stream, canon_streams(sm, full, b1, b2, b3, tom, tog),
+                     (int)start_exp, M, K, d_eoff, d_fixed, d_exps);
+  return status_of(hipGetLastError());
+}
+
+extern "C" int zs_retiled_decompress(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
+                                     const int32_t* d_eoff, uint8_t start_exp, uint16_t* out,
+                                     int M, int K) {
+  if (!shape_ok(M, K) || !d_fixed || !d_exps || !d_eoff || !out) return ZS_E_INVAL;
+  if ((reinterpret_cast<uintptr_t>(d_fixed) & 15) || (reinterpret_cast<uintptr_t>(d_exps) & 15))
+    return ZS_E_INVAL;
+  const int64_t nrec = (int64_t)(M / 16) * (K / 64);
+  hipLaunchKernelGGL(rdecompress_kernel, dim3(r_grid(nrec, 4)), dim3(256), 0,
+                     (hipStream_t)stream, d_fixed, d_exps, d_eoff, (int)start_exp, out, M, K);
+  return status_of(hipGetLastError());
+}
+
+extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
+                             const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B,
+                             uint16_t* C, int M, int N, int K, uint16_t* ws, int split_k) {
+  if (!shape_ok(M, K) || N <= 0 || !d_fixed || !d_exps || !d_eoff || !B || !C) return ZS_E_INVAL;
+  if ((reinterpret_cast<uintptr_t>(d_fixed) & 15) || (reinterpret_cast<uintptr_t>(d_exps) & 15) ||
+      (reinterpret_cast<uintptr_t>(B) & 15) || (K % 8))
+    return ZS_E_INVAL;
+  const int KT = K / 64;
+  if (split_k < 1 || split_k > KT) return ZS_E_INVAL;
+  if (split_k > 1 && !ws) return ZS_E_INVAL;
+  if ((int64_t)M * N * split_k > INT32_MAX * 2LL) return ZS_E_OVERFLOW;
+  const int kb_per_split = (KT - 1) / split_k + 1;
+  hipStream_t st = (hipStream_t)stream;
+  uint16_t* out = split_k == 1 ? C : ws;
+  const int nb = (N + 15) / 16;
+  const int se = (int)start_exp;
+  hipError_t e;
+  if (nb <= 1) e = launch_rgemm<1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+  else if (nb <= 2) e = launch_rgemm<2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+  else if (nb <= 3) e = launch_rgemm<3>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+  else if (nb <= 4) e = launch_rgemm<4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+  else if (nb <= 6) e = launch_rgemm<6>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+  else e = launch_rgemm<8>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+  if (e != hipSuccess) return (int)e;
+  if (split_k > 1) {
+    const int64_t mn = (int64_t)M * N;
+    const int64_t threads = (mn + 7) / 8;
+    hipLaunchKernelGGL(rsplitk_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256),
+                       0, st, C, ws, mn, split_k);
+    e = hipGetLastError();
+  }
+  return status_of(e);
+}
