@@ -1,7 +1,8 @@
 """GPU parity of the CDNA4 re-tiled layout: encoders byte-identical to the
 oracle, decompress bit-exact, and ZipGEMM over the re-tiled layout identical
-(bit for bit) to ZipGEMM over the canonical streams it was built from, and
-within 1e-2 relative error of the fp32-accumulated product."""
+(bit for bit, N <= 16) or equal up to fp32 summation order (N > 16, 64-row
+kernel) to ZipGEMM over the canonical streams it was built from, and within
+1e-2 relative error of the fp32-accumulated product."""
 import numpy as np
 import pytest
 
@@ -94,10 +95,34 @@ def test_retiled_zipgemm_equals_canonical(torch_cuda, M, K, N):
     Yr = zs.zipgemm(r, x)
     torch.cuda.synchronize()
     yr = from_torch_bf16(Yr)
-    np.testing.assert_array_equal(yr, from_torch_bf16(Yc))
+    yc = from_torch_bf16(Yc)
+    if N <= 16:
+        # same workgroup shape and summation order as the canonical kernel
+        np.testing.assert_array_equal(yr, yc)
+    else:
+        # 64-row kernel: two K phases instead of eight, so the fp32 sums differ
+        # only in rounding -- at most a couple of bf16 ulps of the output
+        a, b = zo.bf16_to_f32(yr), zo.bf16_to_f32(yc)
+        assert np.all(np.abs(a - b) <= 2.0 ** -6 * np.maximum(np.abs(a), np.abs(b)) + 1e-6)
     ref = zo.gemm_f32(W, X)
     err = np.abs(zo.bf16_to_f32(yr) - ref).max() / max(np.abs(ref).max(), 1e-30)
     assert err <= 1e-2
+
+
+@pytest.mark.parametrize("N,split_k", [(20, 1), (64, 1), (128, 1), (40, 2)])
+def test_retiled_zipgemm_large_grid(torch_cuda, N, split_k):
+    # M / 64 * split_k >= 384 selects the two-phase 64-row kernel
+    torch = torch_cuda
+    rng = np.random.default_rng(N * 3 + split_k)
+    M, K = 24576, 128
+    W = weights_bf16(rng, (M, K), outlier_frac=0.01)
+    X = zo.f32_to_bf16(rng.standard_normal((N, K), dtype=np.float32))
+    r = zs.compress_retiled(to_torch_bf16(W))
+    Y = zs.zipgemm(r, to_torch_bf16(X), split_k=split_k)
+    torch.cuda.synchronize()
+    y = zo.bf16_to_f32(from_torch_bf16(Y))
+    ref = zo.gemm_f32(W, X) if split_k == 1 else zo.bf16_to_f32(zo.gemm_splitk_bf16(W, X, split_k))
+    assert np.abs(y - ref).max() / np.abs(ref).max() <= 1e-2
 
 
 @pytest.mark.parametrize("split_k,N", [(2, 24), (4, 16), (3, 100), (8, 1)])

@@ -31,7 +31,7 @@ namespace zs {
 constexpr int kRecBytes = 1408;
 constexpr int kRecP32 = 1024;
 constexpr int kRecP16 = 1280;
-constexpr int kExpChunks = 64;                     // staged exponent chunks per record
+constexpr int kExpChunks = 16;                     // staged exponent chunks per record
 constexpr int kExpStage = kExpChunks * 16 + 32;    // + window-read slack
 
 struct RTables {

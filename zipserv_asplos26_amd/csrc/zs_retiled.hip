@@ -212,8 +212,9 @@ __global__ __launch_bounds__(256) void remit_canon_kernel(Streams s, int start_e
 
 // ---------------------------------------------------------------------------
 // Record fetch: the fixed part straight into registers, the outlier bytes as
-// up to 64 16-byte chunks (lane l: chunk l) bound for a wave-private LDS stage.
-// A record with more than 64 chunks of outliers is decoded from global memory.
+// up to kExpChunks 16-byte chunks (lane l: chunk l) bound for a wave-private
+// LDS stage.  A record with more outlier bytes than that (over ~23% outliers)
+// is decoded with its outlier windows read from global memory.
 // ---------------------------------------------------------------------------
 struct RStage {
   RecRegs r;
@@ -424,6 +425,179 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
   }
 }
 
+// ---------------------------------------------------------------------------
+// ZipGEMM over the re-tiled layout for wider batches (N > 16).  Workgroup =
+// 4*PH waves on one 64-row tile (4 bands) x one split-K slice x 16*NB
+// columns; wave w decodes band w%4 of K tiles kb0 + PH*s + w/4 (PH
+// interleaved phases).  Each X tile (16*NB x 64) is loaded once per workgroup into LDS
+// and read by the four band waves of its phase, so X crosses L2 a quarter as
+// often as with 16-row workgroups.  Records are fetched two steps ahead into
+// registers, X tiles two steps ahead into registers and one step ahead into
+// a double-buffered LDS tile; one barrier per step.
+// ---------------------------------------------------------------------------
+constexpr int kXRow = 144;  // LDS pitch of an X tile row (128 B + 16 B pad)
+
+template <int NB, int PH>
+struct RWideSmem {
+  static constexpr int kX = PH * 2 * 16 * NB * kXRow;   // [phase][buffer] tiles
+  static constexpr int kStages = 4 * PH * 2 * kExpStage;
+  static constexpr int kMain = (int)sizeof(RTables) + kStages + kX;
+  static constexpr int kRed = (PH - 1) * 4 * NB * 64 * 16;
+  static constexpr int kBytes = kMain > kRed ? kMain : kRed;
+};
+
+template <int NB, int PH>
+__global__ __launch_bounds__(PH * 256) void rgemm_wide_kernel(const uint8_t* fixed,
+                                                              const uint8_t* exps,
+                                                              const int32_t* eoff, int start_exp,
+                                                              const uint16_t* X, uint16_t* Y,
+                                                              int M, int N, int K,
+                                                              int kb_per_split) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[RWideSmem<NB, PH>::kBytes];
+  RTables& T = *reinterpret_cast<RTables*>(smem);
+  build_r_tables(T, start_exp, threadIdx.x, blockDim.x);
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = lane_id();
+  const int q = w & 3, p = w >> 2;
+  const int t = threadIdx.x & 255;  // thread index within the phase
+  uint8_t* stage0 = smem + sizeof(RTables) + w * 2 * kExpStage;
+  uint8_t* stage1 = stage0 + kExpStage;
+  uint8_t* xbase = smem + sizeof(RTables) + RWideSmem<NB, PH>::kStages + p * 2 * 16 * NB * kXRow;
+  uint8_t* xb0 = xbase;
+  uint8_t* xb1 = xbase + 16 * NB * kXRow;
+  const int band = blockIdx.x * 4 + q;
+  const int split = blockIdx.y;
+  const int n0 = blockIdx.z * NB * 16;
+  const int KT = K >> 6;
+  const int kb0 = split * kb_per_split;
+  const int kb1 = min(kb0 + kb_per_split, KT);
+  const int span = max(kb1 - kb0, 0);
+  const int steps = (span + PH - 1) / PH;         // same for every phase
+  const int cnt = (span - p + PH - 1) / PH;       // valid tiles of this phase
+  // K tile of step j of this phase, clamped into the slice (clamped steps
+  // only repeat an in-bounds load and skip the decode).
+  auto tile_of = [&](int j) { return min(kb0 + PH * j + p, kb1 - 1); };
+  const int64_t rowrec = (int64_t)band * KT;
+
+  // X tile loads of this thread: chunk c = t + 256 i, row c/8, 16-byte column c%8.
+  constexpr int kXC = (NB + 1) / 2;  // chunks per thread (NB = 1: threads 0..127)
+  const uint16_t* xsrc[kXC];
+  int xdst[kXC];
+#pragma unroll
+  for (int i = 0; i < kXC; ++i) {
+    const int c = t + 256 * i;
+    const int row = min(c >> 3, 16 * NB - 1), cc = c & 7;
+    xsrc[i] = X + (int64_t)min(n0 + row, N - 1) * K + 8 * cc;
+    xdst[i] = c < 128 * NB ? row * kXRow + 16 * cc : -1;
+  }
+  f32x4 acc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int brd = (l & 15) * kXRow + 16 * (l >> 4);  // B fragment byte offset (nb = 0, h = 0)
+
+  // Outlier offsets of this wave's tiles, 64 at a time (lane i: tile c0 + i).
+  int oe0 = 0, oe1 = 0, ochunk = -1;
+  auto offs = [&](int j, int& e0, int& e1) {
+    const int c = j & ~63;
+    if (c != ochunk) {
+      ochunk = c;
+      const int64_t ri = rowrec + tile_of(c + l);
+      oe0 = eoff[ri];
+      oe1 = eoff[ri + 1];
+    }
+    e0 = __builtin_amdgcn_readlane(oe0, j - c);
+    e1 = __builtin_amdgcn_readlane(oe1, j - c);
+  };
+  auto issue = [&](int j, RStage& R, RMeta& Mt) {
+    int e0, e1;
+    offs(j, e0, e1);
+    r_issue(fixed, exps, rowrec + tile_of(j), e0, e1, R, Mt);
+  };
+  auto xload = [&](int j, u32x4 (&XR)[kXC]) {
+    const int kk = tile_of(j) * 64;
+#pragma unroll
+    for (int i = 0; i < kXC; ++i) XR[i] = *reinterpret_cast<const u32x4*>(xsrc[i] + kk);
+  };
+  auto xwrite = [&](uint8_t* xb, const u32x4 (&XR)[kXC]) {
+#pragma unroll
+    for (int i = 0; i < kXC; ++i)
+      if (NB > 1 || xdst[i] >= 0) *reinterpret_cast<u32x4*>(xb + xdst[i]) = XR[i];
+  };
+
+  if (span == 0) {  // empty split-K slice (uniform per workgroup)
+    __syncthreads();
+  } else {
+  RStage R0, R1;
+  RMeta M0, M1;
+  u32x4 XA[kXC], XB[kXC];
+  issue(0, R0, M0);
+  issue(1, R1, M1);
+  xload(0, XA);
+  xload(1, XB);
+  r_stage(stage0, R0, M0);
+  xwrite(xb0, XA);
+  xload(2, XA);
+  __syncthreads();  // decode tables and X tile 0 visible
+
+#define RW_STEP(S, CUR, NXT, XCUR, RC, MC, RN, MN, XRN, XRC)                           \
+  {                                                                                  \
+    const RStage cs_ = RC;                                                           \
+    const RMeta cm_ = MC;                                                            \
+    r_stage(NXT, RN, MN);                                                            \
+    issue((S) + 2, RC, MC);                                                          \
+    if ((S) < cnt) {                                                                 \
+      u32x4 a0_, a1_;                                                                \
+      r_decode_staged(T, cs_, cm_, CUR, exps, a0_, a1_);                             \
+      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                         \
+        const uint8_t* bp_ = XCUR + brd + nb_ * 16 * kXRow;                          \
+        const bf16x8 b0_ = *reinterpret_cast<const bf16x8*>(bp_);                    \
+        const bf16x8 b1_ = *reinterpret_cast<const bf16x8*>(bp_ + 64);               \
+        acc[nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0_), b0_,      \
+                                                           acc[nb_], 0, 0, 0);       \
+        acc[nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1_), b1_,      \
+                                                           acc[nb_], 0, 0, 0);       \
+      }                                                                              \
+    }                                                                                \
+    xwrite((XCUR) == xb0 ? xb1 : xb0, XRN);                                          \
+    xload((S) + 3, XRC);                                                             \
+    __syncthreads();                                                                 \
+  }
+  // Step s reads X buffer s%2; X registers: XB holds step s+1, XA step s+2
+  // at the start of an even step (roles swap on odd steps).
+  for (int s = 0; s < steps; s += 2) {
+    RW_STEP(s, stage0, stage1, xb0, R0, M0, R1, M1, XB, XB);
+    if (s + 1 < steps) RW_STEP(s + 1, stage1, stage0, xb1, R1, M1, R0, M0, XA, XA);
+  }
+#undef RW_STEP
+  }
+
+  // Phases 1..PH-1 hand their sums to phase 0 through LDS (added in phase
+  // order, so the result is deterministic); phase 0 writes its band.
+  f32x4* red = reinterpret_cast<f32x4*>(smem);
+  if (p > 0) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) red[(((p - 1) * 4 + q) * NB + nb) * 64 + l] = acc[nb];
+  }
+  __syncthreads();
+  if (p == 0) {
+    uint16_t* out = Y + (int64_t)split * M * N;
+    const int mrow = band * 16 + 4 * (l >> 4);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      f32x4 v = acc[nb];
+#pragma unroll
+      for (int pp = 1; pp < PH; ++pp) v += red[(((pp - 1) * 4 + q) * NB + nb) * 64 + l];
+      const int n = n0 + nb * 16 + (l & 15);
+      if (n < N) {
+        const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+        const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
+        *reinterpret_cast<uint2*>(out + (int64_t)n * M + mrow) = make_uint2(lo, hi);
+      }
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void rsplitk_reduce_kernel(uint16_t* C, const uint16_t* WS,
                                                              int64_t mn, int split_k) {
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
@@ -464,6 +638,16 @@ static hipError_t launch_rgemm(hipStream_t st, const uint8_t* fixed, const uint8
   dim3 grid(M / 16, split_k, (N + NB * 16 - 1) / (NB * 16));
   hipLaunchKernelGGL((rgemm_kernel<NB, kWaves>), grid, dim3(kWaves * 64), 0, st, fixed, exps,
                      eoff, start_exp, X, Y, M, N, K, kb_per_split);
+  return hipGetLastError();
+}
+
+template <int NB, int PH>
+static hipError_t launch_rwide(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
+                               const int32_t* eoff, int start_exp, const uint16_t* X,
+                               uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split) {
+  dim3 grid(M / 64, split_k, (N + NB * 16 - 1) / (NB * 16));
+  hipLaunchKernelGGL((rgemm_wide_kernel<NB, PH>), grid, dim3(PH * 256), 0, st, fixed, exps, eoff,
+                     start_exp, X, Y, M, N, K, kb_per_split);
   return hipGetLastError();
 }
 
@@ -592,12 +776,23 @@ extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t
   const int nb = (N + 15) / 16;
   const int se = (int)start_exp;
   hipError_t e;
-  if (nb <= 1) e = launch_rgemm<1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
-  else if (nb <= 2) e = launch_rgemm<2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
-  else if (nb <= 3) e = launch_rgemm<3>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
-  else if (nb <= 4) e = launch_rgemm<4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
-  else if (nb <= 6) e = launch_rgemm<6>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
-  else e = launch_rgemm<8>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+  // N > 16: 64-row workgroups sharing each X tile through LDS; four K phases
+  // per workgroup (16 waves) when the grid is small, two when it already
+  // covers the GPU.  N <= 16: 16-row workgroups (one band, 8 K phases).
+  const int64_t wide_wgs = (int64_t)(M / 64) * split_k;
+  if (nb >= 2) {
+    const bool ph4 = wide_wgs < 384;
+    if (nb <= 2)
+      e = ph4 ? launch_rwide<2, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split)
+              : launch_rwide<2, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+    else if (nb <= 4)
+      e = ph4 ? launch_rwide<4, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split)
+              : launch_rwide<4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+    else
+      e = launch_rwide<8, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+  } else {
+    e = launch_rgemm<1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+  }
   if (e != hipSuccess) return (int)e;
   if (split_k > 1) {
     const int64_t mn = (int64_t)M * N;
