@@ -244,6 +244,28 @@ int zs_decode_attention(void* stream, const uint16_t* q, const zs_kv_compressed_
 size_t zs_decode_attention_workspace_bytes(int batch, int num_heads, int head_dim, int seqlen_k,
                                            int num_splits);
 
+/* The same decode attention over caches held in the re-tiled layout (no
+ * counterpart in the reference; its KV caches use the canonical streams).
+ * Fields mirror zs_kv_compressed_t with the three re-tiled buffers. */
+typedef struct zs_kv_retiled {
+  const uint8_t* fixed;      /* num_records * 1408 bytes, 16-byte aligned      */
+  const uint8_t* exps;       /* outlier bytes (+ ZS_STREAM_SLACK_BYTES)        */
+  const int32_t* eoff;       /* num_records + 1 offsets into exps              */
+  int32_t rows;
+  int32_t cols;
+  int32_t batch_stride_rows;
+  int32_t head_stride_rows;
+  int32_t start_exp;
+  int32_t layout; /* ZS_LAYOUT_*                                           */
+} zs_kv_retiled_t;
+
+int zs_decode_attention_retiled(void* stream, const uint16_t* q, const zs_kv_retiled_t* k,
+                                const zs_kv_retiled_t* v, const int32_t* cache_seqlens,
+                                int seqlen_k, int batch, int num_heads, int num_heads_k,
+                                int head_dim, float softmax_scale, uint16_t* out,
+                                float* softmax_lse, void* workspace, size_t workspace_bytes,
+                                int num_splits);
+
 /* The uncompressed comparator (bench_zipserv_decode_attention.py:629-631,
  * dense flash_attn_with_kvcache): same kernel with K/V read from dense bf16
  * caches k_cache / v_cache [batch][cache_capacity][num_heads_k][head_dim]. */

@@ -23,7 +23,7 @@ def _bf16_f32(a):
     return zo.bf16_to_f32(a).astype(np.float64)
 
 
-def _run(torch_cuda, B, T, Hkv, H, seqlens=None, splits=0, seed=0, q_zero=False):
+def _run(torch_cuda, B, T, Hkv, H, seqlens=None, splits=0, seed=0, q_zero=False, retiled=False):
     import zipserv_asplos26_amd.attention as za
     torch = torch_cuda
     rng = np.random.default_rng(seed)
@@ -34,8 +34,8 @@ def _run(torch_cuda, B, T, Hkv, H, seqlens=None, splits=0, seed=0, q_zero=False)
     if q_zero:
         q[:] = 0
     kd, vd, qd = to_torch_bf16(k), to_torch_bf16(v), to_torch_bf16(q)
-    ck = za.compress_kv(kd)
-    cv = za.compress_kv(vd)
+    ck = za.compress_kv(kd, retiled=retiled)
+    cv = za.compress_kv(vd, retiled=retiled)
     sl = None if seqlens is None else torch.tensor(seqlens, dtype=torch.int32, device="cuda")
     out, lse = za.flash_attn_with_kvcache_zipserv(
         qd.view(B, 1, H, D), ck, cv, Hkv, T, cache_seqlens=sl, num_splits=splits,
@@ -75,6 +75,20 @@ def _check(res, seqlens=None):
 ])
 def test_attention_matches_oracle(torch_cuda, B, T, Hkv, H, splits):
     _check(_run(torch_cuda, B, T, Hkv, H, splits=splits))
+
+
+@pytest.mark.parametrize("B,T,Hkv,H,splits", [
+    (1, 64, 8, 64, 1), (2, 100, 8, 64, 0), (2, 1000, 8, 64, 3), (1, 4096, 8, 64, 0),
+    (2, 700, 2, 32, 5), (2, 300, 4, 4, 2), (3, 257, 1, 8, 64)])
+def test_attention_retiled_matches_oracle(torch_cuda, B, T, Hkv, H, splits):
+    # same decoded K/V and arithmetic as the canonical path: identical to dense
+    _check(_run(torch_cuda, B, T, Hkv, H, splits=splits, retiled=True))
+
+
+@pytest.mark.parametrize("splits", [1, 0])
+def test_attention_retiled_ragged(torch_cuda, splits):
+    seqlens = [300, 17, 0, 64]
+    _check(_run(torch_cuda, 4, 300, 8, 64, seqlens=seqlens, splits=splits, seed=3, retiled=True))
 
 
 @pytest.mark.parametrize("splits", [1, 0, 4])

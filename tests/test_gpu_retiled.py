@@ -125,6 +125,28 @@ def test_retiled_zipgemm_large_grid(torch_cuda, N, split_k):
     assert np.abs(y - ref).max() / np.abs(ref).max() <= 1e-2
 
 
+@pytest.mark.parametrize("N", [1, 16, 64])
+def test_retiled_mixed_direct_and_staged_records(torch_cuda, N):
+    # Some records carry more outlier bytes than the LDS stage (zero bands:
+    # every element an outlier) next to ordinary records decoded by other waves
+    # of the same workgroup; both decode paths must leave each other intact.
+    torch = torch_cuda
+    rng = np.random.default_rng(77 + N)
+    M, K = 256, 1024
+    W = weights_bf16(rng, (M, K), outlier_frac=0.01)
+    W[16:32, :] = 0                    # one band of all-outlier records
+    W[100:116, 128:256] = 0            # two records of another band
+    X = zo.f32_to_bf16(rng.standard_normal((N, K), dtype=np.float32))
+    r = zs.compress_retiled(to_torch_bf16(W))
+    out = zs.decompress_retiled(r)
+    Y = zs.zipgemm(r, to_torch_bf16(X))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_torch_bf16(out), W)
+    y = zo.bf16_to_f32(from_torch_bf16(Y))
+    ref = zo.gemm_f32(W, X)
+    assert np.abs(y - ref).max() / np.abs(ref).max() <= 1e-2
+
+
 @pytest.mark.parametrize("split_k,N", [(2, 24), (4, 16), (3, 100), (8, 1)])
 def test_retiled_zipgemm_splitk(torch_cuda, split_k, N):
     torch = torch_cuda

@@ -69,6 +69,9 @@ SIGNATURES = {
                   _p, _p, _p, C.c_size_t, C.c_int]),
     "zs_decode_attention_workspace_bytes": (
         C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "zs_decode_attention_retiled": (
+        C.c_int, [_p, _p, _p, _p, _p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
+                  _p, _p, _p, C.c_size_t, C.c_int]),
     "zs_decode_attention_dense": (
         C.c_int, [_p, _p, _p, _p, _p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                   C.c_float, _p, _p, _p, C.c_size_t, C.c_int]),
@@ -111,6 +114,21 @@ def lib() -> C.CDLL:
 def check(fn: str, status: int) -> None:
     if status != ZS_OK:
         raise ZipServError(fn, status)
+
+
+class KVRetiled(C.Structure):
+    """zs_kv_retiled_t of include/zipserv.h."""
+    _fields_ = [
+        ("fixed", _p),
+        ("exps", _p),
+        ("eoff", _p),
+        ("rows", _i32),
+        ("cols", _i32),
+        ("batch_stride_rows", _i32),
+        ("head_stride_rows", _i32),
+        ("start_exp", _i32),
+        ("layout", _i32),
+    ]
 
 
 class KVCompressed(C.Structure):

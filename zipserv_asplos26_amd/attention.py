@@ -15,7 +15,7 @@ from typing import Optional
 
 from . import _lib
 from ._lib import check, lib
-from .codec import _check_cuda, _dptr, _stream, _torch, compress
+from .codec import ZipservRetiled, _check_cuda, _dptr, _stream, _torch, compress, compress_retiled
 
 # flash_attn_interface.py:38-43 (_ZIPSERV_LAYOUT_IDS)
 LAYOUT_IDS = {"by_kv_head": _lib.ZS_LAYOUT_HEAD_MAJOR, "dense": _lib.ZS_LAYOUT_TOKEN_MAJOR,
@@ -53,15 +53,36 @@ def pad_batched_kv_prefix(x):
     return out.view(B * rpb, cols), lr * B, rpb
 
 
-def compress_kv(x, layout: str = "by_kv_head"):
-    """Pack a (B, T, Hkv, D) bf16 cache and compress it on the GPU."""
+def compress_kv(x, layout: str = "by_kv_head", retiled: bool = False):
+    """Pack a (B, T, Hkv, D) bf16 cache and compress it on the GPU into the
+    canonical streams (ZipservCompressed) or the re-tiled layout
+    (ZipservRetiled)."""
     if layout == "by_kv_head":
         mat, logical_rows, _ = pad_batched_kv_prefix_by_kv_head(x)
     elif layout in ("token_major", "dense"):
         mat, logical_rows, _ = pad_batched_kv_prefix(x)
     else:
         raise ValueError(f"unknown layout {layout!r}")
-    return compress(mat.contiguous(), logical_rows, x.shape[-1], layout=layout)
+    fn = compress_retiled if retiled else compress
+    return fn(mat.contiguous(), logical_rows, x.shape[-1], layout=layout)
+
+
+def _retiled_desc(c, *, name, device, batch_size, num_heads_k):
+    """zs_kv_retiled_t for a ZipservRetiled cache (strides as in
+    _normalize_zipserv_kv)."""
+    if c.device != device:
+        raise ValueError(f"{name} must be on {device}")
+    if c.rows % batch_size:
+        raise ValueError(f"{name}.rows must be divisible by batch_size={batch_size}")
+    bsr = c.rows // batch_size
+    if bsr % num_heads_k:
+        raise ValueError(f"{name}.rows must encode an integer rows-per-head for num_heads_k={num_heads_k}")
+    d = _lib.KVRetiled()
+    d.fixed, d.exps, d.eoff = _dptr(c.fixed), _dptr(c.exps), _dptr(c.eoff)
+    d.rows, d.cols = c.rows, c.cols
+    d.batch_stride_rows, d.head_stride_rows = bsr, bsr // num_heads_k
+    d.start_exp, d.layout = c.start_exp, LAYOUT_IDS[str(c.layout)]
+    return d
 
 
 def _normalize_zipserv_kv(desc, *, name: str, device, batch_size: int, num_heads_k: int):
@@ -146,10 +167,20 @@ def flash_attn_with_kvcache_zipserv(q, zipserv_k, zipserv_v, zipserv_num_heads_k
     q3 = _q3(q)
     _check_cuda(q3, "q", torch.bfloat16)
     B, H, D = q3.shape
-    dk, keep_k = _normalize_zipserv_kv(zipserv_k, name="zipserv_k", device=q.device,
-                                       batch_size=B, num_heads_k=zipserv_num_heads_k)
-    dv, keep_v = _normalize_zipserv_kv(zipserv_v, name="zipserv_v", device=q.device,
-                                       batch_size=B, num_heads_k=zipserv_num_heads_k)
+    retiled = isinstance(zipserv_k, ZipservRetiled)
+    if retiled != isinstance(zipserv_v, ZipservRetiled):
+        raise ValueError("zipserv_k and zipserv_v must use the same layout")
+    if retiled:
+        dk = _retiled_desc(zipserv_k, name="zipserv_k", device=q.device, batch_size=B,
+                           num_heads_k=zipserv_num_heads_k)
+        dv = _retiled_desc(zipserv_v, name="zipserv_v", device=q.device, batch_size=B,
+                           num_heads_k=zipserv_num_heads_k)
+        keep_k, keep_v = zipserv_k, zipserv_v
+    else:
+        dk, keep_k = _normalize_zipserv_kv(zipserv_k, name="zipserv_k", device=q.device,
+                                           batch_size=B, num_heads_k=zipserv_num_heads_k)
+        dv, keep_v = _normalize_zipserv_kv(zipserv_v, name="zipserv_v", device=q.device,
+                                           batch_size=B, num_heads_k=zipserv_num_heads_k)
     scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
     out = torch.empty_like(q3)
     lse = torch.empty((B, H), dtype=torch.float32, device=q.device) if return_softmax_lse else None
@@ -158,7 +189,8 @@ def flash_attn_with_kvcache_zipserv(q, zipserv_k, zipserv_v, zipserv_num_heads_k
     wsb = int(L.zs_decode_attention_workspace_bytes(B, H, D, seqlen_k, num_splits))
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=q.device)
     import ctypes
-    check("zs_decode_attention", L.zs_decode_attention(
+    fn_name = "zs_decode_attention_retiled" if retiled else "zs_decode_attention"
+    check(fn_name, getattr(L, fn_name)(
         _stream(), _dptr(q3), ctypes.byref(dk), ctypes.byref(dv), _dptr(sl), int(seqlen_k), B, H,
         int(zipserv_num_heads_k), D, scale, _dptr(out), _dptr(lse), _dptr(ws), ws.numel(),
         int(num_splits)))

@@ -25,6 +25,7 @@
 
 #include "../../include/zipserv.h"
 #include "zs_device.hpp"
+#include "zs_rdecode.hpp"
 #include "zs_stage.hpp"
 
 namespace zs {
@@ -36,10 +37,29 @@ constexpr int kHeadDim = 128;
 constexpr int kAttnWaves = 4;
 constexpr int kVRow = 160;                  // LDS row pitch of the V tile (bytes)
 constexpr int kVBytes = 16 * kVRow;         // 16 tokens x 64 dims (+ pad)
-constexpr int kAttnWaveLds = 2 * kStBytes + kVBytes;
+constexpr int kModeCanon = 0;    // canonical TCA-TBE streams
+constexpr int kModeDense = 1;    // dense bf16 caches
+constexpr int kModeRetiled = 2;  // re-tiled records (zs_rdecode.hpp)
+
+template <int kMode>
+struct AttnLds {
+  // per-workgroup decode tables, then per-wave stages and the V tile
+  static constexpr int kTables = kMode == kModeCanon ? (int)sizeof(DecodeTables) + 256 * 16
+                                 : kMode == kModeRetiled ? (int)sizeof(RTables) + 256 * 16
+                                                         : 0;
+  static constexpr int kWave = (kMode == kModeCanon ? 2 * kStBytes
+                                : kMode == kModeRetiled ? 2 * kExpStage : 0) + kVBytes;
+  static constexpr int kBytes = kTables + kAttnWaves * kWave;
+};
 
 struct AttnParams {
-  Streams k, v;                 // compressed caches (compressed kernel)
+  Streams k, v;                 // compressed caches (canonical kernel)
+  const uint8_t* kfix;          // re-tiled caches: fixed records, outlier bytes, offsets
+  const uint8_t* kexp;
+  const int32_t* keo;
+  const uint8_t* vfix;
+  const uint8_t* vexp;
+  const int32_t* veo;
   const uint16_t* kd;           // dense caches [B][cap][Hkv][D] (dense kernel)
   const uint16_t* vd;
   int k_start, v_start;         // start_exp of K and V
@@ -89,14 +109,20 @@ __device__ __forceinline__ int kv_tile(int rowbase, int med, int c) {
   return ((rowbase >> 6) + (med >> 2)) * 2 + c;
 }
 
-template <bool kDense>
+template <int kMode>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnParams p) {
+  constexpr bool kDense = kMode == kModeDense;
   extern __shared__ __attribute__((aligned(16))) uint8_t attn_smem[];
   DecodeTables& T = *reinterpret_cast<DecodeTables*>(attn_smem);
-  uint4* e1v = reinterpret_cast<uint4*>(attn_smem + sizeof(DecodeTables));
-  if constexpr (!kDense) {
+  RTables& RT = *reinterpret_cast<RTables*>(attn_smem);
+  uint4* e1v = reinterpret_cast<uint4*>(
+      attn_smem + (kMode == kModeRetiled ? sizeof(RTables) : sizeof(DecodeTables)));
+  if constexpr (kMode == kModeCanon) {
     build_decode_tables(T, p.k_start, threadIdx.x, blockDim.x);
     build_e1(e1v, p.v_start, threadIdx.x, blockDim.x);
+  } else if constexpr (kMode == kModeRetiled) {
+    build_r_tables(RT, p.k_start, threadIdx.x, blockDim.x);
+    build_r_e1(e1v, p.v_start, threadIdx.x, blockDim.x);
   }
   __syncthreads();
 
@@ -114,10 +140,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnParams p) {
   const int t1 = min(t0 + p.chunk, L);
   const int nmed = t1 > t0 ? (t1 - t0 + 15) >> 4 : 0;
 
-  uint8_t* wl = attn_smem + (kDense ? 0 : sizeof(DecodeTables) + 256 * 16) + w * kAttnWaveLds;
+  uint8_t* wl = attn_smem + AttnLds<kMode>::kTables + w * AttnLds<kMode>::kWave;
+  constexpr int kStage = kMode == kModeCanon ? kStBytes : kExpStage;
   uint8_t* stage0 = wl;
-  uint8_t* stage1 = wl + kStBytes;
-  uint8_t* vbuf = wl + 2 * kStBytes;
+  uint8_t* stage1 = wl + kStage;
+  uint8_t* vbuf = wl + AttnLds<kMode>::kWave - kVBytes;
 
   // q^T fragments (B operand): lane l -> head l%16 of this KV group, dims
   // 32c + 8*(l/16) .. +7.  Heads past the group read head 0 and are dropped.
@@ -226,6 +253,64 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnParams p) {
           fetch(jn <= last ? jn : ((last & ~3) | i), A0[i], A1[i]);
           consume(i, (j >> 2), a0, a1);
         }
+      }
+    } else if constexpr (kMode == kModeRetiled) {
+      // Records fetched four steps ahead into registers; outlier bytes staged
+      // one step ahead.  Steps K0,K1,V0,V1 of median `med` are the records
+      // of its band in K (column tiles 0, 1), then in V.
+      for (int c0 = 0; c0 < nstep; c0 += 64) {
+        const int n = min(nstep - c0, 64);
+        const int lastc = n - 1;
+        int oe0, oe1;
+        {
+          const int j = c0 + min(l, lastc);
+          const int ty = j & 3, med = j >> 2;
+          const int64_t rec = (int64_t)(((ty < 2 ? k_rowbase : v_rowbase) >> 4) + med) * 2 + (ty & 1);
+          const int32_t* eo = ty < 2 ? p.keo : p.veo;
+          oe0 = eo[rec];
+          oe1 = eo[rec + 1];
+        }
+        RStage R0, R1, R2, R3;
+        RMeta M0, M1, M2, M3;
+#define ZR_ISSUE(J, I, R, MT)                                                           \
+  {                                                                                     \
+    const int jj_ = (J);                                                                \
+    const int med_ = (c0 + jj_) >> 2;                                                   \
+    const int64_t rec_ =                                                                \
+        (int64_t)((((I) < 2 ? k_rowbase : v_rowbase) >> 4) + med_) * 2 + ((I) & 1);    \
+    r_issue((I) < 2 ? p.kfix : p.vfix, (I) < 2 ? p.kexp : p.vexp, rec_,                 \
+            __builtin_amdgcn_readlane(oe0, jj_), __builtin_amdgcn_readlane(oe1, jj_), R, \
+            MT);                                                                        \
+  }
+#define ZR_CLAMP(J, I) ((J) <= lastc ? (J) : ((lastc & ~3) | (I)))
+#define ZR_STEP(J, I, CUR, NXT, RC, MC, RN, MN)                                         \
+  {                                                                                     \
+    const RStage cs_ = RC;                                                              \
+    const RMeta cm_ = MC;                                                               \
+    r_stage(NXT, RN, MN);                                                               \
+    ZR_ISSUE(ZR_CLAMP((J) + 4, I), I, RC, MC);                                          \
+    u32x4 a0_, a1_;                                                                     \
+    if (cm_.nch <= kExpChunks)                                                          \
+      r_decode(RT, (I) < 2 ? RT.e1 : e1v, cs_.r, (const uint8_t*)(CUR), cm_.rel, a0_, a1_); \
+    else                                                                                \
+      r_decode(RT, (I) < 2 ? RT.e1 : e1v, cs_.r, ((I) < 2 ? p.kexp : p.vexp) + cm_.e0,  \
+               0, a0_, a1_);                                                            \
+    consume((I), (c0 + (J)) >> 2, a0_, a1_);                                            \
+  }
+        ZR_ISSUE(0, 0, R0, M0);  // n >= 4: a chunk holds whole medians
+        ZR_ISSUE(1, 1, R1, M1);
+        ZR_ISSUE(2, 2, R2, M2);
+        ZR_ISSUE(3, 3, R3, M3);
+        r_stage(stage0, R0, M0);
+        for (int j = 0; j < n; j += 4) {
+          ZR_STEP(j, 0, stage0, stage1, R0, M0, R1, M1);
+          ZR_STEP(j + 1, 1, stage1, stage0, R1, M1, R2, M2);
+          ZR_STEP(j + 2, 2, stage0, stage1, R2, M2, R3, M3);
+          ZR_STEP(j + 3, 3, stage1, stage0, R3, M3, R0, M0);
+        }
+#undef ZR_STEP
+#undef ZR_CLAMP
+#undef ZR_ISSUE
       }
     } else {
       // Offsets of up to 64 steps at a time (lane i -> step c0 + i).
@@ -353,7 +438,7 @@ static size_t attn_ws_bytes(int batch, int heads, int splits) {
   return (size_t)batch * heads * splits * (kHeadDim + 2) * sizeof(float);
 }
 
-template <bool kDense>
+template <int kMode>
 static int attn_launch(hipStream_t st, AttnParams& p, void* workspace, size_t ws_bytes) {
   if (p.splits > 1) {
     if (!workspace || ws_bytes < attn_ws_bytes(p.batch, p.heads, p.splits)) return ZS_E_INVAL;
@@ -362,9 +447,8 @@ static int attn_launch(hipStream_t st, AttnParams& p, void* workspace, size_t ws
   }
   const int items = p.batch * p.heads_k * p.splits;
   const int grid = (items + kAttnWaves - 1) / kAttnWaves;
-  const size_t lds = (kDense ? 0 : sizeof(DecodeTables) + 256 * 16) +
-                     (size_t)kAttnWaves * kAttnWaveLds;
-  hipLaunchKernelGGL(attn_kernel<kDense>, dim3(grid), dim3(kAttnWaves * 64), lds, st, p);
+  const size_t lds = AttnLds<kMode>::kBytes;
+  hipLaunchKernelGGL(attn_kernel<kMode>, dim3(grid), dim3(kAttnWaves * 64), lds, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   if (p.splits > 1) {
@@ -452,7 +536,60 @@ extern "C" int zs_decode_attention(void* stream, const uint16_t* q, const zs_kv_
   p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
   p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
-  return attn_launch<false>((hipStream_t)stream, p, workspace, workspace_bytes);
+  return attn_launch<kModeCanon>((hipStream_t)stream, p, workspace, workspace_bytes);
+}
+
+extern "C" int zs_decode_attention_retiled(void* stream, const uint16_t* q,
+                                           const zs_kv_retiled_t* k, const zs_kv_retiled_t* v,
+                                           const int32_t* cache_seqlens, int seqlen_k,
+                                           int batch, int num_heads, int num_heads_k,
+                                           int head_dim, float softmax_scale, uint16_t* out,
+                                           float* softmax_lse, void* workspace,
+                                           size_t workspace_bytes, int num_splits) {
+  int stc = attn_common_checks(batch, num_heads, num_heads_k, head_dim, seqlen_k, num_splits, q,
+                               out);
+  if (stc != ZS_OK) return stc;
+  if (!k || !v) return ZS_E_INVAL;
+  const zs_kv_retiled_t* kv[2] = {k, v};
+  for (const zs_kv_retiled_t* c : kv) {
+    if (!c->fixed || !c->exps || !c->eoff) return ZS_E_INVAL;
+    if ((reinterpret_cast<uintptr_t>(c->fixed) & 15) || (reinterpret_cast<uintptr_t>(c->exps) & 15))
+      return ZS_E_INVAL;
+    if (c->layout != ZS_LAYOUT_HEAD_MAJOR) return ZS_E_UNSUPPORTED;
+    if (c->cols != kHeadDim || c->rows <= 0 || (c->rows % 64)) return ZS_E_INVAL;
+    if (c->head_stride_rows <= 0 || (c->head_stride_rows % 64) ||
+        c->batch_stride_rows != num_heads_k * c->head_stride_rows ||
+        (int64_t)c->batch_stride_rows * batch > c->rows || c->head_stride_rows < seqlen_k)
+      return ZS_E_INVAL;
+    if (c->start_exp < 0 || c->start_exp > 255) return ZS_E_INVAL;
+  }
+  AttnParams p{};
+  p.kfix = k->fixed;
+  p.kexp = k->exps;
+  p.keo = k->eoff;
+  p.vfix = v->fixed;
+  p.vexp = v->exps;
+  p.veo = v->eoff;
+  p.k_start = k->start_exp;
+  p.v_start = v->start_exp;
+  p.k_bsr = k->batch_stride_rows;
+  p.k_hsr = k->head_stride_rows;
+  p.v_bsr = v->batch_stride_rows;
+  p.v_hsr = v->head_stride_rows;
+  p.q = q;
+  p.out = out;
+  p.lse = softmax_lse;
+  p.seqlens = cache_seqlens;
+  p.seqlen_k = seqlen_k;
+  p.batch = batch;
+  p.heads = num_heads;
+  p.heads_k = num_heads_k;
+  p.group = num_heads / num_heads_k;
+  p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k);
+  p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
+  p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
+  p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  return attn_launch<kModeRetiled>((hipStream_t)stream, p, workspace, workspace_bytes);
 }
 
 extern "C" int zs_decode_attention_dense(void* stream, const uint16_t* q, const uint16_t* k_cache,
@@ -483,5 +620,5 @@ extern "C" int zs_decode_attention_dense(void* stream, const uint16_t* q, const 
   p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
   p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
-  return attn_launch<true>((hipStream_t)stream, p, workspace, workspace_bytes);
+  return attn_launch<kModeDense>((hipStream_t)stream, p, workspace, workspace_bytes);
 }

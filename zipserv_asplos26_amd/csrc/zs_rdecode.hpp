@@ -153,4 +153,51 @@ __device__ __forceinline__ void r_decode(const RTables& T, const uint4* e1, cons
   o1 = r_half(T, e1, r.p32 >> 24, r.p16 & 0xFFu, (r.p16 >> 8) & 0xFFu, r.sm[2], r.sm[3], c0, c1);
 }
 
+// ---------------------------------------------------------------------------
+// Record fetch: the fixed part straight into registers, the outlier bytes as
+// up to kExpChunks 16-byte chunks (lane l: chunk l) bound for a wave-private
+// LDS stage.  A record with more outlier bytes than that (over ~23% outliers)
+// is decoded with its outlier windows read from global memory.
+// ---------------------------------------------------------------------------
+struct RStage {
+  RecRegs r;
+  u32x4 ex;
+};
+struct RMeta {
+  int e0;    // first outlier byte of the record (stream offset)
+  int rel;   // e0 - first staged byte
+  int nch;   // staged chunks (> kExpChunks: decode from global memory)
+};
+
+__device__ __forceinline__ void r_issue(const uint8_t* fixed, const uint8_t* exps, int64_t rec,
+                                        int e0, int e1, RStage& s, RMeta& mt) {
+  const int l = lane_id();
+  const uint8_t* f = fixed + rec * kRecBytes;
+  s.r.sm = *reinterpret_cast<const u32x4*>(f + 16 * l);
+  s.r.p32 = *reinterpret_cast<const uint32_t*>(f + kRecP32 + 4 * l);
+  s.r.p16 = *reinterpret_cast<const uint16_t*>(f + kRecP16 + 2 * l);
+  const int ea0 = e0 & ~15;
+  const int nch = (e1 - ea0 + 15) >> 4;
+  mt.e0 = e0;
+  mt.rel = e0 - ea0;
+  mt.nch = nch;
+  s.ex = *reinterpret_cast<const u32x4*>(exps + ea0 + (l < nch ? 16 * l : 0));
+}
+
+// Records whose outlier bytes exceed the stage are decoded from global memory
+// and are not staged (the stage holds kExpChunks chunks).
+__device__ __forceinline__ void r_stage(uint8_t* st, const RStage& s, const RMeta& mt) {
+  const int l = lane_id();
+  if (mt.nch <= kExpChunks && l < mt.nch) *reinterpret_cast<u32x4*>(st + 16 * l) = s.ex;
+}
+
+__device__ __forceinline__ void r_decode_staged(const RTables& T, const RStage& s,
+                                                const RMeta& mt, const uint8_t* st,
+                                                const uint8_t* exps, u32x4& o0, u32x4& o1) {
+  if (mt.nch <= kExpChunks)
+    r_decode(T, T.e1, s.r, st, mt.rel, o0, o1);
+  else
+    r_decode(T, T.e1, s.r, exps + mt.e0, 0, o0, o1);
+}
+
 }  // namespace zs
