@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--reps", type=int, default=20, help="graph replays per (shape, N) in the per-kernel timing")
+    ap.add_argument("--splits", default="1,2,4",
+                    help="split-K values tried per (shape, N); the fastest is used")
     ap.add_argument("--no-c3", action="store_true", help="skip the 80-layer Llama-3.1-70B sweep")
     ap.add_argument("--no-attention", action="store_true", help="skip the decode-attention sweep")
     ap.add_argument("--no-kv", action="store_true", help="skip the KV-cache codec sweep")
@@ -391,7 +393,7 @@ def main():
     for si, (name, M, K) in enumerate(SHAPES):
         for N in NS:
             best = None
-            for sk in SPLITS:
+            for sk in [int(v) for v in args.splits.split(",")]:
                 ws = zs.codec.splitk_workspace(layers[0][si][5], N, sk)
                 def srun(si=si, N=N, M=M, K=K, sk=sk, ws=ws):
                     for r in range(args.reps):
