@@ -293,10 +293,10 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
     // lane i: outlier offsets of tile c0 + i (clamped to the chunk)
     const int64_t ri = rec0 + (int64_t)(c0 + min(l, last)) * WAVES;
     const int oe0 = eoff[ri], oe1 = eoff[ri + 1];
-    constexpr bool kXRing = NB <= 2;
+    // X fragments are loaded one tile ahead (an L2 hit); records three ahead.
     RStage R0, R1, R2;
     RMeta M0, M1, M2;
-    bf16x8 X0[2][NB], X1[2][NB], X2[2][NB], xc[2][NB], xn[2][NB];
+    bf16x8 xc[2][NB], xn[2][NB];
 #define RZ_LOADX(J, DST)                                                            \
   {                                                                                 \
     const int kk_ = (kb0 + w + (c0 + (J)) * WAVES) * 64;                            \
@@ -304,24 +304,22 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
       _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_)                          \
         DST[h_][nb_] = *reinterpret_cast<const bf16x8*>(xrow[nb_] + kk_ + 32 * h_); \
   }
-#define RZ_ISSUE(J, R, MT, XD)                                                      \
+#define RZ_ISSUE(J, R, MT)                                                          \
   {                                                                                 \
     const int j_ = (J);                                                             \
     r_issue(fixed, exps, rec0 + (int64_t)(c0 + j_) * WAVES,                         \
             __builtin_amdgcn_readlane(oe0, j_), __builtin_amdgcn_readlane(oe1, j_), \
             R, MT);                                                                 \
-    if constexpr (kXRing) RZ_LOADX(j_, XD);                                         \
   }
-#define RZ_STEP(J, CUR, NXT, RC, MC, XC, RN, MN)                                         \
+#define RZ_STEP(J, CUR, NXT, RC, MC, RN, MN)                                             \
   {                                                                                      \
     const RStage cs_ = RC;                                                               \
     const RMeta cm_ = MC;                                                                \
     _Pragma("unroll") for (int h_ = 0; h_ < 2; ++h_)                                     \
-      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_)                               \
-        xc[h_][nb_] = kXRing ? XC[h_][nb_] : xn[h_][nb_];                                \
+      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) xc[h_][nb_] = xn[h_][nb_];    \
     r_stage(NXT, RN, MN);                                                                \
-    RZ_ISSUE(min((J) + 3, last), RC, MC, XC);                                            \
-    if constexpr (!kXRing) RZ_LOADX(min((J) + 1, last), xn);                             \
+    RZ_ISSUE(min((J) + 3, last), RC, MC);                                                \
+    RZ_LOADX(min((J) + 1, last), xn);                                                    \
     if ((J) < n) {                                                                       \
       u32x4 a0_, a1_;                                                                    \
       r_decode_staged(T, cs_, cm_, CUR, exps, a0_, a1_);                                 \
@@ -333,15 +331,15 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
       }                                                                                  \
     }                                                                                    \
   }
-    RZ_ISSUE(0, R0, M0, X0);
-    RZ_ISSUE(min(1, last), R1, M1, X1);
-    RZ_ISSUE(min(2, last), R2, M2, X2);
-    if constexpr (!kXRing) RZ_LOADX(0, xn);
+    RZ_ISSUE(0, R0, M0);
+    RZ_ISSUE(min(1, last), R1, M1);
+    RZ_ISSUE(min(2, last), R2, M2);
+    RZ_LOADX(0, xn);
     r_stage(stage0, R0, M0);
     for (int j = 0; j < n; j += 3) {
-      RZ_STEP(j, stage0, stage1, R0, M0, X0, R1, M1);
-      RZ_STEP(j + 1, stage1, stage2, R1, M1, X1, R2, M2);
-      RZ_STEP(j + 2, stage2, stage0, R2, M2, X2, R0, M0);
+      RZ_STEP(j, stage0, stage1, R0, M0, R1, M1);
+      RZ_STEP(j + 1, stage1, stage2, R1, M1, R2, M2);
+      RZ_STEP(j + 2, stage2, stage0, R2, M2, R0, M0);
     }
 #undef RZ_STEP
 #undef RZ_ISSUE
