@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
-"""ZipGEMM benchmark on one MI355X (BASELINE.json metric, config 2).
+"""ZipGEMM benchmark on one MI355X (the benchmark spec's headline metric, config 2).
 
-Workload: Llama-3-8B-shaped projections
+Workload (benchmark config 2): Llama-3-8B-shaped projections
 qkv 6144x4096, o 4096x4096, gate/up 14336x4096, down 4096x14336 with
 W ~ N(0, 0.02) bf16 and 0.1% of entries scaled x30, X[N, K] ~ N(0, 1) bf16.
 One *step* is one decoder layer's five ZipGEMMs at every N in {1, 8, 16, 32,
@@ -88,7 +88,7 @@ C3_LAYERS = 80
 
 
 def bench_c3(torch, zs, stream, gen, dev):
-    """80 Llama-3.1-70B layers (W ~ N(0, 0.02) bf16) compressed on
+    """Benchmark config 3: 80 Llama-3.1-70B layers (W ~ N(0, 0.02) bf16) compressed on
     the GPU into the re-tiled layout and resident; per-token time of the 400
     ZipGEMMs at each N, the dense comparator timed on 8 distinct resident layers
     and scaled to 80."""
@@ -162,13 +162,13 @@ ATTN_CASES = [(1, 4096), (1, 16384), (1, 32768), (8, 4096), (8, 16384), (8, 3276
 
 
 def kv_tensor(torch, gen, dev, B, T, Hkv=8, D=128):
-    """BASELINE configs 4/5: N(0,1) times per-(head, channel) lognormal(0,1) scales."""
+    """Benchmark configs 4/5: N(0,1) times per-(head, channel) lognormal(0,1) scales."""
     scale = torch.exp(torch.randn(1, 1, Hkv, D, device=dev, generator=gen))
     return (torch.randn(B, T, Hkv, D, device=dev, generator=gen) * scale).to(torch.bfloat16)
 
 
 def bench_attention(torch, zs, stream, gen, dev):
-    """GQA 64/8, D 128, one query token, compressed vs dense KV.
+    """Benchmark config 5: GQA 64/8, D 128, one query token, compressed vs dense KV.
     B=64 at T=32k is left out: one K tensor (2.15 G elements) exceeds the int32
     stream offsets of the format."""
     import zipserv_asplos26_amd.attention as za
@@ -202,7 +202,7 @@ def bench_attention(torch, zs, stream, gen, dev):
 
 
 def bench_kv(torch, zs, dev, gen):
-    """KV-cache compress / decompress throughput (GB/s of
+    """Benchmark config 4: KV-cache compress / decompress throughput (GB/s of
     original bytes), ratio and bit-exact recovery, by_kv_head layout, for the
     canonical streams and the re-tiled layout."""
     import zipserv_asplos26_amd.attention as za
@@ -338,7 +338,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1 "
-                          "(multi-GPU sharding is design-only, see DESIGN.md)"}))
+                          "(multi-GPU sharding is a design note, not a run mode)"}))
         sys.exit(2)
     import torch
 
@@ -388,7 +388,7 @@ def main():
     stream = torch.cuda.Stream()
 
     # Split-K per (shape, N): the reference sweeps Split_K in {1, 2, 4}
-    # (BASELINE config 2); the fastest on this GPU is kept for the step.
+    # (benchmark config 2); the fastest on this GPU is kept for the step.
     splits, wss = {}, {}
     for si, (name, M, K) in enumerate(SHAPES):
         for N in NS:
@@ -499,7 +499,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "llama3-8b-projections ZipGEMM sweep (BASELINE config 2)",
+            "workload": "llama3-8b-projections ZipGEMM sweep (benchmark config 2)",
             "shapes": {n: [m, k] for n, m, k in SHAPES},
             "N": NS,
             "split_k": "per (shape, N), fastest of 1/2/4 (see per_launch)",

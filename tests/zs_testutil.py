@@ -18,7 +18,7 @@ def weights_bf16(rng, shape, std=0.02, outlier_frac=0.0, outlier_scale=30.0):
 
 
 def kv_bf16(rng, batch, tokens, heads, dim):
-    """KV ~ N(0,1) * per-(head, channel) lognormal(0,1) scales."""
+    """KV ~ N(0,1) * per-(head, channel) lognormal(0,1) scales (benchmark config 4)."""
     scales = np.exp(rng.standard_normal((1, 1, heads, dim))).astype(np.float32)
     x = rng.standard_normal((batch, tokens, heads, dim), dtype=np.float32) * scales
     return zo.f32_to_bf16(x)
