@@ -95,9 +95,18 @@ def build(force: bool = False) -> str:
 
 
 def lib() -> C.CDLL:
-    """Load libzipserv.so; raise if it has not been built."""
+    """Load libzipserv.so; raise if it has not been built.
+
+    torch is imported first when it is installed: torch's wheel ships its own
+    HIP runtime under another file name, and the library must bind to that
+    same runtime (one per process) rather than pull in /opt/rocm's copy
+    before torch loads its own."""
     global _lib
     if _lib is None:
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(
                 f"libzipserv.so not found at {LIB_PATH}; build it with "
