@@ -109,6 +109,27 @@ def test_retiled_zipgemm_equals_canonical(torch_cuda, M, K, N):
     assert err <= 1e-2
 
 
+@pytest.mark.parametrize("N", [1, 7, 16])
+def test_retiled_zipgemm_two_bands_per_wave(torch_cuda, N):
+    # M / 16 >= 768 selects two bands per wave.  Per band the summation order
+    # is unchanged, so the result is bit-identical to the canonical kernel.
+    torch = torch_cuda
+    rng = np.random.default_rng(501 + N)
+    M, K = 64 * 193, 256
+    W = weights_bf16(rng, (M, K), outlier_frac=0.01)
+    X = zo.f32_to_bf16(rng.standard_normal((N, K), dtype=np.float32))
+    c = upload(zo.compress(W))
+    r = zs.retile(c)
+    x = to_torch_bf16(X)
+    Yc = zs.zipgemm(c, x)
+    Yr = zs.zipgemm(r, x)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_torch_bf16(Yr), from_torch_bf16(Yc))
+    ref = zo.gemm_f32(W, X)
+    y = zo.bf16_to_f32(from_torch_bf16(Yr))
+    assert np.abs(y - ref).max() / np.abs(ref).max() <= 1e-2
+
+
 @pytest.mark.parametrize("N,split_k", [(20, 1), (64, 1), (128, 1), (40, 2)])
 def test_retiled_zipgemm_large_grid(torch_cuda, N, split_k):
     # M / 64 * split_k >= 384 selects the two-phase 64-row kernel

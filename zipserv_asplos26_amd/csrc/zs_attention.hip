@@ -290,7 +290,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnParams p) {
     r_stage(NXT, RN, MN);                                                               \
     ZR_ISSUE(ZR_CLAMP((J) + 4, I), I, RC, MC);                                          \
     u32x4 a0_, a1_;                                                                     \
-    if (cm_.nch <= kExpChunks)                                                          \
+    if (r_staged(cm_))                                                                  \
       r_decode(RT, (I) < 2 ? RT.e1 : e1v, cs_.r, (const uint8_t*)(CUR), cm_.rel, a0_, a1_); \
     else                                                                                \
       r_decode(RT, (I) < 2 ? RT.e1 : e1v, cs_.r, ((I) < 2 ? p.kexp : p.vexp) + cm_.e0,  \

@@ -155,46 +155,63 @@ __device__ __forceinline__ void r_decode(const RTables& T, const uint4* e1, cons
 
 // ---------------------------------------------------------------------------
 // Record fetch: the fixed part straight into registers, the outlier bytes as
-// up to kExpChunks 16-byte chunks (lane l: chunk l) bound for a wave-private
-// LDS stage.  A record with more outlier bytes than that (over ~23% outliers)
-// is decoded with its outlier windows read from global memory.
+// up to kExpWords dwords (lane l: dword l, 4 bytes per lane so the load
+// returns 256 B, not 1 KB) bound for a wave-private LDS stage.  A record with
+// more outlier bytes than that (over ~24% outliers) is decoded with its
+// outlier windows read from global memory.
 // ---------------------------------------------------------------------------
+constexpr int kExpWords = kExpChunks * 4;
+
 struct RStage {
   RecRegs r;
-  u32x4 ex;
+  uint32_t ex;
 };
 struct RMeta {
-  int e0;    // first outlier byte of the record (stream offset)
-  int rel;   // e0 - first staged byte
-  int nch;   // staged chunks (> kExpChunks: decode from global memory)
+  int e0;   // first outlier byte of the record (stream offset)
+  int rel;  // e0 - first staged byte
+  int nw;   // staged dwords (> kExpWords: decode from global memory)
 };
 
-__device__ __forceinline__ void r_issue(const uint8_t* fixed, const uint8_t* exps, int64_t rec,
-                                        int e0, int e1, RStage& s, RMeta& mt) {
+__device__ __forceinline__ bool r_staged(const RMeta& mt) { return mt.nw <= kExpWords; }
+
+// Fixed part of record `rec` (no dependency on the outlier offsets).
+__device__ __forceinline__ void r_issue_fixed(const uint8_t* fixed, int64_t rec, RStage& s) {
   const int l = lane_id();
   const uint8_t* f = fixed + rec * kRecBytes;
   s.r.sm = *reinterpret_cast<const u32x4*>(f + 16 * l);
   s.r.p32 = *reinterpret_cast<const uint32_t*>(f + kRecP32 + 4 * l);
   s.r.p16 = *reinterpret_cast<const uint16_t*>(f + kRecP16 + 2 * l);
-  const int ea0 = e0 & ~15;
-  const int nch = (e1 - ea0 + 15) >> 4;
+}
+
+// Outlier bytes [e0, e1) of a record, as dwords from e0 & ~3.
+__device__ __forceinline__ void r_issue_exps(const uint8_t* exps, int e0, int e1, RStage& s,
+                                             RMeta& mt) {
+  const int l = lane_id();
+  const int ea0 = e0 & ~3;
+  const int nw = (e1 - ea0 + 3) >> 2;
   mt.e0 = e0;
   mt.rel = e0 - ea0;
-  mt.nch = nch;
-  s.ex = *reinterpret_cast<const u32x4*>(exps + ea0 + (l < nch ? 16 * l : 0));
+  mt.nw = nw;
+  s.ex = *reinterpret_cast<const uint32_t*>(exps + ea0 + (l < nw ? 4 * l : 0));
+}
+
+__device__ __forceinline__ void r_issue(const uint8_t* fixed, const uint8_t* exps, int64_t rec,
+                                        int e0, int e1, RStage& s, RMeta& mt) {
+  r_issue_fixed(fixed, rec, s);
+  r_issue_exps(exps, e0, e1, s, mt);
 }
 
 // Records whose outlier bytes exceed the stage are decoded from global memory
-// and are not staged (the stage holds kExpChunks chunks).
+// and are not staged (the stage holds kExpWords dwords).
 __device__ __forceinline__ void r_stage(uint8_t* st, const RStage& s, const RMeta& mt) {
   const int l = lane_id();
-  if (mt.nch <= kExpChunks && l < mt.nch) *reinterpret_cast<u32x4*>(st + 16 * l) = s.ex;
+  if (r_staged(mt) && l < mt.nw) *reinterpret_cast<uint32_t*>(st + 4 * l) = s.ex;
 }
 
 __device__ __forceinline__ void r_decode_staged(const RTables& T, const RStage& s,
                                                 const RMeta& mt, const uint8_t* st,
                                                 const uint8_t* exps, u32x4& o0, u32x4& o1) {
-  if (mt.nch <= kExpChunks)
+  if (r_staged(mt))
     r_decode(T, T.e1, s.r, st, mt.rel, o0, o1);
   else
     r_decode(T, T.e1, s.r, exps + mt.e0, 0, o0, o1);

@@ -240,108 +240,115 @@ __global__ __launch_bounds__(256) void rdecompress_kernel(const uint8_t* fixed,
 }
 
 // ---------------------------------------------------------------------------
-// ZipGEMM over the re-tiled layout.  Workgroup = WAVES waves on one 16-row
-// band x one split-K slice x 16*NB output columns; wave w takes K tiles
-// kb0+w, kb0+w+WAVES, ...  Records are fetched three tiles ahead into a
-// register ring, their outlier bytes staged one tile ahead.
+// ZipGEMM over the re-tiled layout for N <= 16.  Workgroup = WAVES waves on F
+// consecutive 16-row bands x one split-K slice; wave w takes K tiles kb0+w,
+// kb0+w+WAVES, ... of all F bands, so each X fragment it loads feeds F
+// records (X bytes per record / F).  Records are fetched three tiles ahead
+// into a register ring, their outlier bytes staged one tile ahead, X one
+// tile ahead.
 // ---------------------------------------------------------------------------
-template <int NB, int WAVES>
+template <int F, int WAVES>
 struct RGemmSmem {
-  static constexpr int kMain = (int)sizeof(RTables) + WAVES * 3 * kExpStage;
-  static constexpr int kRed = (WAVES / 2) * NB * 64 * 16;
+  static constexpr int kMain = (int)sizeof(RTables) + WAVES * 3 * F * kExpStage;
+  static constexpr int kRed = (WAVES / 2) * F * 64 * 16;
   static constexpr int kBytes = kMain > kRed ? kMain : kRed;
 };
 
-template <int NB, int WAVES>
+template <int F, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
                                                            const uint8_t* exps,
                                                            const int32_t* eoff, int start_exp,
                                                            const uint16_t* X, uint16_t* Y, int M,
                                                            int N, int K, int kb_per_split) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[RGemmSmem<NB, WAVES>::kBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[RGemmSmem<F, WAVES>::kBytes];
   RTables& T = *reinterpret_cast<RTables*>(smem);
   build_r_tables(T, start_exp, threadIdx.x, blockDim.x);
   __syncthreads();
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
-  uint8_t* stage0 = smem + sizeof(RTables) + w * 3 * kExpStage;
-  uint8_t* stage1 = stage0 + kExpStage;
-  uint8_t* stage2 = stage1 + kExpStage;
-  const int band = blockIdx.x;
+  // stage s of band f: smem + sizeof(RTables) + ((w * 3 + s) * F + f) * kExpStage
+  uint8_t* stg = smem + sizeof(RTables) + w * 3 * F * kExpStage;
+  const int bands = M >> 4;
+  const int band0 = blockIdx.x * F;
   const int split = blockIdx.y;
-  const int n0 = blockIdx.z * NB * 16;
   const int KT = K >> 6;
   const int kb0 = split * kb_per_split;
   const int kb1 = min(kb0 + kb_per_split, KT);
   const int cnt = kb1 - kb0 > w ? (kb1 - kb0 - w + WAVES - 1) / WAVES : 0;
-  const int64_t rec0 = (int64_t)band * KT + kb0 + w;  // record of this wave's tile 0
+  int64_t rec0[F];  // record of this wave's tile 0, per band (past the end: last band)
+#pragma unroll
+  for (int f = 0; f < F; ++f) rec0[f] = (int64_t)min(band0 + f, bands - 1) * KT + kb0 + w;
 
-  const uint16_t* xrow[NB];
+  const uint16_t* xrow = X + (int64_t)min(l & 15, N - 1) * K + 8 * (l >> 4);
+  f32x4 acc[F];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int n = min(n0 + nb * 16 + (l & 15), N - 1);
-    xrow[nb] = X + (int64_t)n * K + 8 * (l >> 4);
-  }
-  f32x4 acc[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int f = 0; f < F; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int c0 = 0; c0 < cnt; c0 += 64) {
     const int n = min(cnt - c0, 64);
     const int last = n - 1;
-    // lane i: outlier offsets of tile c0 + i (clamped to the chunk)
-    const int64_t ri = rec0 + (int64_t)(c0 + min(l, last)) * WAVES;
-    const int oe0 = eoff[ri], oe1 = eoff[ri + 1];
-    // X fragments are loaded one tile ahead (an L2 hit); records three ahead.
-    RStage R0, R1, R2;
-    RMeta M0, M1, M2;
-    bf16x8 xc[2][NB], xn[2][NB];
-#define RZ_LOADX(J, DST)                                                            \
-  {                                                                                 \
-    const int kk_ = (kb0 + w + (c0 + (J)) * WAVES) * 64;                            \
-    _Pragma("unroll") for (int h_ = 0; h_ < 2; ++h_)                                \
-      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_)                          \
-        DST[h_][nb_] = *reinterpret_cast<const bf16x8*>(xrow[nb_] + kk_ + 32 * h_); \
+    // lane i: outlier offsets of tile c0 + i (clamped to the chunk), per band
+    int oe0[F], oe1[F];
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+      const int64_t ri = rec0[f] + (int64_t)(c0 + min(l, last)) * WAVES;
+      oe0[f] = eoff[ri];
+      oe1[f] = eoff[ri + 1];
+    }
+    RStage R0[F], R1[F], R2[F];
+    RMeta M0[F], M1[F], M2[F];
+    bf16x8 xc[2], xn[2];
+#define RZ_LOADX(J, DST)                                                          \
+  {                                                                               \
+    const int kk_ = (kb0 + w + (c0 + (J)) * WAVES) * 64;                          \
+    DST[0] = *reinterpret_cast<const bf16x8*>(xrow + kk_);                        \
+    DST[1] = *reinterpret_cast<const bf16x8*>(xrow + kk_ + 32);                   \
   }
-#define RZ_ISSUE(J, R, MT)                                                          \
-  {                                                                                 \
-    const int j_ = (J);                                                             \
-    r_issue(fixed, exps, rec0 + (int64_t)(c0 + j_) * WAVES,                         \
-            __builtin_amdgcn_readlane(oe0, j_), __builtin_amdgcn_readlane(oe1, j_), \
-            R, MT);                                                                 \
+#define RZ_ISSUE(J, R, MT)                                                              \
+  {                                                                                     \
+    const int j_ = (J);                                                                 \
+    _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_)                                    \
+      r_issue(fixed, exps, rec0[f_] + (int64_t)(c0 + j_) * WAVES,                       \
+              __builtin_amdgcn_readlane(oe0[f_], j_), __builtin_amdgcn_readlane(oe1[f_], j_), \
+              R[f_], MT[f_]);                                                           \
   }
-#define RZ_STEP(J, CUR, NXT, RC, MC, RN, MN)                                             \
-  {                                                                                      \
-    const RStage cs_ = RC;                                                               \
-    const RMeta cm_ = MC;                                                                \
-    _Pragma("unroll") for (int h_ = 0; h_ < 2; ++h_)                                     \
-      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) xc[h_][nb_] = xn[h_][nb_];    \
-    r_stage(NXT, RN, MN);                                                                \
-    RZ_ISSUE(min((J) + 3, last), RC, MC);                                                \
-    RZ_LOADX(min((J) + 1, last), xn);                                                    \
-    if ((J) < n) {                                                                       \
-      u32x4 a0_, a1_;                                                                    \
-      r_decode_staged(T, cs_, cm_, CUR, exps, a0_, a1_);                                 \
-      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                             \
-        acc[nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0_), xc[0][nb_],   \
-                                                           acc[nb_], 0, 0, 0);           \
-        acc[nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1_), xc[1][nb_],   \
-                                                           acc[nb_], 0, 0, 0);           \
-      }                                                                                  \
-    }                                                                                    \
+#define RZ_STAGE(S, R, MT)                                                     \
+  {                                                                            \
+    _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_)                           \
+      r_stage(stg + ((S) * F + f_) * kExpStage, R[f_], MT[f_]);                \
+  }
+#define RZ_STEP(J, SC, SN, RC, MC, RN, MN)                                                 \
+  {                                                                                        \
+    xc[0] = xn[0];                                                                         \
+    xc[1] = xn[1];                                                                         \
+    RZ_LOADX(min((J) + 1, last), xn);                                                      \
+    RZ_STAGE(SN, RN, MN);                                                                  \
+    if ((J) < n) {                                                                         \
+      _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_) {                                   \
+        u32x4 a0_, a1_;                                                                    \
+        r_decode_staged(T, RC[f_], MC[f_], stg + ((SC) * F + f_) * kExpStage, exps, a0_,   \
+                        a1_);                                                              \
+        acc[f_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0_), xc[0], acc[f_], \
+                                                          0, 0, 0);                        \
+        acc[f_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1_), xc[1], acc[f_], \
+                                                          0, 0, 0);                        \
+      }                                                                                    \
+    }                                                                                      \
+    RZ_ISSUE(min((J) + 3, last), RC, MC);                                                  \
   }
     RZ_ISSUE(0, R0, M0);
     RZ_ISSUE(min(1, last), R1, M1);
     RZ_ISSUE(min(2, last), R2, M2);
     RZ_LOADX(0, xn);
-    r_stage(stage0, R0, M0);
+    RZ_STAGE(0, R0, M0);
     for (int j = 0; j < n; j += 3) {
-      RZ_STEP(j, stage0, stage1, R0, M0, R1, M1);
-      RZ_STEP(j + 1, stage1, stage2, R1, M1, R2, M2);
-      RZ_STEP(j + 2, stage2, stage0, R2, M2, R0, M0);
+      RZ_STEP(j, 0, 1, R0, M0, R1, M1);
+      RZ_STEP(j + 1, 1, 2, R1, M1, R2, M2);
+      RZ_STEP(j + 2, 2, 0, R2, M2, R0, M0);
     }
 #undef RZ_STEP
+#undef RZ_STAGE
 #undef RZ_ISSUE
 #undef RZ_LOADX
   }
@@ -353,23 +360,23 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
   for (int half = WAVES / 2; half >= 1; half /= 2) {
     if (w >= half && w < 2 * half) {
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) red[((w - half) * NB + nb) * 64 + l] = acc[nb];
+      for (int f = 0; f < F; ++f) red[((w - half) * F + f) * 64 + l] = acc[f];
     }
     __syncthreads();
     if (w < half) {
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) acc[nb] += red[(w * NB + nb) * 64 + l];
+      for (int f = 0; f < F; ++f) acc[f] += red[(w * F + f) * 64 + l];
     }
     __syncthreads();
   }
   if (w == 0) {
     uint16_t* out = Y + (int64_t)split * M * N;
-    const int mrow = band * 16 + 4 * (l >> 4);
+    const int n = l & 15;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const f32x4 v = acc[nb];
-      const int n = n0 + nb * 16 + (l & 15);
-      if (n < N) {
+    for (int f = 0; f < F; ++f) {
+      const f32x4 v = acc[f];
+      if (n < N && band0 + f < bands) {
+        const int mrow = (band0 + f) * 16 + 4 * (l >> 4);
         const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
         const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
         *reinterpret_cast<uint2*>(out + (int64_t)n * M + mrow) = make_uint2(lo, hi);
@@ -380,46 +387,47 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
 
 // ---------------------------------------------------------------------------
 // ZipGEMM over the re-tiled layout for wider batches (N > 16).  Workgroup =
-// 4*PH waves on one 64-row tile (4 bands) x one split-K slice x 16*NB
-// columns; wave w decodes band w%4 of K tiles kb0 + PH*s + w/4 (PH
-// interleaved phases).  Each X tile (16*NB x 64) is loaded once per workgroup into LDS
-// and read by the four band waves of its phase, so X crosses L2 a quarter as
-// often as with 16-row workgroups.  Records are fetched two steps ahead into
+// BANDS*PH waves on one 16*BANDS-row tile x one split-K slice x 16*NB
+// columns; wave w decodes band w%BANDS of K tiles kb0 + PH*s + w/BANDS (PH
+// interleaved phases).  Each X tile (16*NB x 64) is loaded once per
+// workgroup into LDS and read by the BANDS band waves of its phase, so X
+// crosses L2 1/BANDS as often as with 16-row workgroups.  Records are fetched two steps ahead into
 // registers, X tiles two steps ahead into registers and one step ahead into
 // a double-buffered LDS tile; one barrier per step.
 // ---------------------------------------------------------------------------
 constexpr int kXRow = 144;  // LDS pitch of an X tile row (128 B + 16 B pad)
 
-template <int NB, int PH>
+template <int NB, int BANDS, int PH>
 struct RWideSmem {
   static constexpr int kX = PH * 2 * 16 * NB * kXRow;   // [phase][buffer] tiles
-  static constexpr int kStages = 4 * PH * 2 * kExpStage;
+  static constexpr int kStages = BANDS * PH * 2 * kExpStage;
   static constexpr int kMain = (int)sizeof(RTables) + kStages + kX;
-  static constexpr int kRed = (PH - 1) * 4 * NB * 64 * 16;
+  static constexpr int kRed = (PH - 1) * BANDS * NB * 64 * 16;
   static constexpr int kBytes = kMain > kRed ? kMain : kRed;
 };
 
-template <int NB, int PH>
-__global__ __launch_bounds__(PH * 256) void rgemm_wide_kernel(const uint8_t* fixed,
+template <int NB, int BANDS, int PH>
+__global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8_t* fixed,
                                                               const uint8_t* exps,
                                                               const int32_t* eoff, int start_exp,
                                                               const uint16_t* X, uint16_t* Y,
                                                               int M, int N, int K,
                                                               int kb_per_split) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[RWideSmem<NB, PH>::kBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[RWideSmem<NB, BANDS, PH>::kBytes];
   RTables& T = *reinterpret_cast<RTables*>(smem);
   build_r_tables(T, start_exp, threadIdx.x, blockDim.x);
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
-  const int q = w & 3, p = w >> 2;
-  const int t = threadIdx.x & 255;  // thread index within the phase
+  const int q = w % BANDS, p = w / BANDS;
+  const int t = threadIdx.x % (BANDS * 64);  // thread index within the phase
   uint8_t* stage0 = smem + sizeof(RTables) + w * 2 * kExpStage;
   uint8_t* stage1 = stage0 + kExpStage;
-  uint8_t* xbase = smem + sizeof(RTables) + RWideSmem<NB, PH>::kStages + p * 2 * 16 * NB * kXRow;
+  uint8_t* xbase =
+      smem + sizeof(RTables) + RWideSmem<NB, BANDS, PH>::kStages + p * 2 * 16 * NB * kXRow;
   uint8_t* xb0 = xbase;
   uint8_t* xb1 = xbase + 16 * NB * kXRow;
-  const int band = blockIdx.x * 4 + q;
+  const int band = blockIdx.x * BANDS + q;
   const int split = blockIdx.y;
   const int n0 = blockIdx.z * NB * 16;
   const int KT = K >> 6;
@@ -433,13 +441,14 @@ __global__ __launch_bounds__(PH * 256) void rgemm_wide_kernel(const uint8_t* fix
   auto tile_of = [&](int j) { return min(kb0 + PH * j + p, kb1 - 1); };
   const int64_t rowrec = (int64_t)band * KT;
 
-  // X tile loads of this thread: chunk c = t + 256 i, row c/8, 16-byte column c%8.
-  constexpr int kXC = (NB + 1) / 2;  // chunks per thread (NB = 1: threads 0..127)
+  // X tile loads of this thread: chunk c = t + 64*BANDS*i, row c/8, 16-byte
+  // column c%8 (128*NB chunks per tile; threads past them load and drop).
+  constexpr int kXC = (2 * NB + BANDS - 1) / BANDS;  // chunks per thread
   const uint16_t* xsrc[kXC];
   int xdst[kXC];
 #pragma unroll
   for (int i = 0; i < kXC; ++i) {
-    const int c = t + 256 * i;
+    const int c = t + 64 * BANDS * i;
     const int row = min(c >> 3, 16 * NB - 1), cc = c & 7;
     xsrc[i] = X + (int64_t)min(n0 + row, N - 1) * K + 8 * cc;
     xdst[i] = c < 128 * NB ? row * kXRow + 16 * cc : -1;
@@ -475,7 +484,8 @@ __global__ __launch_bounds__(PH * 256) void rgemm_wide_kernel(const uint8_t* fix
   auto xwrite = [&](uint8_t* xb, const u32x4 (&XR)[kXC]) {
 #pragma unroll
     for (int i = 0; i < kXC; ++i)
-      if (NB > 1 || xdst[i] >= 0) *reinterpret_cast<u32x4*>(xb + xdst[i]) = XR[i];
+      if (2 * NB >= BANDS * (i + 1) || xdst[i] >= 0)
+        *reinterpret_cast<u32x4*>(xb + xdst[i]) = XR[i];
   };
 
   if (span == 0) {  // empty split-K slice (uniform per workgroup)
@@ -530,7 +540,7 @@ __global__ __launch_bounds__(PH * 256) void rgemm_wide_kernel(const uint8_t* fix
   f32x4* red = reinterpret_cast<f32x4*>(smem);
   if (p > 0) {
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) red[(((p - 1) * 4 + q) * NB + nb) * 64 + l] = acc[nb];
+    for (int nb = 0; nb < NB; ++nb) red[(((p - 1) * BANDS + q) * NB + nb) * 64 + l] = acc[nb];
   }
   __syncthreads();
   if (p == 0) {
@@ -540,7 +550,7 @@ __global__ __launch_bounds__(PH * 256) void rgemm_wide_kernel(const uint8_t* fix
     for (int nb = 0; nb < NB; ++nb) {
       f32x4 v = acc[nb];
 #pragma unroll
-      for (int pp = 1; pp < PH; ++pp) v += red[(((pp - 1) * 4 + q) * NB + nb) * 64 + l];
+      for (int pp = 1; pp < PH; ++pp) v += red[(((pp - 1) * BANDS + q) * NB + nb) * 64 + l];
       const int n = n0 + nb * 16 + (l & 15);
       if (n < N) {
         const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
@@ -583,24 +593,24 @@ static int r_grid(int64_t nrec, int waves_per_block) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, 256 * 64));
 }
 
-template <int NB>
+template <int F>
 static hipError_t launch_rgemm(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
                                const int32_t* eoff, int start_exp, const uint16_t* X,
                                uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split) {
-  constexpr int kWaves = NB <= 4 ? 8 : 4;
-  dim3 grid(M / 16, split_k, (N + NB * 16 - 1) / (NB * 16));
-  hipLaunchKernelGGL((rgemm_kernel<NB, kWaves>), grid, dim3(kWaves * 64), 0, st, fixed, exps,
+  constexpr int kWaves = 8;
+  dim3 grid((M / 16 + F - 1) / F, split_k, 1);
+  hipLaunchKernelGGL((rgemm_kernel<F, kWaves>), grid, dim3(kWaves * 64), 0, st, fixed, exps,
                      eoff, start_exp, X, Y, M, N, K, kb_per_split);
   return hipGetLastError();
 }
 
-template <int NB, int PH>
+template <int NB, int BANDS, int PH>
 static hipError_t launch_rwide(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
                                const int32_t* eoff, int start_exp, const uint16_t* X,
                                uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split) {
-  dim3 grid(M / 64, split_k, (N + NB * 16 - 1) / (NB * 16));
-  hipLaunchKernelGGL((rgemm_wide_kernel<NB, PH>), grid, dim3(PH * 256), 0, st, fixed, exps, eoff,
-                     start_exp, X, Y, M, N, K, kb_per_split);
+  dim3 grid(M / (16 * BANDS), split_k, (N + NB * 16 - 1) / (NB * 16));
+  hipLaunchKernelGGL((rgemm_wide_kernel<NB, BANDS, PH>), grid, dim3(BANDS * PH * 64), 0, st, fixed,
+                     exps, eoff, start_exp, X, Y, M, N, K, kb_per_split);
   return hipGetLastError();
 }
 
@@ -731,20 +741,25 @@ extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t
   hipError_t e;
   // N > 16: 64-row workgroups sharing each X tile through LDS; four K phases
   // per workgroup (16 waves) when the grid is small, two when it already
-  // covers the GPU.  N <= 16: 16-row workgroups (one band, 8 K phases).
+  // covers the GPU.  N <= 16: workgroups of 8 K phases over one or two bands.
   const int64_t wide_wgs = (int64_t)(M / 64) * split_k;
   if (nb >= 2) {
     const bool ph4 = wide_wgs < 384;
     if (nb <= 2)
-      e = ph4 ? launch_rwide<2, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split)
-              : launch_rwide<2, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+      e = ph4 ? launch_rwide<2, 4, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split)
+              : launch_rwide<2, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
     else if (nb <= 4)
-      e = ph4 ? launch_rwide<4, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split)
-              : launch_rwide<4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+      e = ph4 ? launch_rwide<4, 4, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split)
+              : launch_rwide<4, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
     else
-      e = launch_rwide<8, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+      e = launch_rwide<8, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
   } else {
-    e = launch_rgemm<1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+    // Two bands per wave halve the X bytes per record but also the grid:
+    // only when the grid stays above ~1.5 workgroups per CU.
+    if (M / 16 >= 768)
+      e = launch_rgemm<2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+    else
+      e = launch_rgemm<1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
   }
   if (e != hipSuccess) return (int)e;
   if (split_k > 1) {
