@@ -621,23 +621,25 @@ int64_t zso_compress_retiled(const uint16_t* a, int M, int K, int start_exp, uin
     eoff[0] = 0;
     for (int64_t r = 0; r < nrec; ++r) {
         uint8_t* f = fixed + r * ZSO_REC_BYTES;
-        unsigned B[64][2][3];
-        memset(B, 0, sizeof(B));
+        uint32_t C[64][2];
+        memset(C, 0, sizeof(C));
         for (int h = 0; h < 2; ++h)          /* outliers in (h, l, i) order */
             for (int l = 0; l < 64; ++l)
                 for (int i = 0; i < 8; ++i) {
-                    int row, col;
+                    int row, col, prow, pcol;
                     const uint16_t v = a[zso_rec_elem(M, K, r, h, l, i, &row, &col)];
+                    const uint16_t vp = a[zso_rec_elem(M, K, r, h, l, i ^ 1, &prow, &pcol)];
                     const unsigned e = (v >> 7) & 0xFFu;
                     const unsigned d = (e - st) & 0xFFu;
                     const unsigned code = (d >= 1 && d <= 7) ? d : 0;
-                    f[16 * l + 8 * h + i] = (uint8_t)(((v >> 8) & 0x80u) | (v & 0x7Fu));
-                    for (int p = 0; p < 3; ++p) B[l][h][p] |= ((code >> p) & 1u) << i;
-                    if (code == 0) exps[nout++] = (uint8_t)d;
+                    /* mantissa << 1 | sign of the pair partner (element i ^ 1) */
+                    f[16 * l + 8 * h + i] = (uint8_t)(((v & 0x7Fu) << 1) | ((vp >> 15) & 1u));
+                    C[l][h] |= (uint32_t)code << (3 * i);
+                    if (code == 0) exps[nout++] = (uint8_t)e;
                 }
         for (int l = 0; l < 64; ++l) {
-            const uint32_t w32 = B[l][0][0] | (B[l][0][1] << 8) | (B[l][0][2] << 16) | (B[l][1][0] << 24);
-            const uint16_t w16 = (uint16_t)(B[l][1][1] | (B[l][1][2] << 8));
+            const uint32_t w32 = C[l][0] | (C[l][1] << 24);
+            const uint16_t w16 = (uint16_t)(C[l][1] >> 8);
             memcpy(f + 1024 + 4 * l, &w32, 4);
             memcpy(f + 1280 + 2 * l, &w16, 2);
         }
@@ -659,16 +661,15 @@ void zso_decompress_retiled(const uint8_t* fixed, const uint8_t* exps, const int
                 uint16_t w16;
                 memcpy(&w32, f + 1024 + 4 * l, 4);
                 memcpy(&w16, f + 1280 + 2 * l, 2);
-                const unsigned b1 = h ? (w32 >> 24) : (w32 & 0xFFu);
-                const unsigned b2 = h ? (w16 & 0xFFu) : ((w32 >> 8) & 0xFFu);
-                const unsigned b3 = h ? (unsigned)(w16 >> 8) : ((w32 >> 16) & 0xFFu);
+                const uint32_t c = h ? ((w32 >> 24) | ((uint32_t)w16 << 8)) : (w32 & 0xFFFFFFu);
                 for (int i = 0; i < 8; ++i) {
-                    const unsigned code = ((b1 >> i) & 1u) | (((b2 >> i) & 1u) << 1) | (((b3 >> i) & 1u) << 2);
-                    const unsigned s = f[16 * l + 8 * h + i];
-                    const unsigned e = code ? ((st + code) & 0xFFu) : ((st + exps[k++]) & 0xFFu);
+                    const unsigned code = (c >> (3 * i)) & 7u;
+                    const unsigned e = code ? ((st + code) & 0xFFu) : exps[k++];
+                    const unsigned s = f[16 * l + 8 * h + i];            /* own mantissa */
+                    const unsigned sp = f[16 * l + 8 * h + (i ^ 1)];     /* holds own sign */
                     int row, col;
                     out[zso_rec_elem(M, K, r, h, l, i, &row, &col)] =
-                        (uint16_t)(((s & 0x80u) << 8) | (e << 7) | (s & 0x7Fu));
+                        (uint16_t)(((sp & 1u) << 15) | (e << 7) | (s >> 1));
                 }
             }
     }

@@ -99,12 +99,12 @@ void zso_decode_attention_f64(const uint16_t* q, const uint16_t* k, const uint16
 /* record r = band*(K/64) + kt covers rows 16*band..+15, cols 64*kt..+63.    */
 /* Element (h, l, i) of a record (half h < 2, lane l < 64, i < 8) is row     */
 /* 16*band + l%16, col 64*kt + 32*h + 8*(l/16) + i.  Fixed part, 1408 B per  */
-/* record: byte 16*l + 8*h + i = sign|mantissa byte of (h,l,i); bytes        */
-/* 1024 + 4*l.. = u32 (B1(0,l) | B2(0,l)<<8 | B3(0,l)<<16 | B1(1,l)<<24);    */
-/* bytes 1280 + 2*l.. = u16 (B2(1,l) | B3(1,l)<<8), Bp(h,l) bit i = bit p-1  */
-/* of the 3-bit code of (h,l,i) (0 = outlier, else exponent start+code).     */
-/* Exponent stream: for each outlier, in (h, l, i) order, the byte           */
-/* (exponent - start_exp) mod 256, at exps[eoff[r] + k]; eoff has           */
+/* record: byte 16*l + 8*h + i = (mantissa(h,l,i) << 1) | sign(h,l,i^1)     */
+/* (the sign bit is the pair partner's); bytes 1024 + 4*l.. = u32            */
+/* (C(0,l) | C(1,l) << 24); bytes 1280 + 2*l.. = u16 (C(1,l) >> 8), where    */
+/* C(h,l) = sum_i code(h,l,i) << 3i and code 0 = outlier, else exponent      */
+/* start + code (mod 256).  Exponent stream: for each outlier, in (h, l, i)  */
+/* order, its exponent byte, at exps[eoff[r] + k]; eoff has                  */
 /* num_records + 1 cumulative entries.                                       */
 /* ------------------------------------------------------------------------ */
 #define ZSO_REC_BYTES 1408

@@ -213,3 +213,4 @@ def test_retiled_rejects_bad_args(torch_cuda):
     assert L.zs_retiled_mm(*args(N=0)) == zs._lib.ZS_E_INVAL
     assert L.zs_retiled_mm(*args(sk=2)) == zs._lib.ZS_E_INVAL    # split-K needs a workspace
     assert L.zs_retiled_mm(*args(sk=3)) == zs._lib.ZS_E_INVAL    # more slices than K tiles
+    assert L.zs_retiled_mm(*args(sk=0)) == zs._lib.ZS_E_INVAL

@@ -44,32 +44,45 @@ def test_retiled_all_ones_known_answer():
     W = np.full((64, 64), 0x3F80, np.uint16)  # 1.0: exponent 127 -> window start 126, code 1
     r = zo.compress_retiled(W, 126)
     f = r.fixed.reshape(4, 1408)
-    assert np.all(f[:, :1024] == 0)                      # sign 0, mantissa 0
+    assert np.all(f[:, :1024] == 0)                      # mantissa 0, partner sign 0
     p32 = f[:, 1024:1280].copy().view(np.uint32)
     p16 = f[:, 1280:1408].copy().view(np.uint16)
-    assert np.all(p32 == 0xFF0000FF) and np.all(p16 == 0)  # plane 1 all ones, planes 2,3 zero
+    # eight 3-bit codes 1 per half: 0o11111111 = 0x249249
+    assert np.all(p32 == 0x49249249) and np.all(p16 == 0x2492)
     assert r.exps.size == 0 and np.all(r.eoff == 0)
 
 
+def _codes(f, lane, h):
+    w32 = int(f[1024 + 4 * lane:1028 + 4 * lane].view(np.uint32)[0])
+    w16 = int(f[1280 + 2 * lane:1282 + 2 * lane].view(np.uint16)[0])
+    c = ((w32 >> 24) | (w16 << 8)) if h else (w32 & 0xFFFFFF)
+    return [(c >> (3 * i)) & 7 for i in range(8)]
+
+
 def test_retiled_single_outlier_placement():
-    rng = np.random.default_rng(7)
     W = np.full((128, 128), 0x3F80, np.uint16)
     row, col = 37, 101
     W[row, col] = 0xC4A5  # sign 1, exponent 137 (outside 127..133), mantissa 0x25
     r = zo.compress_retiled(W, 126)
     band, kt, h, lane, i = _lane_of(row, col)
     rec = band * 2 + kt
-    assert r.exps.tolist() == [(137 - 126) & 0xFF]
+    assert r.exps.tolist() == [137]                      # the raw exponent byte
     assert np.diff(r.eoff).tolist() == [1 if k == rec else 0 for k in range(16)]
     f = r.fixed.reshape(16, 1408)[rec]
-    assert f[16 * lane + 8 * h + i] == 0x80 | 0x25  # sign | mantissa
-    w32 = int(f[1024 + 4 * lane:1028 + 4 * lane].view(np.uint32)[0])
-    w16 = int(f[1280 + 2 * lane:1282 + 2 * lane].view(np.uint16)[0])
-    b1 = (w32 >> 24) if h else (w32 & 0xFF)
-    assert b1 == 0xFF & ~(1 << i)  # the outlier's code is 0: its plane-1 bit is clear
-    assert (w16 if h else (w32 >> 8) & 0xFFFF) == 0
+    assert f[16 * lane + 8 * h + i] == 0x25 << 1         # mantissa << 1, partner sign 0
+    assert f[16 * lane + 8 * h + (i ^ 1)] == 0x01        # partner: mantissa 0, this sign 1
+    assert _codes(f, lane, h) == [0 if k == i else 1 for k in range(8)]
+    assert _codes(f, lane, 1 - h) == [1] * 8
     np.testing.assert_array_equal(zo.decompress_retiled(r), W)
-    del rng
+
+
+def test_retiled_signs_follow_partner():
+    # every sign pattern of a pair, every mantissa, in-window and outlier
+    a = np.arange(1 << 16, dtype=np.uint32)
+    W = (a.astype(np.uint16)).reshape(1024, 64)
+    for st in (0, 120, 250):
+        r = zo.compress_retiled(W, st)
+        np.testing.assert_array_equal(zo.decompress_retiled(r), W)
 
 
 def test_retiled_exponent_wrap():
@@ -78,7 +91,7 @@ def test_retiled_exponent_wrap():
     W = (rng.integers(0, 7, (64, 64)) << 7).astype(np.uint16) | rng.integers(0, 128, (64, 64)).astype(np.uint16)
     W[5, 5] = 0x4000  # exponent 128: outlier
     r = zo.compress_retiled(W, 255)
-    assert r.exps.size == 1 and r.exps[0] == (128 - 255) & 0xFF
+    assert r.exps.size == 1 and r.exps[0] == 128
     np.testing.assert_array_equal(zo.decompress_retiled(r), W)
 
 
@@ -86,7 +99,7 @@ def test_retiled_all_outliers_and_zeros():
     rng = np.random.default_rng(4)
     Z = np.zeros((64, 128), np.uint16)
     r = zo.compress_retiled(Z, 126)      # exponent 0 is outside 127..133: all outliers
-    assert r.exps.size == Z.size and np.all(r.exps == (0 - 126) & 0xFF)
+    assert r.exps.size == Z.size and np.all(r.exps == 0)
     np.testing.assert_array_equal(zo.decompress_retiled(r), Z)
     X = normal_bf16(rng, (64, 128), std=1e-30)
     r = zo.compress_retiled(X, 10)

@@ -480,9 +480,10 @@ def zipgemm(c, x, split_k: int = 1, out=None, workspace=None):
     n = x.shape[0]
     if out is None:
         out = torch.empty((n, c.rows), dtype=torch.bfloat16, device=x.device)
+    retiled = isinstance(c, ZipservRetiled)
     if split_k > 1 and workspace is None:
         workspace = splitk_workspace(c, n, split_k)
-    if isinstance(c, ZipservRetiled):
+    if retiled:
         check("zs_retiled_mm",
               lib().zs_retiled_mm(_stream(), _dptr(c.fixed), _dptr(c.exps), _dptr(c.eoff),
                                   c.start_exp & 0xFF, _dptr(x), _dptr(out), c.rows, n, c.cols,

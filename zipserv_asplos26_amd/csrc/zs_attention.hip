@@ -45,7 +45,7 @@ template <int kMode>
 struct AttnLds {
   // per-workgroup decode tables, then per-wave stages and the V tile
   static constexpr int kTables = kMode == kModeCanon ? (int)sizeof(DecodeTables) + 256 * 16
-                                 : kMode == kModeRetiled ? (int)sizeof(RTables) + 256 * 16
+                                 : kMode == kModeRetiled ? (int)sizeof(RTables)
                                                          : 0;
   static constexpr int kWave = (kMode == kModeCanon ? 2 * kStBytes
                                 : kMode == kModeRetiled ? 2 * kExpStage : 0) + kVBytes;
@@ -121,9 +121,9 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnParams p) {
     build_decode_tables(T, p.k_start, threadIdx.x, blockDim.x);
     build_e1(e1v, p.v_start, threadIdx.x, blockDim.x);
   } else if constexpr (kMode == kModeRetiled) {
-    build_r_tables(RT, p.k_start, threadIdx.x, blockDim.x);
-    build_r_e1(e1v, p.v_start, threadIdx.x, blockDim.x);
+    build_r_tables(RT, threadIdx.x, blockDim.x);
   }
+  const RExp kex = r_exp(p.k_start), vex = r_exp(p.v_start);
   __syncthreads();
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -291,9 +291,9 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnParams p) {
     ZR_ISSUE(ZR_CLAMP((J) + 4, I), I, RC, MC);                                          \
     u32x4 a0_, a1_;                                                                     \
     if (r_staged(cm_))                                                                  \
-      r_decode(RT, (I) < 2 ? RT.e1 : e1v, cs_.r, (const uint8_t*)(CUR), cm_.rel, a0_, a1_); \
+      r_decode(RT, (I) < 2 ? kex : vex, cs_.r, (const uint8_t*)(CUR), cm_.rel, a0_, a1_);   \
     else                                                                                \
-      r_decode(RT, (I) < 2 ? RT.e1 : e1v, cs_.r, ((I) < 2 ? p.kexp : p.vexp) + cm_.e0,  \
+      r_decode(RT, (I) < 2 ? kex : vex, cs_.r, ((I) < 2 ? p.kexp : p.vexp) + cm_.e0,    \
                0, a0_, a1_);                                                            \
     consume((I), (c0 + (J)) >> 2, a0_, a1_);                                            \
   }

@@ -117,9 +117,10 @@ __global__ __launch_bounds__(1024) void rscan_kernel(const int32_t* counts, int6
   }
 }
 
-// Writes one record from the lane's 16 bf16 values and plane bytes.
+// Writes one record from the lane's 16 bf16 values and their code bit-planes
+// (Bp bit i = bit p-1 of the code of element i).
 __device__ __forceinline__ void emit_record(uint8_t* fixed, uint8_t* exps, int64_t rec,
-                                            int64_t ebase, uint32_t st, const u32x4 v[2],
+                                            int64_t ebase, const u32x4 v[2],
                                             const uint32_t b[2][3]) {
   const int l = lane_id();
   u32x4 sm;
@@ -130,19 +131,29 @@ __device__ __forceinline__ void emit_record(uint8_t* fixed, uint8_t* exps, int64
       uint32_t w = 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t x = (v[h][(4 * q + j) >> 1] >> (16 * (j & 1))) & 0xFFFFu;
-        w |= (((x >> 8) & 0x80u) | (x & 0x7Fu)) << (8 * j);
+        const int i = 4 * q + j;
+        const uint32_t x = (v[h][i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+        const uint32_t xp = (v[h][i >> 1] >> (16 * ((i & 1) ^ 1))) & 0xFFFFu;  // partner i^1
+        w |= (((x & 0x7Fu) << 1) | (xp >> 15)) << (8 * j);
       }
       sm[2 * h + q] = w;
     }
-  const uint32_t p32 = b[0][0] | (b[0][1] << 8) | (b[0][2] << 16) | (b[1][0] << 24);
-  const uint32_t p16 = b[1][1] | (b[1][2] << 8);
+  uint32_t c[2], n[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    c[h] = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      c[h] |= (((b[h][0] >> i) & 1u) | (((b[h][1] >> i) & 1u) << 1) | (((b[h][2] >> i) & 1u) << 2))
+              << (3 * i);
+    n[h] = 8 - __builtin_popcount(b[h][0] | b[h][1] | b[h][2]);
+  }
   uint8_t* f = fixed + rec * kRecBytes;
   *reinterpret_cast<u32x4*>(f + 16 * l) = sm;
-  *reinterpret_cast<uint32_t*>(f + kRecP32 + 4 * l) = p32;
-  *reinterpret_cast<uint16_t*>(f + kRecP16 + 2 * l) = (uint16_t)p16;
+  *reinterpret_cast<uint32_t*>(f + kRecP32 + 4 * l) = c[0] | (c[1] << 24);
+  *reinterpret_cast<uint16_t*>(f + kRecP16 + 2 * l) = (uint16_t)(c[1] >> 8);
   int rank0, rank1;
-  r_ranks(p32, p16, rank0, rank1);
+  r_scan(n[0], n[1], rank0, rank1);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     uint32_t fm = ~(b[h][0] | b[h][1] | b[h][2]) & 0xFFu;
@@ -151,7 +162,7 @@ __device__ __forceinline__ void emit_record(uint8_t* fixed, uint8_t* exps, int64
       const int i = __builtin_ctz(fm);
       fm &= fm - 1;
       const uint32_t x = (v[h][i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-      exps[o++] = (uint8_t)((((x >> 7) & 0xFFu) - st) & 0xFFu);
+      exps[o++] = (uint8_t)((x >> 7) & 0xFFu);
     }
   }
 }
@@ -171,7 +182,7 @@ __global__ __launch_bounds__(256) void remit_kernel(const uint16_t* a, int M, in
       v[h] = *reinterpret_cast<const u32x4*>(rec_src(a, K, rec, h));
       classify8(v[h], st, b[h][0], b[h][1], b[h][2]);
     }
-    emit_record(fixed, exps, rec, eoff[rec], st, v, b);
+    emit_record(fixed, exps, rec, eoff[rec], v, b);
   }
 }
 
@@ -206,7 +217,7 @@ __global__ __launch_bounds__(256) void remit_canon_kernel(Streams s, int start_e
       smb += tot;
       fb += 512 - tot;
     }
-    emit_record(fixed, exps, rec, eoff[rec], (uint32_t)start_exp & 0xFFu, v, b);
+    emit_record(fixed, exps, rec, eoff[rec], v, b);
   }
 }
 
@@ -219,7 +230,8 @@ __global__ __launch_bounds__(256) void rdecompress_kernel(const uint8_t* fixed,
                                                           uint16_t* out, int M, int K) {
   __shared__ RTables T;
   __shared__ __attribute__((aligned(16))) uint8_t stg[4][kExpStage];
-  build_r_tables(T, start_exp, threadIdx.x, blockDim.x);
+  build_r_tables(T, threadIdx.x, blockDim.x);
+  const RExp ex = r_exp(start_exp);
   __syncthreads();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
@@ -231,7 +243,7 @@ __global__ __launch_bounds__(256) void rdecompress_kernel(const uint8_t* fixed,
     r_issue(fixed, exps, rec, eoff[rec], eoff[rec + 1], s, mt);
     r_stage(stg[w], s, mt);
     u32x4 o0, o1;
-    r_decode_staged(T, s, mt, stg[w], exps, o0, o1);
+    r_decode_staged(T, ex, s, mt, stg[w], exps, o0, o1);
     const int64_t band = rec / KT, kt = rec % KT;
     uint16_t* dst = out + (band * 16 + (l & 15)) * (int64_t)K + kt * 64 + 8 * (l >> 4);
     *reinterpret_cast<u32x4*>(dst) = o0;
@@ -262,7 +274,8 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
                                                            int N, int K, int kb_per_split) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[RGemmSmem<F, WAVES>::kBytes];
   RTables& T = *reinterpret_cast<RTables*>(smem);
-  build_r_tables(T, start_exp, threadIdx.x, blockDim.x);
+  build_r_tables(T, threadIdx.x, blockDim.x);
+  const RExp ex = r_exp(start_exp);
   __syncthreads();
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -327,7 +340,7 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
     if ((J) < n) {                                                                         \
       _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_) {                                   \
         u32x4 a0_, a1_;                                                                    \
-        r_decode_staged(T, RC[f_], MC[f_], stg + ((SC) * F + f_) * kExpStage, exps, a0_,   \
+        r_decode_staged(T, ex, RC[f_], MC[f_], stg + ((SC) * F + f_) * kExpStage, exps, a0_, \
                         a1_);                                                              \
         acc[f_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0_), xc[0], acc[f_], \
                                                           0, 0, 0);                        \
@@ -415,7 +428,8 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
                                                               int kb_per_split) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[RWideSmem<NB, BANDS, PH>::kBytes];
   RTables& T = *reinterpret_cast<RTables*>(smem);
-  build_r_tables(T, start_exp, threadIdx.x, blockDim.x);
+  build_r_tables(T, threadIdx.x, blockDim.x);
+  const RExp ex = r_exp(start_exp);
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
@@ -511,7 +525,7 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
     issue((S) + 2, RC, MC);                                                          \
     if ((S) < cnt) {                                                                 \
       u32x4 a0_, a1_;                                                                \
-      r_decode_staged(T, cs_, cm_, CUR, exps, a0_, a1_);                             \
+      r_decode_staged(T, ex, cs_, cm_, CUR, exps, a0_, a1_);                         \
       _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                         \
         const uint8_t* bp_ = XCUR + brd + nb_ * 16 * kXRow;                          \
         const bf16x8 b0_ = *reinterpret_cast<const bf16x8*>(bp_);                    \
@@ -733,12 +747,12 @@ extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t
   if (split_k < 1 || split_k > KT) return ZS_E_INVAL;
   if (split_k > 1 && !ws) return ZS_E_INVAL;
   if ((int64_t)M * N * split_k > INT32_MAX * 2LL) return ZS_E_OVERFLOW;
-  const int kb_per_split = (KT - 1) / split_k + 1;
   hipStream_t st = (hipStream_t)stream;
-  uint16_t* out = split_k == 1 ? C : ws;
-  const int nb = (N + 15) / 16;
   const int se = (int)start_exp;
   hipError_t e;
+  const int kb_per_split = (KT - 1) / split_k + 1;
+  uint16_t* out = split_k == 1 ? C : ws;
+  const int nb = (N + 15) / 16;
   // N > 16: 64-row workgroups sharing each X tile through LDS; four K phases
   // per workgroup (16 waves) when the grid is small, two when it already
   // covers the GPU.  N <= 16: workgroups of 8 K phases over one or two bands.
