@@ -109,10 +109,11 @@ def test_retiled_zipgemm_equals_canonical(torch_cuda, M, K, N):
     assert err <= 1e-2
 
 
-@pytest.mark.parametrize("N", [1, 7, 16])
+@pytest.mark.parametrize("N", [1, 9, 16])
 def test_retiled_zipgemm_two_bands_per_wave(torch_cuda, N):
-    # M / 16 >= 768 selects two bands per wave.  Per band the summation order
-    # is unchanged, so the result is bit-identical to the canonical kernel.
+    # N > 8 with M / 16 >= 384 selects two bands per wave.  Per band the
+    # summation order is unchanged, so the result is bit-identical to the
+    # canonical kernel.
     torch = torch_cuda
     rng = np.random.default_rng(501 + N)
     M, K = 64 * 193, 256

@@ -768,9 +768,10 @@ extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t
     else
       e = launch_rwide<8, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
   } else {
-    // Two bands per wave halve the X bytes per record but also the grid:
-    // only when the grid stays above ~1.5 workgroups per CU.
-    if (M / 16 >= 768)
+    // Two bands per wave halve the X bytes per record (the cost that grows
+    // with N) but also the grid: for N > 8 once the grid keeps at least
+    // 192 workgroups.
+    if (N > 8 && M / 16 >= 384)
       e = launch_rgemm<2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
     else
       e = launch_rgemm<1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
