@@ -161,10 +161,10 @@ int zs_init_bf16_matrix_triple_bitmap_gpu(
 /* CDNA4 re-tiled layout (this library's device layout; no counterpart in   */
 /* the reference).  A lossless rearrangement of the canonical streams with  */
 /* the same size: one fixed 1408-byte record per 16x64 tile (record r =     */
-/* band * K/64 + kt) holding every element's sign|mantissa byte and the    */
-/* three code bit-planes in MFMA-lane order, plus a stream of outlier       */
-/* exponent bytes ((exponent - start_exp) mod 256) with num_records + 1    */
-/* int32 cumulative offsets.  `fixed` and `exps` must be 16-byte aligned    */
+/* band * K/64 + kt) holding every element's mantissa and sign bits and its */
+/* 3-bit exponent code in MFMA-lane order, plus a stream of the outliers'   */
+/* exponent bytes with num_records + 1 int32 cumulative offsets (layout in  */
+/* csrc/zs_rdecode.hpp).  `fixed` and `exps` must be 16-byte aligned    */
 /* and `exps` must keep ZS_STREAM_SLACK_BYTES readable bytes past its end.  */
 /* ---------------------------------------------------------------------- */
 int64_t zs_retiled_num_records(int M, int K);
