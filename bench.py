@@ -81,6 +81,27 @@ def timed(torch, stream, graphs, steps, warmup):
     return s.elapsed_time(e) / 1e3
 
 
+def timed_dist(torch, stream, graph, replays, warmup):
+    """Seconds of each of `replays` replays of `graph`, HIP events on `stream`."""
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
+    with torch.cuda.stream(stream):
+        ev[0].record(stream)
+        for i in range(replays):
+            graph.replay()
+            ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    return [ev[i].elapsed_time(ev[i + 1]) / 1e3 for i in range(replays)]
+
+
+def pct(v, q):
+    """q-th percentile (nearest rank) of a list."""
+    v = sorted(v)
+    return v[min(len(v) - 1, max(0, int(round(q / 100 * (len(v) - 1)))))]
+
+
 C3_SHAPES = [("qkv", 10240, 8192), ("o", 8192, 8192), ("gate", 28672, 8192), ("up", 28672, 8192),
              ("down", 8192, 28672)]
 C3_NS = [1, 8, 16, 32, 64, 128, 256]
@@ -297,38 +318,48 @@ def make_layer(torch, zs, gen, dev):
 
 
 def cpu_baseline(torch, layer, seed):
-    """Oracle (plain-C restatement, 1 thread) decode + fp32 GEMM of one layer at
-    N=16: the same work per launch as the GPU step's N=16 row, measured in the
-    metric's unit (effective TB/s)."""
+    """Oracle (plain-C restatement) decode + fp32 GEMM of one Llama-3-8B layer
+    at N=16 -- the same work per launch as the GPU step's N=16 row, in the
+    metric's unit (effective TB/s) -- on all the host cores this process may
+    use (decoder parallel over global tiles, GEMM over rows of W), with the
+    single-thread time of the same work beside it."""
     import numpy as np
 
     import oracle as zo
+    threads = int(os.environ.get("OMP_NUM_THREADS") or min(os.cpu_count() or 1, 16))
     rng = np.random.default_rng(seed)
-    total_bytes, t_dec, t_gemm, t_enc = 0, 0.0, 0.0, 0.0
+    total_bytes, t_enc = 0, 0.0
+    t = {"dec1": 0.0, "gemm1": 0.0, "decN": 0.0, "gemmN": 0.0}
     for name, M, K, w, c, r in layer:
         W = w.cpu().view(torch.int16).numpy().view(np.uint16)
         t0 = time.perf_counter()
         e = zo.compress(W, variant="sse")
         t_enc += time.perf_counter() - t0
         X = zo.f32_to_bf16(rng.standard_normal((16, K), dtype=np.float32))
-        t0 = time.perf_counter()
-        D = zo.decompress(e)
-        t1 = time.perf_counter()
-        zo.gemm_f32(D, X)
-        t2 = time.perf_counter()
-        t_dec += t1 - t0
-        t_gemm += t2 - t1
+        for tag, nt in (("1", 1), ("N", threads)):
+            t0 = time.perf_counter()
+            D = zo.decompress_mt(e, nt)
+            t1 = time.perf_counter()
+            zo.gemm_f32_mt(D, X, nt)
+            t2 = time.perf_counter()
+            t["dec" + tag] += t1 - t0
+            t["gemm" + tag] += t2 - t1
         total_bytes += 2 * M * K
+    sN = t["decN"] + t["gemmN"]
+    s1 = t["dec1"] + t["gemm1"]
     return {
-        "value": round(total_bytes / (t_dec + t_gemm) / 1e12, 6),
+        "value": round(total_bytes / sN / 1e12, 6),
         "unit": "TB/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": ("oracle zso_decompress + zso_gemm_f32 (fp32 accumulate) of one Llama-3-8B layer "
-                   "(qkv,o,gate,up,down) at N=16, single thread"),
-        "seconds": round(t_dec + t_gemm, 3),
-        "decompress_s": round(t_dec, 3),
-        "gemm_s": round(t_gemm, 3),
+        "sample": ("oracle zso_decompress_mt + zso_gemm_f32_mt (fp32 accumulate) of one "
+                   f"Llama-3-8B layer (qkv,o,gate,up,down) at N=16, {threads} threads"),
+        "seconds": round(sN, 3),
+        "decompress_s": round(t["decN"], 3),
+        "gemm_s": round(t["gemmN"], 3),
+        "single_thread": {"value": round(total_bytes / s1 / 1e12, 6), "unit": "TB/s",
+                          "seconds": round(s1, 3), "decompress_s": round(t["dec1"], 3),
+                          "gemm_s": round(t["gemm1"], 3)},
         "compress_sse_s": round(t_enc, 3),
         "compress_GBps": round(total_bytes / t_enc / 1e9, 3),
         "host_cpu": platform.processor() or platform.machine(),
@@ -434,7 +465,8 @@ def main():
         result_dense = step_bytes * args.steps / t_dense / 1e12
 
     # Per-(shape, N) kernel timing: `reps` launches in one graph, cycling
-    # through the resident layers, timed with events on the replay stream.
+    # through the resident layers, timed with events on the replay stream
+    # around each of 9 replays; zip_us is the median replay, p10/p90 beside it.
     per = []
     sum_alg_bytes, sum_kernel_s = 0.0, 0.0
     for si, (name, M, K) in enumerate(SHAPES):
@@ -443,7 +475,8 @@ def main():
                 for r in range(args.reps):
                     zs.zipgemm(layers[r % len(layers)][si][5], xs[(N, K)], split_k=splits[(si, N)],
                                out=outs[(N, M)], workspace=wss[(si, N)])
-            tz = timed(torch, stream, [capture(torch, stream, zrun)], 3, 1) / (3 * args.reps)
+            dz = [t / args.reps for t in timed_dist(torch, stream, capture(torch, stream, zrun), 9, 1)]
+            tz = pct(dz, 50)
             comp = layers[0][si][5].compressed_bytes
             sk = splits[(si, N)]
             alg = comp + 2 * N * K + 2 * N * M + (4 * sk * M * N if sk > 1 else 0)
@@ -456,14 +489,21 @@ def main():
             row = {"shape": name, "M": M, "K": K, "N": N, "kernel": kernel_name(N, M, sk),
                    "split_k": sk,
                    "canonical_us": round(tc * 1e6, 3),
-                   "zip_us": round(tz * 1e6, 3), "alg_bytes": alg,
+                   "zip_us": round(tz * 1e6, 3),
+                   "zip_us_p10": round(pct(dz, 10) * 1e6, 3),
+                   "zip_us_p90": round(pct(dz, 90) * 1e6, 3),
+                   "alg_bytes": alg,
                    "eff_TBps": round(2 * M * K / tz / 1e12, 3),
-                   "comp_TBps": round(alg / tz / 1e12, 3)}
+                   "comp_TBps": round(alg / tz / 1e12, 3),
+                   # MFMA use: dense-equivalent flops against the 2.5 PFLOP/s bf16 peak
+                   "TFLOPs": round(2 * M * N * K / tz / 1e12, 2),
+                   "mfma_frac": round(2 * M * N * K / tz / 2.5e15, 4)}
             if not args.no_dense:
                 def drun(si=si, N=N, M=M, K=K):
                     for r in range(args.reps):
                         torch.matmul(xs[(N, K)], layers[r % len(layers)][si][3].t(), out=outs[(N, M)])
-                td = timed(torch, stream, [capture(torch, stream, drun)], 3, 1) / (3 * args.reps)
+                td = pct([t / args.reps for t in
+                          timed_dist(torch, stream, capture(torch, stream, drun), 9, 1)], 50)
                 row["dense_us"] = round(td * 1e6, 2)
                 row["speedup"] = round(td / tz, 3)
             per.append(row)

@@ -50,6 +50,10 @@ def lib():
         L.zso_decompress.restype = C.c_int
         L.zso_decompress.argtypes = [p, C.c_int64, p, C.c_int64, p, p, p, p, C.c_int, C.c_int, C.c_int, p]
         L.zso_gemm_f32.argtypes = [p, p, C.c_int, C.c_int, C.c_int, p]
+        L.zso_decompress_mt.restype = C.c_int
+        L.zso_decompress_mt.argtypes = [p, C.c_int64, p, C.c_int64, p, p, p, p, C.c_int, C.c_int,
+                                        C.c_int, p, C.c_int]
+        L.zso_gemm_f32_mt.argtypes = [p, p, C.c_int, C.c_int, C.c_int, p, C.c_int]
         L.zso_gemm_splitk_bf16.argtypes = [p, p, C.c_int, C.c_int, C.c_int, C.c_int, p]
         L.zso_decode_attention_f64.argtypes = [p, p, p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                                p, C.c_double, p, p]
@@ -211,6 +215,31 @@ def decompress(e: Encoded, start_exp: int | None = None) -> np.ndarray:
     if rc != 0:
         raise ValueError("oracle decompress: stream index out of range")
     return out
+
+
+def decompress_mt(e: Encoded, threads: int = 0) -> np.ndarray:
+    """decompress() parallel over global tiles (CPU baseline; same output)."""
+    out = np.zeros((e.rows, e.cols), np.uint16)
+    sm = np.ascontiguousarray(e.sign_mantissa)
+    fu = np.ascontiguousarray(e.compressed_full)
+    rc = lib().zso_decompress_mt(_ptr(sm), sm.size, _ptr(fu), fu.size,
+                                 _ptr(e.bitmap1), _ptr(e.bitmap2), _ptr(e.bitmap3),
+                                 _ptr(e.tile_offsets_global), e.rows, e.cols, e.start_exp,
+                                 _ptr(out), int(threads))
+    if rc != 0:
+        raise ValueError("oracle decompress: stream index out of range")
+    return out
+
+
+def gemm_f32_mt(W: np.ndarray, X: np.ndarray, threads: int = 0) -> np.ndarray:
+    """gemm_f32() with each W row widened once, parallel over rows (same result)."""
+    W = np.ascontiguousarray(W, dtype=np.uint16)
+    X = np.ascontiguousarray(X, dtype=np.uint16)
+    M, K = W.shape
+    N = X.shape[0]
+    Y = np.zeros((N, M), np.float32)
+    lib().zso_gemm_f32_mt(_ptr(W), _ptr(X), M, N, K, _ptr(Y), int(threads))
+    return Y
 
 
 def gemm_f32(W: np.ndarray, X: np.ndarray) -> np.ndarray:

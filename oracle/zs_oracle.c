@@ -23,6 +23,7 @@
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+#include <omp.h>
 #include <tmmintrin.h> /* SSSE3 (_mm_shuffle_epi8) for the SIMD restatement */
 
 /* ------------------------------------------------------------------------ */
@@ -544,6 +545,69 @@ void zso_gemm_f32(const uint16_t* W, const uint16_t* X, int M, int N, int K, flo
     }
     free(xr);
     free(wr);
+}
+
+/* CPU baseline variants (same arithmetic, same summation order per output):
+ * the decoder parallel over global tiles, and a GEMM that widens each W row
+ * once and reuses it for all N columns, parallel over rows of W.  `threads`
+ * <= 0 uses every core OpenMP sees. */
+int zso_decompress_mt(const uint8_t* sm, int64_t sm_len, const uint16_t* full, int64_t full_len,
+                      const uint64_t* b1, const uint64_t* b2, const uint64_t* b3,
+                      const int32_t* tog, int M, int K, int start_exp, uint16_t* out,
+                      int threads) {
+    if (check_dims(M, K)) return -1;
+    init_tile_pos();
+    const int gtk = K / 64, ngt = (M / 64) * gtk;
+    int bad = 0;
+    if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for num_threads(threads) schedule(static) reduction(| : bad)
+    for (int g = 0; g < ngt; ++g) {
+        int64_t hi = tog[g * 2], fi = tog[g * 2 + 1];
+        const int grow = (g / gtk) * 64, gcol = (g % gtk) * 64;
+        for (int st = 0; st < 64 && !bad; ++st) {
+            const int64_t t = (int64_t)g * 64 + st;
+            const uint64_t w1 = b1[t], w2 = b2[t], w3 = b3[t], ind = w1 | w2 | w3;
+            const int r0 = grow + g_pos_row[st], c0 = gcol + g_pos_col[st];
+            for (int pos = 0; pos < 64; ++pos) {
+                const int64_t o = (int64_t)(r0 + pos / 8) * K + c0 + pos % 8;
+                if ((ind >> pos) & 1) {
+                    if (hi < 0 || hi >= sm_len) { bad = 1; break; }
+                    const uint8_t c = sm[hi++];
+                    const int code = (int)(((w3 >> pos) & 1) << 2 | ((w2 >> pos) & 1) << 1 | ((w1 >> pos) & 1));
+                    const uint8_t e = (uint8_t)(start_exp + code);
+                    out[o] = (uint16_t)(((c >> 7) & 1) << 15 | (uint16_t)e << 7 | (c & 0x7F));
+                } else {
+                    if (fi < 0 || fi >= full_len) { bad = 1; break; }
+                    out[o] = full[fi++];
+                }
+            }
+        }
+    }
+    return bad ? -1 : 0;
+}
+
+void zso_gemm_f32_mt(const uint16_t* W, const uint16_t* X, int M, int N, int K, float* Y,
+                     int threads) {
+    float* xf = (float*)malloc((size_t)N * K * sizeof(float));
+    for (int64_t i = 0; i < (int64_t)N * K; ++i) xf[i] = zso_bf16_to_f32(X[i]);
+    if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel num_threads(threads)
+    {
+        float* wr = (float*)malloc((size_t)K * sizeof(float));
+#pragma omp for schedule(static)
+        for (int m = 0; m < M; ++m) {
+            const uint16_t* w = W + (int64_t)m * K;
+            for (int k = 0; k < K; ++k) wr[k] = zso_bf16_to_f32(w[k]);
+            for (int n = 0; n < N; ++n) {
+                const float* xr = xf + (int64_t)n * K;
+                float acc = 0.f;
+                for (int k = 0; k < K; ++k) acc += wr[k] * xr[k];
+                Y[(int64_t)n * M + m] = acc;
+            }
+        }
+        free(wr);
+    }
+    free(xf);
 }
 
 void zso_gemm_splitk_bf16(const uint16_t* W, const uint16_t* X, int M, int N, int K, int S,

@@ -72,6 +72,15 @@ int zso_decompress(const uint8_t* sm, int64_t sm_len, const uint16_t* full, int6
 /* Y[n][m] = sum_k W[m][k] * X[n][k], fp32 accumulation in ascending k, result
  * kept in fp32 (no rounding) -- the closed form ZipGEMM must match
  * (csrc/L_Kernel.cuh:294-571 computes the same product, output [N][M]). */
+/* CPU-baseline variants, same results: decoder parallel over global tiles;
+ * GEMM with each W row widened once, parallel over rows (threads <= 0: all
+ * cores). */
+int zso_decompress_mt(const uint8_t* sm, int64_t sm_len, const uint16_t* full, int64_t full_len,
+                      const uint64_t* b1, const uint64_t* b2, const uint64_t* b3,
+                      const int32_t* tog, int M, int K, int start_exp, uint16_t* out,
+                      int threads);
+void zso_gemm_f32_mt(const uint16_t* W, const uint16_t* X, int M, int N, int K, float* Y,
+                     int threads);
 void zso_gemm_f32(const uint16_t* W, const uint16_t* X, int M, int N, int K, float* Y);
 /* Split-K model: csrc/L_Kernel.cuh:316-326 partitions K into ceil(NK/S) GT
  * blocks per split, each split's fp32 sum is rounded to bf16, then

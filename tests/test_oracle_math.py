@@ -126,3 +126,15 @@ def test_attention_special_cases():
     ko[0, 5, 0, 0] = 0x3F80
     out, _ = zo.decode_attention_f64(qo, ko, v)
     np.testing.assert_allclose(out[0, 0], zo.bf16_to_f32(v[0, 5, 0]).astype(np.float64), atol=1e-12)
+
+
+@pytest.mark.parametrize("threads", [1, 3, 0])
+def test_multithreaded_baseline_variants_match(threads):
+    # the CPU-baseline variants (parallel decoder, row-parallel GEMM) give the
+    # same bits as the single-threaded oracle functions
+    rng = np.random.default_rng(11)
+    W = weights_bf16(rng, (192, 320), outlier_frac=0.02)
+    X = normal_bf16(rng, (5, 320))
+    e = zo.compress(W)
+    np.testing.assert_array_equal(zo.decompress_mt(e, threads), W)
+    np.testing.assert_array_equal(zo.gemm_f32_mt(W, X, threads), zo.gemm_f32(W, X))
