@@ -235,7 +235,14 @@ typedef struct zs_kv_compressed {
  * int32 [batch]) or seqlen_k when cache_seqlens is NULL.  softmax_lse
  * (optional, [batch][num_heads] fp32) is the natural-log normaliser.
  * num_splits = 0 picks a split of the sequence across workgroups; splits > 1
- * need `workspace` of zs_decode_attention_workspace_bytes bytes. */
+ * need `workspace` of zs_decode_attention_workspace_bytes bytes.
+ * Layouts (flash.h:19-20): HEAD_MAJOR caches (row (b*Hkv + h)*head_stride +
+ * t) are decoded inside the attention kernel; TOKEN_MAJOR caches (row
+ * b*batch_stride + t*Hkv + h) run staged -- both are first decompressed into
+ * the front of `workspace`, which then needs zs_kv_staging_bytes(layout,
+ * rows, cols) for K and for V in addition (the same result, bit for bit).
+ * K and V must share one layout. */
+int64_t zs_kv_staging_bytes(int layout, int rows, int cols);
 int zs_decode_attention(void* stream, const uint16_t* q, const zs_kv_compressed_t* k,
                         const zs_kv_compressed_t* v, const int32_t* cache_seqlens, int seqlen_k,
                         int batch, int num_heads, int num_heads_k, int head_dim,

@@ -23,7 +23,8 @@ def _bf16_f32(a):
     return zo.bf16_to_f32(a).astype(np.float64)
 
 
-def _run(torch_cuda, B, T, Hkv, H, seqlens=None, splits=0, seed=0, q_zero=False, retiled=False):
+def _run(torch_cuda, B, T, Hkv, H, seqlens=None, splits=0, seed=0, q_zero=False, retiled=False,
+         layout="by_kv_head"):
     import zipserv_asplos26_amd.attention as za
     torch = torch_cuda
     rng = np.random.default_rng(seed)
@@ -34,8 +35,8 @@ def _run(torch_cuda, B, T, Hkv, H, seqlens=None, splits=0, seed=0, q_zero=False,
     if q_zero:
         q[:] = 0
     kd, vd, qd = to_torch_bf16(k), to_torch_bf16(v), to_torch_bf16(q)
-    ck = za.compress_kv(kd, retiled=retiled)
-    cv = za.compress_kv(vd, retiled=retiled)
+    ck = za.compress_kv(kd, layout=layout, retiled=retiled)
+    cv = za.compress_kv(vd, layout=layout, retiled=retiled)
     sl = None if seqlens is None else torch.tensor(seqlens, dtype=torch.int32, device="cuda")
     out, lse = za.flash_attn_with_kvcache_zipserv(
         qd.view(B, 1, H, D), ck, cv, Hkv, T, cache_seqlens=sl, num_splits=splits,
@@ -97,6 +98,22 @@ def test_attention_ragged_seqlens(torch_cuda, splits):
     _check(_run(torch_cuda, 4, 300, 8, 64, seqlens=seqlens, splits=splits, seed=3), seqlens)
 
 
+@pytest.mark.parametrize("retiled", [False, True])
+@pytest.mark.parametrize("B,T,Hkv,H,splits,seqlens", [
+    (1, 64, 8, 64, 1, None),
+    (2, 100, 8, 64, 0, None),     # T * Hkv not a multiple of 64: padded batch rows
+    (2, 1000, 8, 64, 3, None),
+    (2, 700, 2, 32, 5, None),     # GQA group 16
+    (2, 300, 4, 4, 2, None),      # MHA
+    (4, 300, 8, 64, 0, [300, 17, 0, 64]),
+])
+def test_attention_token_major(torch_cuda, retiled, B, T, Hkv, H, splits, seqlens):
+    # token-major caches (row b*batch_stride + t*Hkv + h) run staged: the
+    # result equals the dense kernel's bit for bit, and the oracle's
+    _check(_run(torch_cuda, B, T, Hkv, H, seqlens=seqlens, splits=splits, seed=11,
+                retiled=retiled, layout="token_major"), seqlens)
+
+
 def test_attention_single_token_returns_v(torch_cuda):
     # T = 1: softmax weight 1, out = V[0] exactly (bf16 in, bf16 out).
     q, k, v, out, *_ = _run(torch_cuda, 2, 1, 8, 64, splits=1, seed=5)
@@ -142,7 +159,11 @@ def test_attention_rejects_unsupported(torch_cuda):
     assert call(d, d, splits=2) == zs._lib.ZS_E_INVAL  # two splits need a workspace
     tm = za._lib.KVCompressed.from_buffer_copy(d)
     tm.layout = zs._lib.ZS_LAYOUT_TOKEN_MAJOR
-    assert call(tm, d) == zs._lib.ZS_E_UNSUPPORTED
+    assert call(tm, d) == zs._lib.ZS_E_UNSUPPORTED   # K and V layouts differ
+    assert call(tm, tm) == zs._lib.ZS_E_INVAL        # token-major needs staging workspace
+    assert L.zs_kv_staging_bytes(zs._lib.ZS_LAYOUT_TOKEN_MAJOR, 1024, 128) == 1024 * 128 * 2
+    assert L.zs_kv_staging_bytes(zs._lib.ZS_LAYOUT_HEAD_MAJOR, 1024, 128) == 0
+    assert L.zs_kv_staging_bytes(7, 1024, 128) == -1
     bad = za._lib.KVCompressed.from_buffer_copy(d)
     bad.head_stride_rows = 32
     assert call(bad, d) == zs._lib.ZS_E_INVAL

@@ -467,9 +467,45 @@ static int attn_common_checks(int batch, int heads, int heads_k, int head_dim, i
   return ZS_OK;
 }
 
+// Geometry of one compressed cache against the call: head-major rows are
+// ((b * Hkv + h) * head_stride + t), token-major rows b * batch_stride +
+// t * Hkv + h (bench_zipserv_decode_attention.py:337-354).
+static int kv_geometry_ok(int layout, int rows, int cols, int bsr, int hsr, int start_exp,
+                          int batch, int heads_k, int seqlen_k) {
+  if (layout != ZS_LAYOUT_HEAD_MAJOR && layout != ZS_LAYOUT_TOKEN_MAJOR) return ZS_E_UNSUPPORTED;
+  if (cols != kHeadDim || rows <= 0 || (rows % 64)) return ZS_E_INVAL;
+  if (hsr <= 0 || bsr != heads_k * hsr || (int64_t)bsr * batch > rows || hsr < seqlen_k)
+    return ZS_E_INVAL;
+  if (layout == ZS_LAYOUT_HEAD_MAJOR ? (hsr % 64) : (bsr % 64)) return ZS_E_INVAL;
+  if (start_exp < 0 || start_exp > 255) return ZS_E_INVAL;
+  return ZS_OK;
+}
+
+static size_t staging_bytes(int layout, int rows, int cols) {
+  if (layout != ZS_LAYOUT_TOKEN_MAJOR) return 0;
+  return ((size_t)rows * cols * 2 + 255) / 256 * 256;
+}
+
+// Token-major caches run staged: both caches are decompressed into the
+// workspace (dense [B][head_stride][Hkv][D] views of their rows) and the
+// attention kernel runs in its dense mode on them.
+static int attn_staged(hipStream_t st, AttnParams& p, const uint16_t* kd, const uint16_t* vd,
+                       int cap, void* workspace, size_t ws_bytes) {
+  p.kd = kd;
+  p.vd = vd;
+  p.cap = cap;
+  return attn_launch<kModeDense>(st, p, workspace, ws_bytes);
+}
+
 }  // namespace zs
 
 using namespace zs;
+
+extern "C" int64_t zs_kv_staging_bytes(int layout, int rows, int cols) {
+  if (rows <= 0 || cols <= 0) return -1;
+  if (layout != ZS_LAYOUT_HEAD_MAJOR && layout != ZS_LAYOUT_TOKEN_MAJOR) return -1;
+  return (int64_t)staging_bytes(layout, rows, cols);
+}
 
 extern "C" size_t zs_decode_attention_workspace_bytes(int batch, int num_heads, int head_dim,
                                                       int seqlen_k, int num_splits) {
@@ -495,14 +531,12 @@ extern "C" int zs_decode_attention(void* stream, const uint16_t* q, const zs_kv_
     if (!c->sign_mantissa || !c->compressed_full || !c->bitmap1 || !c->bitmap2 ||
         !c->bitmap3 || !c->tile_offsets_median || !c->tile_offsets_global)
       return ZS_E_INVAL;
-    if (c->layout != ZS_LAYOUT_HEAD_MAJOR) return ZS_E_UNSUPPORTED;
-    if (c->cols != kHeadDim || c->rows <= 0 || (c->rows % 64)) return ZS_E_INVAL;
-    if (c->head_stride_rows <= 0 || (c->head_stride_rows % 64) ||
-        c->batch_stride_rows != num_heads_k * c->head_stride_rows ||
-        (int64_t)c->batch_stride_rows * batch > c->rows || c->head_stride_rows < seqlen_k)
-      return ZS_E_INVAL;
-    if (c->start_exp < 0 || c->start_exp > 255) return ZS_E_INVAL;
+    const int g = kv_geometry_ok(c->layout, c->rows, c->cols, c->batch_stride_rows,
+                                 c->head_stride_rows, c->start_exp, batch, num_heads_k, seqlen_k);
+    if (g != ZS_OK) return g;
   }
+  if (k->layout != v->layout || k->head_stride_rows != v->head_stride_rows)
+    return ZS_E_UNSUPPORTED;
   AttnParams p{};
   auto streams = [](const zs_kv_compressed_t* c) {
     Streams s;
@@ -536,6 +570,26 @@ extern "C" int zs_decode_attention(void* stream, const uint16_t* q, const zs_kv_
   p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
   p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  if (k->layout == ZS_LAYOUT_TOKEN_MAJOR) {
+    const size_t sk = staging_bytes(k->layout, k->rows, k->cols);
+    const size_t sv = staging_bytes(v->layout, v->rows, v->cols);
+    if (!workspace || workspace_bytes < sk + sv) return ZS_E_INVAL;
+    uint16_t* kd = reinterpret_cast<uint16_t*>(workspace);
+    uint16_t* vd = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(workspace) + sk);
+    const zs_kv_compressed_t* src[2] = {k, v};
+    uint16_t* dst[2] = {kd, vd};
+    for (int i = 0; i < 2; ++i) {
+      const zs_kv_compressed_t* c = src[i];
+      const int e = zs_bf16_triple_bitmap_decompress(
+          stream, c->sign_mantissa, c->compressed_full, c->bitmap1, c->bitmap2, c->bitmap3,
+          c->tile_offsets_median, c->tile_offsets_global, c->max_high_freq_count,
+          c->max_full_count, (uint8_t)c->start_exp, dst[i], c->rows, c->cols);
+      if (e != ZS_OK) return e;
+    }
+    return attn_staged((hipStream_t)stream, p, kd, vd, k->head_stride_rows,
+                       reinterpret_cast<uint8_t*>(workspace) + sk + sv,
+                       workspace_bytes - sk - sv);
+  }
   return attn_launch<kModeCanon>((hipStream_t)stream, p, workspace, workspace_bytes);
 }
 
@@ -555,14 +609,12 @@ extern "C" int zs_decode_attention_retiled(void* stream, const uint16_t* q,
     if (!c->fixed || !c->exps || !c->eoff) return ZS_E_INVAL;
     if ((reinterpret_cast<uintptr_t>(c->fixed) & 15) || (reinterpret_cast<uintptr_t>(c->exps) & 15))
       return ZS_E_INVAL;
-    if (c->layout != ZS_LAYOUT_HEAD_MAJOR) return ZS_E_UNSUPPORTED;
-    if (c->cols != kHeadDim || c->rows <= 0 || (c->rows % 64)) return ZS_E_INVAL;
-    if (c->head_stride_rows <= 0 || (c->head_stride_rows % 64) ||
-        c->batch_stride_rows != num_heads_k * c->head_stride_rows ||
-        (int64_t)c->batch_stride_rows * batch > c->rows || c->head_stride_rows < seqlen_k)
-      return ZS_E_INVAL;
-    if (c->start_exp < 0 || c->start_exp > 255) return ZS_E_INVAL;
+    const int g = kv_geometry_ok(c->layout, c->rows, c->cols, c->batch_stride_rows,
+                                 c->head_stride_rows, c->start_exp, batch, num_heads_k, seqlen_k);
+    if (g != ZS_OK) return g;
   }
+  if (k->layout != v->layout || k->head_stride_rows != v->head_stride_rows)
+    return ZS_E_UNSUPPORTED;
   AttnParams p{};
   p.kfix = k->fixed;
   p.kexp = k->exps;
@@ -589,6 +641,24 @@ extern "C" int zs_decode_attention_retiled(void* stream, const uint16_t* q,
   p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
   p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  if (k->layout == ZS_LAYOUT_TOKEN_MAJOR) {
+    const size_t sk = staging_bytes(k->layout, k->rows, k->cols);
+    const size_t sv = staging_bytes(v->layout, v->rows, v->cols);
+    if (!workspace || workspace_bytes < sk + sv) return ZS_E_INVAL;
+    uint16_t* kd = reinterpret_cast<uint16_t*>(workspace);
+    uint16_t* vd = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(workspace) + sk);
+    const zs_kv_retiled_t* src[2] = {k, v};
+    uint16_t* dst[2] = {kd, vd};
+    for (int i = 0; i < 2; ++i) {
+      const int e = zs_retiled_decompress(stream, src[i]->fixed, src[i]->exps, src[i]->eoff,
+                                          (uint8_t)src[i]->start_exp, dst[i], src[i]->rows,
+                                          src[i]->cols);
+      if (e != ZS_OK) return e;
+    }
+    return attn_staged((hipStream_t)stream, p, kd, vd, k->head_stride_rows,
+                       reinterpret_cast<uint8_t*>(workspace) + sk + sv,
+                       workspace_bytes - sk - sv);
+  }
   return attn_launch<kModeRetiled>((hipStream_t)stream, p, workspace, workspace_bytes);
 }
 

@@ -252,27 +252,27 @@ __global__ __launch_bounds__(256) void rdecompress_kernel(const uint8_t* fixed,
 }
 
 // ---------------------------------------------------------------------------
-// ZipGEMM over the re-tiled layout for N <= 16.  Workgroup = WAVES waves on F
-// consecutive 16-row bands x one split-K slice; wave w takes K tiles kb0+w,
-// kb0+w+WAVES, ... of all F bands, so each X fragment it loads feeds F
-// records (X bytes per record / F).  Records are fetched three tiles ahead
-// into a register ring, their outlier bytes staged one tile ahead, X one
-// tile ahead.
+// ZipGEMM over the re-tiled layout, narrow batches.  Workgroup = WAVES waves
+// on F consecutive 16-row bands x one split-K slice x 16*NB columns; wave w
+// takes K tiles kb0+w, kb0+w+WAVES, ... of all F bands, so each X fragment
+// it loads feeds F records (X bytes per record / F).  Records are fetched
+// three tiles ahead into a register ring, their outlier bytes staged one tile
+// ahead, X one tile ahead.
 // ---------------------------------------------------------------------------
-template <int F, int WAVES>
+template <int F, int NB, int WAVES>
 struct RGemmSmem {
   static constexpr int kMain = (int)sizeof(RTables) + WAVES * 3 * F * kExpStage;
-  static constexpr int kRed = (WAVES / 2) * F * 64 * 16;
+  static constexpr int kRed = (WAVES / 2) * F * NB * 64 * 16;
   static constexpr int kBytes = kMain > kRed ? kMain : kRed;
 };
 
-template <int F, int WAVES>
+template <int F, int NB, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
                                                            const uint8_t* exps,
                                                            const int32_t* eoff, int start_exp,
                                                            const uint16_t* X, uint16_t* Y, int M,
                                                            int N, int K, int kb_per_split) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[RGemmSmem<F, WAVES>::kBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[RGemmSmem<F, NB, WAVES>::kBytes];
   RTables& T = *reinterpret_cast<RTables*>(smem);
   build_r_tables(T, threadIdx.x, blockDim.x);
   const RExp ex = r_exp(start_exp);
@@ -285,6 +285,7 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
   const int bands = M >> 4;
   const int band0 = blockIdx.x * F;
   const int split = blockIdx.y;
+  const int n0 = blockIdx.z * NB * 16;
   const int KT = K >> 6;
   const int kb0 = split * kb_per_split;
   const int kb1 = min(kb0 + kb_per_split, KT);
@@ -293,10 +294,13 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
 #pragma unroll
   for (int f = 0; f < F; ++f) rec0[f] = (int64_t)min(band0 + f, bands - 1) * KT + kb0 + w;
 
-  const uint16_t* xrow = X + (int64_t)min(l & 15, N - 1) * K + 8 * (l >> 4);
-  f32x4 acc[F];
+  const uint16_t* xrow[NB];
 #pragma unroll
-  for (int f = 0; f < F; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int nb = 0; nb < NB; ++nb)
+    xrow[nb] = X + (int64_t)min(n0 + nb * 16 + (l & 15), N - 1) * K + 8 * (l >> 4);
+  f32x4 acc[F * NB];
+#pragma unroll
+  for (int i = 0; i < F * NB; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int c0 = 0; c0 < cnt; c0 += 64) {
     const int n = min(cnt - c0, 64);
@@ -311,12 +315,14 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
     }
     RStage R0[F], R1[F], R2[F];
     RMeta M0[F], M1[F], M2[F];
-    bf16x8 xc[2], xn[2];
+    bf16x8 xc[2][NB], xn[2][NB];
 #define RZ_LOADX(J, DST)                                                          \
   {                                                                               \
     const int kk_ = (kb0 + w + (c0 + (J)) * WAVES) * 64;                          \
-    DST[0] = *reinterpret_cast<const bf16x8*>(xrow + kk_);                        \
-    DST[1] = *reinterpret_cast<const bf16x8*>(xrow + kk_ + 32);                   \
+    _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                        \
+      DST[0][nb_] = *reinterpret_cast<const bf16x8*>(xrow[nb_] + kk_);            \
+      DST[1][nb_] = *reinterpret_cast<const bf16x8*>(xrow[nb_] + kk_ + 32);       \
+    }                                                                             \
   }
 #define RZ_ISSUE(J, R, MT)                                                              \
   {                                                                                     \
@@ -333,8 +339,10 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
   }
 #define RZ_STEP(J, SC, SN, RC, MC, RN, MN)                                                 \
   {                                                                                        \
-    xc[0] = xn[0];                                                                         \
-    xc[1] = xn[1];                                                                         \
+    _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                                 \
+      xc[0][nb_] = xn[0][nb_];                                                             \
+      xc[1][nb_] = xn[1][nb_];                                                             \
+    }                                                                                      \
     RZ_LOADX(min((J) + 1, last), xn);                                                      \
     RZ_STAGE(SN, RN, MN);                                                                  \
     if ((J) < n) {                                                                         \
@@ -342,10 +350,13 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
         u32x4 a0_, a1_;                                                                    \
         r_decode_staged(T, ex, RC[f_], MC[f_], stg + ((SC) * F + f_) * kExpStage, exps, a0_, \
                         a1_);                                                              \
-        acc[f_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0_), xc[0], acc[f_], \
-                                                          0, 0, 0);                        \
-        acc[f_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1_), xc[1], acc[f_], \
-                                                          0, 0, 0);                        \
+        _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                             \
+          f32x4& c_ = acc[f_ * NB + nb_];                                                  \
+          c_ = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0_), xc[0][nb_], c_, 0,  \
+                                                       0, 0);                              \
+          c_ = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1_), xc[1][nb_], c_, 0,  \
+                                                       0, 0);                              \
+        }                                                                                  \
       }                                                                                    \
     }                                                                                      \
     RZ_ISSUE(min((J) + 3, last), RC, MC);                                                  \
@@ -373,28 +384,30 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
   for (int half = WAVES / 2; half >= 1; half /= 2) {
     if (w >= half && w < 2 * half) {
 #pragma unroll
-      for (int f = 0; f < F; ++f) red[((w - half) * F + f) * 64 + l] = acc[f];
+      for (int i = 0; i < F * NB; ++i) red[((w - half) * F * NB + i) * 64 + l] = acc[i];
     }
     __syncthreads();
     if (w < half) {
 #pragma unroll
-      for (int f = 0; f < F; ++f) acc[f] += red[(w * F + f) * 64 + l];
+      for (int i = 0; i < F * NB; ++i) acc[i] += red[(w * F * NB + i) * 64 + l];
     }
     __syncthreads();
   }
   if (w == 0) {
     uint16_t* out = Y + (int64_t)split * M * N;
-    const int n = l & 15;
 #pragma unroll
-    for (int f = 0; f < F; ++f) {
-      const f32x4 v = acc[f];
-      if (n < N && band0 + f < bands) {
-        const int mrow = (band0 + f) * 16 + 4 * (l >> 4);
-        const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
-        const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
-        *reinterpret_cast<uint2*>(out + (int64_t)n * M + mrow) = make_uint2(lo, hi);
+    for (int f = 0; f < F; ++f)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const f32x4 v = acc[f * NB + nb];
+        const int n = n0 + nb * 16 + (l & 15);
+        if (n < N && band0 + f < bands) {
+          const int mrow = (band0 + f) * 16 + 4 * (l >> 4);
+          const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+          const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
+          *reinterpret_cast<uint2*>(out + (int64_t)n * M + mrow) = make_uint2(lo, hi);
+        }
       }
-    }
   }
 }
 
@@ -607,13 +620,13 @@ static int r_grid(int64_t nrec, int waves_per_block) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, 256 * 64));
 }
 
-template <int F>
+template <int F, int NB>
 static hipError_t launch_rgemm(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
                                const int32_t* eoff, int start_exp, const uint16_t* X,
                                uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split) {
   constexpr int kWaves = 8;
-  dim3 grid((M / 16 + F - 1) / F, split_k, 1);
-  hipLaunchKernelGGL((rgemm_kernel<F, kWaves>), grid, dim3(kWaves * 64), 0, st, fixed, exps,
+  dim3 grid((M / 16 + F - 1) / F, split_k, (N + NB * 16 - 1) / (NB * 16));
+  hipLaunchKernelGGL((rgemm_kernel<F, NB, kWaves>), grid, dim3(kWaves * 64), 0, st, fixed, exps,
                      eoff, start_exp, X, Y, M, N, K, kb_per_split);
   return hipGetLastError();
 }
@@ -772,9 +785,9 @@ extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t
     // with N) but also the grid: for N > 8 once the grid keeps at least
     // 192 workgroups.
     if (N > 8 && M / 16 >= 384)
-      e = launch_rgemm<2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+      e = launch_rgemm<2, 1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
     else
-      e = launch_rgemm<1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+      e = launch_rgemm<1, 1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
   }
   if (e != hipSuccess) return (int)e;
   if (split_k > 1) {
