@@ -109,7 +109,14 @@ __device__ __forceinline__ int kv_tile(int rowbase, int med, int c) {
   return ((rowbase >> 6) + (med >> 2)) * 2 + c;
 }
 
-template <int kMode>
+// Combine buffer of kWpi > 1: per wave, 32 O values + m + l per lane.
+constexpr int kCombineBytes = kAttnWaves * 34 * 64 * 4;
+
+// kWpi = 1: the workgroup's waves take four (batch, KV head, split) items.
+// kWpi = kAttnWaves: its waves share one item, each a contiguous quarter of
+// the split's tokens, and merge their softmax states in LDS at the end (for
+// small grids: 4x the waves without the cost of 4x the global splits).
+template <int kMode, int kWpi>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnParams p) {
   constexpr bool kDense = kMode == kModeDense;
   extern __shared__ __attribute__((aligned(16))) uint8_t attn_smem[];
@@ -128,16 +135,18 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnParams p) {
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
-  const int item = blockIdx.x * kAttnWaves + w;
-  if (item >= p.batch * p.heads_k * p.splits) return;
+  const int item = kWpi == 1 ? blockIdx.x * kAttnWaves + w : blockIdx.x;
+  if (item >= p.batch * p.heads_k * p.splits) return;  // uniform when kWpi > 1
   const int sp = item % p.splits;
   const int h = (item / p.splits) % p.heads_k;
   const int b = item / (p.splits * p.heads_k);
   int L = p.seqlen_k;
   if (p.seqlens) L = min(L, __builtin_amdgcn_readfirstlane(p.seqlens[b]));
   L = max(L, 0);
-  const int t0 = sp * p.chunk;
-  const int t1 = min(t0 + p.chunk, L);
+  // token range of this wave (multiples of 64 from the split's start)
+  const int sub = kWpi == 1 ? p.chunk : ((p.chunk / 64 + kWpi - 1) / kWpi) * 64;
+  const int t0 = sp * p.chunk + (kWpi == 1 ? 0 : w * sub);
+  const int t1 = min(min(t0 + sub, sp * p.chunk + p.chunk), L);
   const int nmed = t1 > t0 ? (t1 - t0 + 15) >> 4 : 0;
 
   uint8_t* wl = attn_smem + AttnLds<kMode>::kTables + w * AttnLds<kMode>::kWave;
@@ -369,6 +378,41 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnParams p) {
     }
   }
 
+  if constexpr (kWpi > 1) {
+    // Merge the waves' softmax states (log2 domain) into wave 0; the decode
+    // tables are dead by now, their LDS holds the states.
+    __syncthreads();
+    float* cb = reinterpret_cast<float*>(attn_smem) + w * 34 * 64 + l;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) cb[(4 * i + r) * 64] = O[i][r];
+    cb[32 * 64] = m_run;
+    cb[33 * 64] = l_run;
+    __syncthreads();
+    if (w != 0) return;
+    const float* c0 = reinterpret_cast<const float*>(attn_smem) + l;
+    float m = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < kWpi; ++v) m = fmaxf(m, c0[(v * 34 + 32) * 64]);
+    const float m_use = m == -INFINITY ? 0.f : m;
+    float lsum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < kWpi; ++v) {
+      const float lv = c0[(v * 34 + 33) * 64];
+      const float sc = lv > 0.f ? __builtin_amdgcn_exp2f(c0[(v * 34 + 32) * 64] - m_use) : 0.f;
+      lsum += lv * sc;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) O[i][r] += c0[(v * 34 + 4 * i + r) * 64] * sc;
+    }
+    m_run = m;
+    l_run = lsum;
+  }
+
   // Results: lane l holds head g = l%16, dims 16*i + 4*(l/16) + r of O[i].
   const int head = h * p.group + g;
   const bool own = g < p.group;
@@ -421,11 +465,19 @@ __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(AttnParams p) {
     p.lse[bh] = lsum > 0.f ? (m + __log2f(lsum)) * 0.6931471805599453f : -INFINITY;
 }
 
+// Workgroups of four waves per item take grids of fewer than this many items.
+constexpr int kSharedItemsBelow = 2048;
+
 static int attn_auto_splits(int batch, int heads_k, int seqlen_k) {
-  // Aim for about 2048 waves; at least 256 tokens per split.
+  // One wave per item: about 2048 waves, at least 256 tokens per split.
+  // Smaller grids run four waves per item (attn_launch); there about 256
+  // items (1024 waves) measure best -- B=1: T=4k 44 -> 21 us, T=32k
+  // 85 -> 51 us -- so fewer global splits.
   const int units = std::max(1, batch * heads_k);
   const int max_splits = std::max(1, (seqlen_k + 255) / 256);
-  return std::min(max_splits, std::max(1, (2048 + units - 1) / units));
+  const int s1 = std::min(max_splits, std::max(1, (2048 + units - 1) / units));
+  if ((int64_t)s1 * units >= kSharedItemsBelow) return s1;
+  return std::min(max_splits, std::max(1, (256 + units - 1) / units));
 }
 
 static int attn_chunk(int seqlen_k, int splits) {
@@ -446,9 +498,16 @@ static int attn_launch(hipStream_t st, AttnParams& p, void* workspace, size_t ws
     p.ws_ml = p.ws_o + (size_t)p.batch * p.heads * p.splits * kHeadDim;
   }
   const int items = p.batch * p.heads_k * p.splits;
-  const int grid = (items + kAttnWaves - 1) / kAttnWaves;
-  const size_t lds = AttnLds<kMode>::kBytes;
-  hipLaunchKernelGGL(attn_kernel<kMode>, dim3(grid), dim3(kAttnWaves * 64), lds, st, p);
+  if (items < kSharedItemsBelow && p.chunk > 64) {
+    // small grid: four waves per item
+    const size_t lds = std::max<size_t>(AttnLds<kMode>::kBytes, kCombineBytes);
+    hipLaunchKernelGGL((attn_kernel<kMode, kAttnWaves>), dim3(items), dim3(kAttnWaves * 64), lds,
+                       st, p);
+  } else {
+    const int grid = (items + kAttnWaves - 1) / kAttnWaves;
+    const size_t lds = AttnLds<kMode>::kBytes;
+    hipLaunchKernelGGL((attn_kernel<kMode, 1>), dim3(grid), dim3(kAttnWaves * 64), lds, st, p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   if (p.splits > 1) {
@@ -510,9 +569,11 @@ extern "C" int64_t zs_kv_staging_bytes(int layout, int rows, int cols) {
 extern "C" size_t zs_decode_attention_workspace_bytes(int batch, int num_heads, int head_dim,
                                                       int seqlen_k, int num_splits) {
   if (batch <= 0 || num_heads <= 0 || head_dim != kHeadDim || seqlen_k < 0) return 0;
-  // num_splits == 0 asks for the automatic choice; its size is bounded by
-  // the split count of a single KV head.
-  const int splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, 1, seqlen_k);
+  // num_splits == 0 asks for the automatic choice, which never exceeds
+  // min(ceil(T/256), ceil(2048/batch)) splits.
+  const int splits = num_splits > 0
+                         ? num_splits
+                         : std::min(std::max(1, (seqlen_k + 255) / 256), (2048 + batch - 1) / batch);
   return attn_ws_bytes(batch, num_heads, splits);
 }
 
