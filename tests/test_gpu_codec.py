@@ -94,6 +94,46 @@ def test_gpu_analyze_histogram(torch_cuda):
     assert top.cpu().tolist() == zo.select_gpu(np.bincount((a >> 7) & 0xFF, minlength=256))
 
 
+def _data_with_counts(counts, rng):
+    """bf16 values whose exponent histogram is exactly `counts`."""
+    e = np.repeat(np.arange(256, dtype=np.uint16), counts)
+    rng.shuffle(e)
+    return (e << 7) | rng.integers(0, 128, e.size, dtype=np.uint16)
+
+
+@pytest.mark.parametrize("case", ["evict_first_min_slot", "ties_at_seventh", "few_present",
+                                  "all_equal", "top_edge", "noncontiguous"])
+def test_gpu_select_window_special_cases(torch_cuda, case):
+    # window selection of zipserv_decode_attention_ext.cu:65-134 (streaming
+    # top-7 evicting the first minimum slot) against the oracle restatement
+    torch = torch_cuda
+    rng = np.random.default_rng(31)
+    c = np.zeros(256, np.int64)
+    if case == "evict_first_min_slot":
+        c[0], c[1], c[7] = 5, 3, 4          # 7 evicts exponent 2 (first zero slot)
+    elif case == "ties_at_seventh":
+        c[100:112] = 9
+        c[105] = 20
+    elif case == "few_present":
+        c[120], c[121], c[125] = 50, 40, 30
+    elif case == "all_equal":
+        c[:] = 3
+    elif case == "top_edge":
+        c[250:256] = [10, 20, 30, 40, 50, 60]
+    else:
+        c[[10, 11, 12, 40, 41, 90, 200]] = [7, 8, 9, 30, 31, 5, 6]
+    a = _data_with_counts(c, rng)
+    t = to_torch_bf16(a)
+    counts = torch.empty(256, dtype=torch.int32, device="cuda")
+    top = torch.empty(7, dtype=torch.int32, device="cuda")
+    rc = zs.lib().zs_analyze_top_exponents_gpu(int(torch.cuda.current_stream().cuda_stream),
+                                              t.data_ptr(), a.size, counts.data_ptr(),
+                                              top.data_ptr(), None)
+    assert rc == 0
+    np.testing.assert_array_equal(counts.cpu().numpy(), c)
+    assert top.cpu().tolist() == zo.select_gpu(c)
+
+
 def rel_err(y, ref):
     return np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30)
 

@@ -4,7 +4,7 @@
 //             -> select_kernel (window choice with the semantics of
 //             kernel_benchmark/zipserv_decode_attention_ext.cu:65-134).
 //   encode:   classify_kernel (bitmaps, small/median tile counts, per-GT
-//             padded totals) -> scan_kernel (global offsets, max, totals)
+//             padded totals) -> cscan_* (global offsets, max, totals)
 //             -> emit_kernel (re-reads the input, packs SM / FULL of a global
 //             tile in LDS and writes them with 16-byte stores at the tile's
 //             16-byte-aligned global offset).
@@ -26,10 +26,14 @@ __global__ void fill_i32_kernel(int32_t* p, int n, int32_t v) {
   if (i < n) p[i] = v;
 }
 
+// 256-bin exponent histogram.  Weights concentrate in a few exponents, so a
+// single LDS copy of the bins serialises on conflicting atomics; 16 copies
+// (lane % 16) cut the worst case from 64-way to 4-way.
 __global__ __launch_bounds__(256) void hist_kernel(const uint16_t* in, int64_t n, int32_t* counts) {
-  __shared__ int32_t h[256];
-  h[threadIdx.x] = 0;
+  __shared__ int32_t h[16][256];
+  for (int i = threadIdx.x; i < 16 * 256; i += blockDim.x) (&h[0][0])[i] = 0;
   __syncthreads();
+  int32_t* hc = h[threadIdx.x & 15];
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
   const bool aligned = (reinterpret_cast<uintptr_t>(in) & 15) == 0;
@@ -40,13 +44,15 @@ __global__ __launch_bounds__(256) void hist_kernel(const uint16_t* in, int64_t n
     const uint32_t d[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      atomicAdd(&h[(d[j] >> 7) & 0xFF], 1);
-      atomicAdd(&h[(d[j] >> 23) & 0xFF], 1);
+      atomicAdd(&hc[(d[j] >> 7) & 0xFF], 1);
+      atomicAdd(&hc[(d[j] >> 23) & 0xFF], 1);
     }
   }
-  for (int64_t i = nvec * 8 + tid; i < n; i += nthreads) atomicAdd(&h[(in[i] >> 7) & 0xFF], 1);
+  for (int64_t i = nvec * 8 + tid; i < n; i += nthreads) atomicAdd(&hc[(in[i] >> 7) & 0xFF], 1);
   __syncthreads();
-  const int32_t c = h[threadIdx.x];
+  int32_t c = 0;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) c += h[k][threadIdx.x];
   if (c) atomicAdd(&counts[threadIdx.x], c);
 }
 
@@ -55,22 +61,55 @@ __global__ __launch_bounds__(256) void hist_kernel(const uint16_t* in, int64_t n
 // replaces the first minimum slot on strictly greater count; candidates are
 // sorted, the first one starting 7 present exponents wins, else the start of
 // the longest consecutive run, clamped to [0, 248].
-__global__ void select_kernel(const int32_t* counts, int32_t* top) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+__global__ __launch_bounds__(64) void select_kernel(const int32_t* counts_g, int32_t* top) {
+  // One wave.  Lane i holds the counts of exponents i, i+64, i+128, i+192;
+  // the streaming top-7 below runs on wave-uniform values (scalar unit),
+  // reading each count with v_readlane instead of a dependent memory load.
+  if (blockIdx.x != 0) return;
+  const int l = threadIdx.x;
+  int cv[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) cv[k] = counts_g[64 * k + l];
+  __shared__ int32_t counts[256];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) counts[64 * k + l] = cv[k];
+  __syncthreads();
   int te[7], tc[7];
+#pragma unroll
   for (int i = 0; i < 7; ++i) {
     te[i] = -1;
     tc[i] = -1;
   }
-  for (int e = 0; e < 256; ++e) {
-    int mi = 0;
-    for (int i = 1; i < 7; ++i)
-      if (tc[i] < tc[mi]) mi = i;
-    if (counts[e] > tc[mi]) {
-      tc[mi] = counts[e];
-      te[mi] = e;
+  // Only an exponent whose count beats the current minimum slot changes the
+  // slots, and the minimum never decreases: walk just those (a ballot of
+  // count > min, refreshed after every change), in exponent order.
+  int tmin = -1;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint64_t mask = __builtin_amdgcn_ballot_w64(cv[k] > tmin);
+    while (mask) {
+      const int j = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      const int c = __builtin_amdgcn_readlane(cv[k], j);
+      int mi = 0;
+#pragma unroll
+      for (int i = 1; i < 7; ++i)
+        if (tc[i] < tc[mi]) mi = i;
+      if (c > tc[mi]) {
+#pragma unroll
+        for (int i = 0; i < 7; ++i)
+          if (i == mi) {
+            tc[i] = c;
+            te[i] = 64 * k + j;
+          }
+        tmin = tc[0];
+#pragma unroll
+        for (int i = 1; i < 7; ++i) tmin = tc[i] < tmin ? tc[i] : tmin;
+        mask &= __builtin_amdgcn_ballot_w64(cv[k] > tmin);
+      }
     }
   }
+  if (l != 0) return;
   int cand[7], n = 0;
   for (int i = 0; i < 7; ++i)
     if (te[i] >= 0) cand[n++] = te[i];
@@ -199,68 +238,170 @@ __global__ __launch_bounds__(256) void classify_kernel(const uint16_t* in, int M
   }
 }
 
-// Single-workgroup scan over the per-tile padded counts: each of the 1024
-// threads owns a contiguous chunk, chunk sums are scanned in LDS, then every
-// thread writes its chunk's cumulative offsets.
-__global__ __launch_bounds__(1024) void scan_kernel(const int32_t* gt_hf, const int32_t* gt_full,
-                                                    int64_t ngt, int32_t* tog, int32_t* hf_off,
-                                                    int32_t* full_off, int32_t* max_hf,
-                                                    int32_t* max_full, int32_t* tot_hf,
-                                                    int32_t* tot_full) {
-  __shared__ int64_t s_hf[1024], s_fu[1024];
-  __shared__ int32_t s_mh[1024], s_mf[1024];
-  const int t = threadIdx.x;
-  const int64_t chunk = (ngt + 1023) / 1024;
-  const int64_t b = std::min<int64_t>(ngt, t * chunk), e = std::min<int64_t>(ngt, b + chunk);
-  int64_t sh = 0, sf = 0;
-  int32_t mh = 0, mf = 0;
-  for (int64_t i = b; i < e; ++i) {
-    sh += gt_hf[i];
-    sf += gt_full[i];
-    mh = max(mh, gt_hf[i]);
-    mf = max(mf, gt_full[i]);
+// Offsets of the global tiles' padded SM / FULL sizes, in three coalesced
+// passes over spans of kSpan global tiles: per-span sums and maxima, one
+// workgroup scanning the span sums, then per-span exclusive offsets.  Output
+// slot i (i < ngt) is the exclusive offset of global tile i and slot ngt the
+// total, in hf_off / full_off and interleaved in tog (the tile_offsets_global
+// array of csrc/L_API.cu).  A span's sums and maxima are parked in its first
+// output slots between the passes.
+constexpr int kSpan = 1024;
+
+struct Pair {
+  int a, b;
+};
+
+__device__ __forceinline__ Pair block256_exclusive2(Pair v, Pair& total) {
+  __shared__ int ws[2][4];
+  const int l = lane_id(), w = threadIdx.x >> 6;
+  const int ia = wave_inclusive_scan(v.a), ib = wave_inclusive_scan(v.b);
+  if (l == 63) {
+    ws[0][w] = ia;
+    ws[1][w] = ib;
   }
-  s_hf[t] = sh;
-  s_fu[t] = sf;
-  s_mh[t] = mh;
-  s_mf[t] = mf;
   __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {
-    int64_t ah = 0, af = 0;
-    if (t >= off) {
-      ah = s_hf[t - off];
-      af = s_fu[t - off];
+  Pair before = {0, 0};
+  for (int i = 0; i < w; ++i) {
+    before.a += ws[0][i];
+    before.b += ws[1][i];
+  }
+  total = {ws[0][0] + ws[0][1] + ws[0][2] + ws[0][3], ws[1][0] + ws[1][1] + ws[1][2] + ws[1][3]};
+  __syncthreads();
+  return {before.a + ia - v.a, before.b + ib - v.b};
+}
+
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off));
+  return v;
+}
+
+__global__ __launch_bounds__(256) void cscan_reduce_kernel(const int32_t* gt_hf,
+                                                           const int32_t* gt_full, int64_t ngt,
+                                                           int32_t* tog, int32_t* hf_off,
+                                                           int32_t* full_off) {
+  __shared__ int wm[2][4];
+  const int64_t base = (int64_t)blockIdx.x * kSpan;
+  Pair s = {0, 0};
+  int mh = 0, mf = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t i = base + j * 256 + threadIdx.x;
+    if (i < ngt) {
+      const int h = gt_hf[i], f = gt_full[i];
+      s.a += h;
+      s.b += f;
+      mh = max(mh, h);
+      mf = max(mf, f);
+    }
+  }
+  mh = wave_max(mh);
+  mf = wave_max(mf);
+  if (lane_id() == 0) {
+    wm[0][threadIdx.x >> 6] = mh;
+    wm[1][threadIdx.x >> 6] = mf;
+  }
+  Pair total;
+  block256_exclusive2(s, total);  // its barrier also publishes wm
+  if (threadIdx.x == 0) {
+    hf_off[base] = total.a;
+    full_off[base] = total.b;
+    tog[2 * base] = max(max(wm[0][0], wm[0][1]), max(wm[0][2], wm[0][3]));
+    tog[2 * base + 1] = max(max(wm[1][0], wm[1][1]), max(wm[1][2], wm[1][3]));
+  }
+}
+
+__global__ __launch_bounds__(1024) void cscan_spans_kernel(int64_t ngt, int32_t* tog,
+                                                           int32_t* hf_off, int32_t* full_off,
+                                                           int32_t* max_hf, int32_t* max_full,
+                                                           int32_t* tot_hf, int32_t* tot_full) {
+  __shared__ int64_t wsum[2][16];
+  __shared__ int32_t wmax[2][16];
+  __shared__ int64_t carry[2];
+  __shared__ int32_t mx[2];
+  const int t = threadIdx.x, l = lane_id(), w = t >> 6;
+  const int64_t nspans = (ngt + kSpan - 1) / kSpan;
+  if (t == 0) carry[0] = carry[1] = mx[0] = mx[1] = 0;
+  __syncthreads();
+  for (int64_t s0 = 0; s0 < nspans; s0 += 1024) {
+    const int64_t sp = s0 + t;
+    const bool in = sp < nspans;
+    const int64_t at = sp * kSpan;
+    const int va = in ? hf_off[at] : 0, vb = in ? full_off[at] : 0;
+    const int ma = wave_max(in ? tog[2 * at] : 0), mb = wave_max(in ? tog[2 * at + 1] : 0);
+    const int ia = wave_inclusive_scan(va), ib = wave_inclusive_scan(vb);
+    if (l == 63) {
+      wsum[0][w] = ia;
+      wsum[1][w] = ib;
+    }
+    if (l == 0) {
+      wmax[0][w] = ma;
+      wmax[1][w] = mb;
     }
     __syncthreads();
-    s_hf[t] += ah;
-    s_fu[t] += af;
-    __syncthreads();
-  }
-  for (int off = 512; off > 0; off >>= 1) {
-    if (t < off) {
-      s_mh[t] = max(s_mh[t], s_mh[t + off]);
-      s_mf[t] = max(s_mf[t], s_mf[t + off]);
+    int64_t ba = carry[0], bb = carry[1];
+    for (int i = 0; i < w; ++i) {
+      ba += wsum[0][i];
+      bb += wsum[1][i];
+    }
+    if (in) {
+      hf_off[at] = (int32_t)(ba + ia - va);
+      full_off[at] = (int32_t)(bb + ib - vb);
     }
     __syncthreads();
-  }
-  int64_t run_h = s_hf[t] - sh, run_f = s_fu[t] - sf;
-  for (int64_t i = b; i < e; ++i) {
-    run_h += gt_hf[i];
-    run_f += gt_full[i];
-    tog[2 * (i + 1)] = (int32_t)run_h;
-    tog[2 * (i + 1) + 1] = (int32_t)run_f;
-    hf_off[i + 1] = (int32_t)run_h;
-    full_off[i + 1] = (int32_t)run_f;
+    if (t == 0) {
+      for (int i = 0; i < 16; ++i) {
+        carry[0] += wsum[0][i];
+        carry[1] += wsum[1][i];
+        mx[0] = max(mx[0], wmax[0][i]);
+        mx[1] = max(mx[1], wmax[1][i]);
+      }
+    }
+    __syncthreads();
   }
   if (t == 0) {
-    tog[0] = 0;
-    tog[1] = 0;
-    hf_off[0] = 0;
-    full_off[0] = 0;
-    *max_hf = s_mh[0];
-    *max_full = s_mf[0];
-    *tot_hf = (int32_t)s_hf[1023];
-    *tot_full = (int32_t)s_fu[1023];
+    const int32_t th = (int32_t)carry[0], tf = (int32_t)carry[1];
+    hf_off[ngt] = th;
+    full_off[ngt] = tf;
+    tog[2 * ngt] = th;
+    tog[2 * ngt + 1] = tf;
+    *tot_hf = th;
+    *tot_full = tf;
+    *max_hf = mx[0];
+    *max_full = mx[1];
+  }
+}
+
+__global__ __launch_bounds__(256) void cscan_write_kernel(const int32_t* gt_hf,
+                                                          const int32_t* gt_full, int64_t ngt,
+                                                          int32_t* tog, int32_t* hf_off,
+                                                          int32_t* full_off) {
+  const int64_t base = (int64_t)blockIdx.x * kSpan;
+  const Pair off = {hf_off[base], full_off[base]};  // rewritten unchanged below
+  const int64_t i0 = base + 4 * threadIdx.x;
+  int ch[4], cf[4];
+  Pair s = {0, 0};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bool in = i0 + j < ngt;
+    ch[j] = in ? gt_hf[i0 + j] : 0;
+    cf[j] = in ? gt_full[i0 + j] : 0;
+    s.a += ch[j];
+    s.b += cf[j];
+  }
+  Pair total;
+  const Pair ex = block256_exclusive2(s, total);
+  int rh = off.a + ex.a, rf = off.b + ex.b;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (i0 + j < ngt) {
+      hf_off[i0 + j] = rh;
+      full_off[i0 + j] = rf;
+      tog[2 * (i0 + j)] = rh;
+      tog[2 * (i0 + j) + 1] = rf;
+    }
+    rh += ch[j];
+    rf += cf[j];
   }
 }
 
@@ -369,8 +510,13 @@ extern "C" int zs_init_bf16_matrix_triple_bitmap_gpu(
   hipLaunchKernelGGL(classify_kernel, dim3(grid), dim3(256), 0, st, d_input, M, K, d_top,
                      reinterpret_cast<uint8_t*>(d_b1), reinterpret_cast<uint8_t*>(d_b2),
                      reinterpret_cast<uint8_t*>(d_b3), d_tiles, d_tom, d_gt_hf, d_gt_full);
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, d_gt_hf, d_gt_full, ngt, d_tog,
-                     d_hf_off, d_full_off, d_max_hf, d_max_full, d_tot_hf, d_tot_full);
+  const unsigned spans = (unsigned)((ngt + kSpan - 1) / kSpan);
+  hipLaunchKernelGGL(cscan_reduce_kernel, dim3(spans), dim3(256), 0, st, d_gt_hf, d_gt_full, ngt,
+                     d_tog, d_hf_off, d_full_off);
+  hipLaunchKernelGGL(cscan_spans_kernel, dim3(1), dim3(1024), 0, st, ngt, d_tog, d_hf_off,
+                     d_full_off, d_max_hf, d_max_full, d_tot_hf, d_tot_full);
+  hipLaunchKernelGGL(cscan_write_kernel, dim3(spans), dim3(256), 0, st, d_gt_hf, d_gt_full, ngt,
+                     d_tog, d_hf_off, d_full_off);
   hipLaunchKernelGGL(emit_kernel, dim3(grid), dim3(256), 0, st, d_input, M, K, d_top, d_tog,
                      d_tom, d_sm, d_full);
   return hip_status(hipGetLastError());

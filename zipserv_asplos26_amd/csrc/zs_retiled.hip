@@ -88,33 +88,98 @@ __global__ __launch_bounds__(256) void rcount_canon_kernel(Streams s, int M, int
   }
 }
 
-// Exclusive scan of the per-record counts into eoff (n + 1 entries) by one
-// workgroup of 1024 threads; *total receives the sum (64-bit).
-__global__ __launch_bounds__(1024) void rscan_kernel(const int32_t* counts, int64_t n,
-                                                     int32_t* eoff, int64_t* total) {
-  __shared__ int64_t part[1024];
-  const int t = threadIdx.x;
-  const int64_t per = (n + 1023) / 1024;
-  const int64_t b = std::min<int64_t>(n, t * per), e = std::min<int64_t>(n, b + per);
-  int64_t s = 0;
-  for (int64_t i = b; i < e; ++i) s += counts[i];
-  part[t] = s;
+// Exclusive scan of the per-record counts into eoff (n + 1 entries), in three
+// launches over tiles of 1024 records: each tile's sum is parked at
+// eoff[tile * 1024], one workgroup turns those into the tiles' exclusive
+// offsets (and writes eoff[n] and *total), then each tile scans its own
+// counts from its offset.  Coalesced loads; the single-workgroup pass only
+// touches n / 1024 values.
+constexpr int kScanTile = 1024;
+
+__device__ __forceinline__ int block256_exclusive(int v, int& total) {
+  __shared__ int ws[4];
+  const int l = lane_id(), w = threadIdx.x >> 6;
+  const int incl = wave_inclusive_scan(v);
+  if (l == 63) ws[w] = incl;
   __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {
-    const int64_t v = t >= off ? part[t - off] : 0;
+  int before = 0;
+  for (int i = 0; i < w; ++i) before += ws[i];
+  total = ws[0] + ws[1] + ws[2] + ws[3];
+  __syncthreads();
+  return before + incl - v;
+}
+
+__global__ __launch_bounds__(256) void rscan_reduce_kernel(const int32_t* counts, int64_t n,
+                                                           int32_t* eoff) {
+  const int64_t base = (int64_t)blockIdx.x * kScanTile;
+  int s = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t i = base + j * 256 + threadIdx.x;
+    if (i < n) s += counts[i];
+  }
+  int total;
+  block256_exclusive(s, total);
+  if (threadIdx.x == 0) eoff[base] = total;
+}
+
+__global__ __launch_bounds__(1024) void rscan_tiles_kernel(int32_t* eoff, int64_t n,
+                                                           int64_t* total) {
+  __shared__ int64_t wsum[16];
+  __shared__ int64_t carry_s;
+  const int t = threadIdx.x, l = lane_id(), w = t >> 6;
+  const int64_t ntiles = (n + kScanTile - 1) / kScanTile;
+  if (t == 0) carry_s = 0;
+  __syncthreads();
+  for (int64_t t0 = 0; t0 < ntiles; t0 += 1024) {
+    const int64_t tile = t0 + t;
+    const int v = tile < ntiles ? eoff[tile * kScanTile] : 0;
+    const int incl = wave_inclusive_scan(v);
+    if (l == 63) wsum[w] = incl;
     __syncthreads();
-    part[t] += v;
+    int64_t before = carry_s;
+    for (int i = 0; i < w; ++i) before += wsum[i];
+    if (tile < ntiles) eoff[tile * kScanTile] = (int32_t)(before + incl - v);
+    __syncthreads();
+    if (t == 0) {
+      int64_t sum = 0;
+      for (int i = 0; i < 16; ++i) sum += wsum[i];
+      carry_s += sum;
+    }
     __syncthreads();
   }
-  int64_t run = part[t] - s;
-  for (int64_t i = b; i < e; ++i) {
-    eoff[i] = (int32_t)run;
-    run += counts[i];
+  if (t == 0) {
+    eoff[n] = (int32_t)carry_s;
+    *total = carry_s;
   }
-  if (t == 1023) {
-    eoff[n] = (int32_t)part[1023];
-    *total = part[1023];
+}
+
+__global__ __launch_bounds__(256) void rscan_write_kernel(const int32_t* counts, int64_t n,
+                                                          int32_t* eoff) {
+  const int64_t base = (int64_t)blockIdx.x * kScanTile;
+  const int off = eoff[base];  // this tile's exclusive offset (rewritten unchanged below)
+  const int64_t i0 = base + 4 * threadIdx.x;
+  int c[4], s = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    c[j] = i0 + j < n ? counts[i0 + j] : 0;
+    s += c[j];
   }
+  int total;
+  int run = off + block256_exclusive(s, total);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (i0 + j < n) eoff[i0 + j] = run;
+    run += c[j];
+  }
+}
+
+static void launch_rscan(hipStream_t st, const int32_t* counts, int64_t n, int32_t* eoff,
+                         int64_t* total) {
+  const int64_t tiles = (n + kScanTile - 1) / kScanTile;
+  hipLaunchKernelGGL(rscan_reduce_kernel, dim3((unsigned)tiles), dim3(256), 0, st, counts, n, eoff);
+  hipLaunchKernelGGL(rscan_tiles_kernel, dim3(1), dim3(1024), 0, st, eoff, n, total);
+  hipLaunchKernelGGL(rscan_write_kernel, dim3((unsigned)tiles), dim3(256), 0, st, counts, n, eoff);
 }
 
 // Writes one record from the lane's 16 bf16 values and their code bit-planes
@@ -670,7 +735,7 @@ extern "C" int zs_compress_retiled_count_gpu(void* stream, const uint16_t* d_inp
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(rcount_kernel, dim3(r_grid(nrec, 4)), dim3(256), 0, st, d_input, M, K,
                      d_top_exponents, d_counts);
-  hipLaunchKernelGGL(rscan_kernel, dim3(1), dim3(1024), 0, st, d_counts, nrec, d_eoff, d_total);
+  launch_rscan(st, d_counts, nrec, d_eoff, d_total);
   return status_of(hipGetLastError());
 }
 
@@ -715,7 +780,7 @@ extern "C" int zs_retile_triple_bitmap_count_gpu(void* stream, const uint8_t* sm
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(rcount_canon_kernel, dim3(r_grid(nrec, 4)), dim3(256), 0, st,
                      canon_streams(sm, full, b1, b2, b3, tom, tog), M, K, d_counts);
-  hipLaunchKernelGGL(rscan_kernel, dim3(1), dim3(1024), 0, st, d_counts, nrec, d_eoff, d_total);
+  launch_rscan(st, d_counts, nrec, d_eoff, d_total);
   return status_of(hipGetLastError());
 }
 
