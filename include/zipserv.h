@@ -142,6 +142,13 @@ int zs_bf16_triple_bitmap_mm(void* stream, const uint8_t* SignMantissa,
 int zs_analyze_top_exponents_gpu(void* stream, const uint16_t* d_input, int64_t numel,
                                  int32_t* d_exponent_counts, int32_t* d_top_exponents,
                                  int32_t* d_done_counter);
+/* The same histogram and selection with 64-bit bins (d_exponent_counts:
+ * 256 uint64), for tensors past the int32 bins above (numel > INT32_MAX,
+ * e.g. a 32 x 8 x 128k x 128 KV cache).  No counterpart in the reference,
+ * whose int32 counters (ext.cu:35-63) overflow there; the window rule is
+ * unchanged, so it returns the same window wherever both apply. */
+int zs_analyze_top_exponents_u64_gpu(void* stream, const uint16_t* d_input, int64_t numel,
+                                     uint64_t* d_exponent_counts, int32_t* d_top_exponents);
 
 /* build/L_API.cuh:144-165 InitBF16MatrixTripleBitmap_GPU: device encoder
  * producing the canonical streams.  d_temp_sm / d_temp_full are accepted for

@@ -257,6 +257,8 @@ def compress_zipserv(input, logical_rows: int | None = None, logical_cols: int |
     dev = input.device
     mk = rows * cols
     ngt = mk // 4096
+    if mk + 16 * ngt > 2**31 - 1:  # int32 stream offsets of the format (ext.cu:184)
+        check("zs_init_bf16_matrix_triple_bitmap_gpu", _lib.ZS_E_OVERFLOW)
     i32 = dict(dtype=torch.int32, device=dev)
     sm = torch.empty(int(L.zs_sign_mantissa_capacity(rows, cols)), dtype=torch.uint8, device=dev)
     fu = torch.empty(int(L.zs_full_capacity(rows, cols)), dtype=torch.bfloat16, device=dev)
@@ -266,10 +268,10 @@ def compress_zipserv(input, logical_rows: int | None = None, logical_cols: int |
     tog = torch.empty(2 * (ngt + 1), **i32)
     ghf, gfu = torch.empty(ngt, **i32), torch.empty(ngt, **i32)
     hoff, foff = torch.empty(ngt + 1, **i32), torch.empty(ngt + 1, **i32)
-    top = torch.empty(7, **i32)
+    small = torch.empty(12, **i32)  # top[0:7] | scalars[8:12]: one D2H copy below
+    top, scal = small[0:7], small[8:12]
     counts = torch.empty(256, **i32)
     done = torch.empty(4, **i32)
-    scal = torch.empty(4, **i32)
     st = _stream()
     check("zs_analyze_top_exponents_gpu",
           L.zs_analyze_top_exponents_gpu(st, _dptr(input), mk, _dptr(counts), _dptr(top), _dptr(done)))
@@ -279,11 +281,13 @@ def compress_zipserv(input, logical_rows: int | None = None, logical_cols: int |
               _dptr(b2), _dptr(b3), _dptr(tiles), _dptr(med), _dptr(tog), None, None,
               _dptr(ghf), _dptr(gfu), _dptr(hoff), _dptr(foff), _dptr(scal[0:]),
               _dptr(scal[1:]), _dptr(scal[2:]), _dptr(scal[3:])))
-    host = torch.cat([scal, top[:1]]).cpu().tolist()  # synchronises, as ext.cu:234-245
-    max_hf, max_full, total_hf, total_full, top0 = host
-    # The slack past the streams is zeroed so every byte a decoder may touch is defined.
-    sm[total_hf:].zero_()
-    fu[total_full:].zero_()
+    host = small.cpu().tolist()  # synchronises, as ext.cu:234-245
+    top0 = host[0]
+    max_hf, max_full, total_hf, total_full = host[8:12]
+    # The slack a decoder may read past the streams is zeroed so it is defined.
+    slack = _lib.ZS_STREAM_SLACK_BYTES
+    sm[total_hf:total_hf + slack].zero_()
+    fu[total_full:total_full + slack // 2].zero_()
     start_exp = top0 - 1
     inclusive = (total_hf + 2 * total_full + (mk // 64) * 3 * 8 + (mk // 64) * 2 * 4
                  + (mk // 1024) * 2 * 4 + (ngt + 1) * 2 * 4 + 7 * 4)
@@ -412,13 +416,14 @@ def compress_retiled(input, logical_rows=None, logical_cols=None, layout="by_kv_
     dev = input.device
     i32 = dict(dtype=torch.int32, device=dev)
     nrec = rows // 16 * (cols // 64)
-    top, counts, done = torch.empty(7, **i32), torch.empty(256, **i32), torch.empty(4, **i32)
+    top, counts = torch.empty(7, **i32), torch.empty(256, dtype=torch.int64, device=dev)
     cnt, eoff = torch.empty(nrec, **i32), torch.empty(nrec + 1, **i32)
     total = torch.empty(1, dtype=torch.int64, device=dev)
     st = _stream()
-    check("zs_analyze_top_exponents_gpu",
-          L.zs_analyze_top_exponents_gpu(st, _dptr(input), rows * cols, _dptr(counts), _dptr(top),
-                                         _dptr(done)))
+    # 64-bit bins: the re-tiled layout takes matrices past 2^31 elements.
+    check("zs_analyze_top_exponents_u64_gpu",
+          L.zs_analyze_top_exponents_u64_gpu(st, _dptr(input), rows * cols, _dptr(counts),
+                                             _dptr(top)))
     check("zs_compress_retiled_count_gpu",
           L.zs_compress_retiled_count_gpu(st, _dptr(input), rows, cols, _dptr(top), _dptr(cnt),
                                           _dptr(eoff), _dptr(total)))

@@ -28,8 +28,11 @@ __global__ void fill_i32_kernel(int32_t* p, int n, int32_t v) {
 
 // 256-bin exponent histogram.  Weights concentrate in a few exponents, so a
 // single LDS copy of the bins serialises on conflicting atomics; 16 copies
-// (lane % 16) cut the worst case from 64-way to 4-way.
-__global__ __launch_bounds__(256) void hist_kernel(const uint16_t* in, int64_t n, int32_t* counts) {
+// (lane % 16) cut the worst case from 64-way to 4-way.  A workgroup's own
+// bins stay below 2^31 (the launch gives each at most 2^30 elements); the
+// global bins are int32 (the reference's) or 64-bit (any numel).
+template <typename C>
+__global__ __launch_bounds__(256) void hist_kernel(const uint16_t* in, int64_t n, C* counts) {
   __shared__ int32_t h[16][256];
   for (int i = threadIdx.x; i < 16 * 256; i += blockDim.x) (&h[0][0])[i] = 0;
   __syncthreads();
@@ -53,7 +56,19 @@ __global__ __launch_bounds__(256) void hist_kernel(const uint16_t* in, int64_t n
   int32_t c = 0;
 #pragma unroll
   for (int k = 0; k < 16; ++k) c += h[k][threadIdx.x];
-  if (c) atomicAdd(&counts[threadIdx.x], c);
+  if (c) {
+    if constexpr (sizeof(C) == 8)
+      atomicAdd(reinterpret_cast<unsigned long long*>(&counts[threadIdx.x]),
+                (unsigned long long)c);
+    else
+      atomicAdd(&counts[threadIdx.x], c);
+  }
+}
+
+__device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), lane);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 // Window selection of zipserv_decode_attention_ext.cu:65-134: seven slots
@@ -61,20 +76,22 @@ __global__ __launch_bounds__(256) void hist_kernel(const uint16_t* in, int64_t n
 // replaces the first minimum slot on strictly greater count; candidates are
 // sorted, the first one starting 7 present exponents wins, else the start of
 // the longest consecutive run, clamped to [0, 248].
-__global__ __launch_bounds__(64) void select_kernel(const int32_t* counts_g, int32_t* top) {
+template <typename C>
+__global__ __launch_bounds__(64) void select_kernel(const C* counts_g, int32_t* top) {
   // One wave.  Lane i holds the counts of exponents i, i+64, i+128, i+192;
   // the streaming top-7 below runs on wave-uniform values (scalar unit),
   // reading each count with v_readlane instead of a dependent memory load.
   if (blockIdx.x != 0) return;
   const int l = threadIdx.x;
-  int cv[4];
+  int64_t cv[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) cv[k] = counts_g[64 * k + l];
-  __shared__ int32_t counts[256];
+  for (int k = 0; k < 4; ++k) cv[k] = (int64_t)counts_g[64 * k + l];
+  __shared__ int64_t counts[256];
 #pragma unroll
   for (int k = 0; k < 4; ++k) counts[64 * k + l] = cv[k];
   __syncthreads();
-  int te[7], tc[7];
+  int te[7];
+  int64_t tc[7];
 #pragma unroll
   for (int i = 0; i < 7; ++i) {
     te[i] = -1;
@@ -83,14 +100,14 @@ __global__ __launch_bounds__(64) void select_kernel(const int32_t* counts_g, int
   // Only an exponent whose count beats the current minimum slot changes the
   // slots, and the minimum never decreases: walk just those (a ballot of
   // count > min, refreshed after every change), in exponent order.
-  int tmin = -1;
+  int64_t tmin = -1;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     uint64_t mask = __builtin_amdgcn_ballot_w64(cv[k] > tmin);
     while (mask) {
       const int j = __builtin_ctzll(mask);
       mask &= mask - 1;
-      const int c = __builtin_amdgcn_readlane(cv[k], j);
+      const int64_t c = readlane64(cv[k], j);
       int mi = 0;
 #pragma unroll
       for (int i = 1; i < 7; ++i)
@@ -471,20 +488,37 @@ using namespace zs;
 
 static int hip_status(hipError_t e) { return e == hipSuccess ? ZS_OK : (int)e; }
 
+template <typename C>
+static int analyze(hipStream_t st, const uint16_t* d_input, int64_t numel, C* d_counts,
+                   int32_t* d_top) {
+  // Enough workgroups to fill the chip, and at most 2^30 elements each.
+  const int64_t blocks = std::max<int64_t>(
+      std::min<int64_t>((numel + 2047) / 2048, (int64_t)device_cu_count() * 4),
+      (numel + (1LL << 30) - 1) >> 30);
+  if (blocks > INT32_MAX) return ZS_E_OVERFLOW;
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(sizeof(C) / 4), dim3(256), 0, st,
+                     reinterpret_cast<int32_t*>(d_counts), (int)(256 * sizeof(C) / 4), 0);
+  hipLaunchKernelGGL(hist_kernel<C>, dim3((unsigned)blocks), dim3(256), 0, st, d_input, numel,
+                     d_counts);
+  hipLaunchKernelGGL(select_kernel<C>, dim3(1), dim3(64), 0, st, d_counts, d_top);
+  return hip_status(hipGetLastError());
+}
+
 extern "C" int zs_analyze_top_exponents_gpu(void* stream, const uint16_t* d_input, int64_t numel,
                                             int32_t* d_counts, int32_t* d_top,
                                             int32_t* d_done) {
   if (!d_input || numel <= 0 || !d_counts || !d_top) return ZS_E_INVAL;
   if (numel > INT32_MAX) return ZS_E_OVERFLOW;  // int32 bins of the reference
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(256), 0, st, d_counts, 256, 0);
   if (d_done) hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, st, d_done, 1, 0);
-  const int64_t blocks = std::max<int64_t>(
-      1, std::min<int64_t>((numel + 2047) / 2048, (int64_t)device_cu_count() * 4));
-  hipLaunchKernelGGL(hist_kernel, dim3((unsigned)blocks), dim3(256), 0, st, d_input, numel,
-                     d_counts);
-  hipLaunchKernelGGL(select_kernel, dim3(1), dim3(64), 0, st, d_counts, d_top);
-  return hip_status(hipGetLastError());
+  return analyze(st, d_input, numel, d_counts, d_top);
+}
+
+extern "C" int zs_analyze_top_exponents_u64_gpu(void* stream, const uint16_t* d_input,
+                                                int64_t numel, uint64_t* d_counts,
+                                                int32_t* d_top) {
+  if (!d_input || numel <= 0 || !d_counts || !d_top) return ZS_E_INVAL;
+  return analyze((hipStream_t)stream, d_input, numel, d_counts, d_top);
 }
 
 extern "C" int zs_init_bf16_matrix_triple_bitmap_gpu(
