@@ -238,7 +238,7 @@ typedef struct zs_kv_compressed {
  * zipserv_k=, zipserv_v=) -> flash_api.cpp:1346-1520 mha_fwd_kvcache for one
  * query token (decode): out[b][h] = softmax(scale * q[b][h] . K[b][:L_b][h/G])
  * . V[b][:L_b][h/G], G = num_heads / num_heads_k, fp32 online softmax.
- * q, out: [batch][num_heads][head_dim] bf16.  L_b = cache_seqlens[b] (device
+ * q, out: [batch][num_heads][head_dim] bf16, 16-byte aligned.  L_b = cache_seqlens[b] (device
  * int32 [batch]) or seqlen_k when cache_seqlens is NULL.  softmax_lse
  * (optional, [batch][num_heads] fp32) is the natural-log normaliser.
  * num_splits = 0 picks a split of the sequence across workgroups; splits > 1

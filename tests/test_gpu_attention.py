@@ -148,11 +148,14 @@ def test_attention_rejects_unsupported(torch_cuda):
     out = torch.empty_like(q)
     L = zs.lib()
 
-    def call(dk, dv, D=128, H=64, Hkv=8, T=128, splits=1):
-        return L.zs_decode_attention(0, q.data_ptr(), ctypes.byref(dk), ctypes.byref(dv), None, T,
-                                     1, H, Hkv, D, 0.1, out.data_ptr(), None, None, 0, splits)
+    def call(dk, dv, D=128, H=64, Hkv=8, T=128, splits=1, qoff=0, ooff=0):
+        return L.zs_decode_attention(0, q.data_ptr() + qoff, ctypes.byref(dk), ctypes.byref(dv),
+                                     None, T, 1, H, Hkv, D, 0.1, out.data_ptr() + ooff, None, None,
+                                     0, splits)
     assert call(d, d) == 0
     torch.cuda.synchronize()
+    assert call(d, d, qoff=2) == zs._lib.ZS_E_INVAL  # q rows are read 16 bytes at a time
+    assert call(d, d, ooff=8) == zs._lib.ZS_E_INVAL
     assert call(d, d, D=64) == zs._lib.ZS_E_UNSUPPORTED
     assert call(d, d, H=63) == zs._lib.ZS_E_INVAL
     assert call(d, d, T=129) == zs._lib.ZS_E_INVAL  # rows per head (128) < seqlen_k

@@ -34,7 +34,8 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kHeadDim = 128;
-constexpr int kAttnWaves = 4;
+constexpr int kAttnWaves = 4;   // waves per workgroup, one item each
+constexpr int kItemWaves = 4;   // waves per workgroup sharing one item (small grids)
 constexpr int kVRow = 160;                  // LDS row pitch of the V tile (bytes)
 constexpr int kVBytes = 16 * kVRow;         // 16 tokens x 64 dims (+ pad)
 constexpr int kModeCanon = 0;    // canonical TCA-TBE streams
@@ -49,7 +50,7 @@ struct AttnLds {
                                                          : 0;
   static constexpr int kWave = (kMode == kModeCanon ? 2 * kStBytes
                                 : kMode == kModeRetiled ? 2 * kExpStage : 0) + kVBytes;
-  static constexpr int kBytes = kTables + kAttnWaves * kWave;
+  static constexpr int bytes(int waves) { return kTables + waves * kWave; }
 };
 
 struct AttnParams {
@@ -110,14 +111,19 @@ __device__ __forceinline__ int kv_tile(int rowbase, int med, int c) {
 }
 
 // Combine buffer of kWpi > 1: per wave, 32 O values + m + l per lane.
-constexpr int kCombineBytes = kAttnWaves * 34 * 64 * 4;
+constexpr int kCombineBytes = kItemWaves * 34 * 64 * 4;
 
-// kWpi = 1: the workgroup's waves take four (batch, KV head, split) items.
-// kWpi = kAttnWaves: its waves share one item, each a contiguous quarter of
-// the split's tokens, and merge their softmax states in LDS at the end (for
-// small grids: 4x the waves without the cost of 4x the global splits).
+// kWpi = 1: the workgroup's kAttnWaves waves take one (batch, KV head,
+// split) item each.  kWpi = kItemWaves: its waves share one item, each a
+// contiguous 1/kWpi of the split's tokens, and merge their softmax states in
+// LDS at the end (for small grids: kWpi x the waves without the cost of
+// kWpi x the global splits).
+// The re-tiled mode asks for three waves per SIMD: the compiler then keeps
+// the MFMA accumulators in ordinary VGPRs (140 in all, no spills) instead of
+// splitting 135 VGPRs + 36 AGPRs, which allowed only two.
 template <int kMode, int kWpi>
-__global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnParams p) {
+__global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
+                             kMode == kModeRetiled ? 3 : 1) void attn_kernel(AttnParams p) {
   constexpr bool kDense = kMode == kModeDense;
   extern __shared__ __attribute__((aligned(16))) uint8_t attn_smem[];
   DecodeTables& T = *reinterpret_cast<DecodeTables*>(attn_smem);
@@ -444,40 +450,100 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnParams p) {
   }
 }
 
-// Merges the split partials of one (batch, head): 128 threads, one per dim.
-__global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(AttnParams p) {
-  const int bh = blockIdx.x;
-  const int d = threadIdx.x;
-  const float* ml = p.ws_ml + (int64_t)bh * p.splits * 2;
-  float m = -INFINITY;
-  for (int s = 0; s < p.splits; ++s) m = fmaxf(m, ml[2 * s]);
-  const float m_use = m == -INFINITY ? 0.f : m;
-  float lsum = 0.f, acc = 0.f;
-  const float* wo = p.ws_o + (int64_t)bh * p.splits * kHeadDim + d;
-  for (int s = 0; s < p.splits; ++s) {
-    const float sc = ml[2 * s + 1] > 0.f ? __builtin_amdgcn_exp2f(ml[2 * s] - m_use) : 0.f;
-    lsum += ml[2 * s + 1] * sc;
-    acc += wo[(int64_t)s * kHeadDim] * sc;
+// Merges the split partials of one (batch, head) with four waves: the split
+// weights exp2(m_s - m) are computed once per chunk of splits into LDS, then
+// wave w takes splits 8w..8w+7 of every 32 (lane l owns dims 2l, 2l+1), so
+// each wave has eight independent partial-output loads in flight and the
+// four wave sums meet in LDS.
+constexpr int kCombineChunk = 512;
+constexpr int kCombineThreads = 256;
+
+__device__ __forceinline__ float block256_reduce(float x, bool is_max, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float y = __shfl_xor(x, off);
+    x = is_max ? fmaxf(x, y) : x + y;
   }
-  const float v = lsum > 0.f ? acc / lsum : 0.f;
-  p.out[(int64_t)bh * kHeadDim + d] = (uint16_t)f32_to_bf16_bits(v);
-  if (p.lse && d == 0)
-    p.lse[bh] = lsum > 0.f ? (m + __log2f(lsum)) * 0.6931471805599453f : -INFINITY;
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  const float r = is_max ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]))
+                         : (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnParams p) {
+  __shared__ float sc[kCombineChunk];
+  __shared__ float red[4];
+  __shared__ float2 part[3][64];
+  const int bh = blockIdx.x;
+  const int t = threadIdx.x, w = t >> 6, l = t & 63;
+  const int S = p.splits;
+  const float* ml = p.ws_ml + (int64_t)bh * S * 2;
+  float m = -INFINITY;
+  for (int s = t; s < S; s += kCombineThreads) m = fmaxf(m, ml[2 * s]);
+  m = block256_reduce(m, true, red);
+  const float m_use = m == -INFINITY ? 0.f : m;
+  float lpart = 0.f;
+  float2 acc = {0.f, 0.f};
+  const float* wo = p.ws_o + (int64_t)bh * S * kHeadDim + 2 * l;
+  for (int c0 = 0; c0 < S; c0 += kCombineChunk) {
+    const int n = min(S - c0, kCombineChunk);
+    for (int i = t; i < n; i += kCombineThreads) {
+      const float2 e = *reinterpret_cast<const float2*>(ml + 2 * (c0 + i));
+      const float wgt = e.y > 0.f ? __builtin_amdgcn_exp2f(e.x - m_use) : 0.f;
+      sc[i] = wgt;
+      lpart += e.y * wgt;
+    }
+    __syncthreads();
+    const float* wc = wo + (int64_t)c0 * kHeadDim;
+    for (int i0 = 8 * w; i0 < n; i0 += 32) {
+      float2 x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        x[j] = i0 + j < n ? *reinterpret_cast<const float2*>(wc + (int64_t)(i0 + j) * kHeadDim)
+                          : float2{0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float g = i0 + j < n ? sc[i0 + j] : 0.f;
+        acc.x += x[j].x * g;
+        acc.y += x[j].y * g;
+      }
+    }
+    __syncthreads();
+  }
+  const float lsum = block256_reduce(lpart, false, red);
+  if (w > 0) part[w - 1][l] = acc;
+  __syncthreads();
+  if (w == 0) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      acc.x += part[i][l].x;
+      acc.y += part[i][l].y;
+    }
+    const float vx = lsum > 0.f ? acc.x / lsum : 0.f, vy = lsum > 0.f ? acc.y / lsum : 0.f;
+    *reinterpret_cast<uint32_t*>(p.out + (int64_t)bh * kHeadDim + 2 * l) =
+        f32_to_bf16_bits(vx) | (f32_to_bf16_bits(vy) << 16);
+    if (p.lse && l == 0)
+      p.lse[bh] = lsum > 0.f ? (m + __log2f(lsum)) * 0.6931471805599453f : -INFINITY;
+  }
 }
 
 // Workgroups of four waves per item take grids of fewer than this many items.
 constexpr int kSharedItemsBelow = 2048;
 
-static int attn_auto_splits(int batch, int heads_k, int seqlen_k) {
+static int attn_auto_splits(int batch, int heads_k, int seqlen_k, bool compressed) {
   // One wave per item: about 2048 waves, at least 256 tokens per split.
-  // Smaller grids run four waves per item (attn_launch); there about 256
-  // items (1024 waves) measure best -- B=1: T=4k 44 -> 21 us, T=32k
-  // 85 -> 51 us -- so fewer global splits.
+  // Smaller grids run four waves per item (attn_launch).  There the
+  // compressed modes, whose record -> exponent-stream loads form a longer
+  // latency chain, measure best at about 512 items (2048 waves; B=1 T=32k
+  // 43 -> 34 us, B=8 T=4k 43 -> 32 us) and the dense mode at about 256.
   const int units = std::max(1, batch * heads_k);
   const int max_splits = std::max(1, (seqlen_k + 255) / 256);
   const int s1 = std::min(max_splits, std::max(1, (2048 + units - 1) / units));
   if ((int64_t)s1 * units >= kSharedItemsBelow) return s1;
-  return std::min(max_splits, std::max(1, (256 + units - 1) / units));
+  const int items = compressed ? 512 : 256;
+  return std::min(max_splits, std::max(1, (items + units - 1) / units));
 }
 
 static int attn_chunk(int seqlen_k, int splits) {
@@ -500,18 +566,19 @@ static int attn_launch(hipStream_t st, AttnParams& p, void* workspace, size_t ws
   const int items = p.batch * p.heads_k * p.splits;
   if (items < kSharedItemsBelow && p.chunk > 64) {
     // small grid: four waves per item
-    const size_t lds = std::max<size_t>(AttnLds<kMode>::kBytes, kCombineBytes);
-    hipLaunchKernelGGL((attn_kernel<kMode, kAttnWaves>), dim3(items), dim3(kAttnWaves * 64), lds,
+    const size_t lds = std::max<size_t>(AttnLds<kMode>::bytes(kItemWaves), kCombineBytes);
+    hipLaunchKernelGGL((attn_kernel<kMode, kItemWaves>), dim3(items), dim3(kItemWaves * 64), lds,
                        st, p);
   } else {
     const int grid = (items + kAttnWaves - 1) / kAttnWaves;
-    const size_t lds = AttnLds<kMode>::kBytes;
+    const size_t lds = AttnLds<kMode>::bytes(kAttnWaves);
     hipLaunchKernelGGL((attn_kernel<kMode, 1>), dim3(grid), dim3(kAttnWaves * 64), lds, st, p);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   if (p.splits > 1) {
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(p.batch * p.heads), dim3(kHeadDim), 0, st, p);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(p.batch * p.heads), dim3(kCombineThreads), 0, st,
+                       p);
     e = hipGetLastError();
   }
   return e == hipSuccess ? ZS_OK : (int)e;
@@ -522,6 +589,8 @@ static int attn_common_checks(int batch, int heads, int heads_k, int head_dim, i
   if (!q || !out || batch <= 0 || heads <= 0 || heads_k <= 0 || seqlen_k < 0 || num_splits < 0)
     return ZS_E_INVAL;
   if (heads % heads_k) return ZS_E_INVAL;
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out)) & 15)
+    return ZS_E_INVAL;  // 16-byte q rows in, 8-byte out stores
   if (head_dim != kHeadDim || heads / heads_k > 16) return ZS_E_UNSUPPORTED;
   return ZS_OK;
 }
@@ -627,7 +696,8 @@ extern "C" int zs_decode_attention(void* stream, const uint16_t* q, const zs_kv_
   p.heads = num_heads;
   p.heads_k = num_heads_k;
   p.group = num_heads / num_heads_k;
-  p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k);
+  p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k,
+                                                                 k->layout != ZS_LAYOUT_TOKEN_MAJOR);
   p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
   p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
@@ -698,7 +768,8 @@ extern "C" int zs_decode_attention_retiled(void* stream, const uint16_t* q,
   p.heads = num_heads;
   p.heads_k = num_heads_k;
   p.group = num_heads / num_heads_k;
-  p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k);
+  p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k,
+                                                                 k->layout != ZS_LAYOUT_TOKEN_MAJOR);
   p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
   p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
@@ -747,7 +818,7 @@ extern "C" int zs_decode_attention_dense(void* stream, const uint16_t* q, const 
   p.heads = num_heads;
   p.heads_k = num_heads_k;
   p.group = num_heads / num_heads_k;
-  p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k);
+  p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k, false);
   p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
   p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
