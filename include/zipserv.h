@@ -290,6 +290,22 @@ int zs_decode_attention_dense(void* stream, const uint16_t* q, const uint16_t* k
                               float* softmax_lse, void* workspace, size_t workspace_bytes,
                               int num_splits);
 
+/* The same over a paged dense cache (flash_attn_interface.py:1583-1658
+ * flash_attn_with_kvcache(..., block_table=) -> flash_api.cpp mha_fwd_kvcache,
+ * flash_fwd_kernel.h:1229-1239,1410-1420): k_cache / v_cache are pages
+ * [num_blocks][page_block_size][num_heads_k][head_dim]; token t of sequence
+ * b is row t % page_block_size of page block_table[b * max_blocks_per_seq +
+ * t / page_block_size].  page_block_size must be a multiple of 16 (the
+ * reference's paged FlashInfer runs use 16; its FlashAttention path asks for
+ * multiples of 256); block_table entries must lie in [0, num_blocks). */
+int zs_decode_attention_dense_paged(void* stream, const uint16_t* q, const uint16_t* k_cache,
+                                    const uint16_t* v_cache, const int32_t* block_table,
+                                    int max_blocks_per_seq, int num_blocks, int page_block_size,
+                                    const int32_t* cache_seqlens, int seqlen_k, int batch,
+                                    int num_heads, int num_heads_k, int head_dim,
+                                    float softmax_scale, uint16_t* out, float* softmax_lse,
+                                    void* workspace, size_t workspace_bytes, int num_splits);
+
 #ifdef __cplusplus
 }
 #endif

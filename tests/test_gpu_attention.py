@@ -171,3 +171,143 @@ def test_attention_rejects_unsupported(torch_cuda):
     bad.head_stride_rows = 32
     assert call(bad, d) == zs._lib.ZS_E_INVAL
     del keep
+
+
+def test_fwd_kvcache_zipserv_standalone(torch_cuda):
+    # csrc/flash_attn_ck/zipserv_fwd_kvcache.cu:380-533 (fwd_kvcache_zipserv):
+    # B = 1, head-major streams passed one by one, logical_kv_len tokens.
+    import zipserv_asplos26_amd as zs
+    import zipserv_asplos26_amd.attention as za
+    torch = torch_cuda
+    rng = np.random.default_rng(17)
+    T, Hkv, H, D, L = 200, 8, 64, 128, 150
+    k = kv_bf16(rng, 1, T, Hkv, D)
+    v = kv_bf16(rng, 1, T, Hkv, D)
+    q = normal_bf16(rng, (1, H, D))
+    kd, vd, qd = to_torch_bf16(k), to_torch_bf16(v), to_torch_bf16(q)
+    pk = zs.compress_zipserv(za.pad_batched_kv_prefix_by_kv_head(kd)[0].contiguous())
+    pv = zs.compress_zipserv(za.pad_batched_kv_prefix_by_kv_head(vd)[0].contiguous())
+
+    def args(parts):
+        m = parts[7].tolist()
+        return list(parts[:7]) + [m[0], m[1], m[4], m[5], m[6]]
+    scale = 1.0 / np.sqrt(D)
+    out, lse = za.fwd_kvcache_zipserv(qd.view(1, 1, H, D), *args(pk), *args(pv), L, Hkv, scale)
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (1, 1, H, D) and tuple(lse.shape) == (1, H, 1)
+    ref, ref_lse = zo.decode_attention_f64(q, k[:, :L], v[:, :L])
+    o = _bf16_f32(from_torch_bf16(out.view(1, H, D)))
+    tol = 2e-3 + np.abs(ref) * 2.0 ** -7 + np.abs(_bf16_f32(v)).max() * 2.0 ** -9
+    assert np.all(np.abs(o - ref) <= tol)
+    np.testing.assert_allclose(lse.view(1, H).cpu().numpy(), ref_lse, rtol=1e-4, atol=1e-3)
+    # the reference's argument checks
+    with pytest.raises(ValueError):  # batch 2
+        za.fwd_kvcache_zipserv(qd.view(1, 1, H, D).expand(2, 1, H, D).contiguous(), *args(pk),
+                               *args(pv), L, Hkv, scale)
+    with pytest.raises(ValueError):  # num_kv_heads != 8
+        za.fwd_kvcache_zipserv(qd.view(1, 1, H, D), *args(pk), *args(pv), L, 4, scale)
+    with pytest.raises(ValueError):  # more tokens than the rows hold
+        za.fwd_kvcache_zipserv(qd.view(1, 1, H, D), *args(pk), *args(pv), 257, Hkv, scale)
+
+
+def _paged(torch, x, page, rng):
+    """(B, T, Hkv, D) torch cache -> pages in a random order + block table."""
+    import zipserv_asplos26_amd.attention as za
+    pages, per_seq = za.make_batched_paged_kv_cache(x, page)
+    perm = rng.permutation(pages.shape[0])          # physical slot of logical page i
+    shuffled = torch.empty_like(pages)
+    shuffled[torch.as_tensor(perm, device=pages.device)] = pages
+    bt = torch.as_tensor(perm.reshape(x.shape[0], per_seq), dtype=torch.int32, device=x.device)
+    return shuffled, bt
+
+
+@pytest.mark.parametrize("page,B,T,seqlens,splits", [
+    (16, 2, 300, None, 0), (16, 4, 300, [300, 17, 0, 64], 0), (32, 3, 1000, None, 3),
+    (256, 2, 700, [700, 513], 1), (16, 1, 4096, None, 0)])
+def test_attention_dense_paged(torch_cuda, page, B, T, seqlens, splits):
+    # block_table path of flash_attn_with_kvcache (flash_fwd_kernel.h:1229-1239):
+    # pages in a shuffled order give the contiguous cache's result bit for bit
+    import zipserv_asplos26_amd.attention as za
+    torch = torch_cuda
+    rng = np.random.default_rng(page + B)
+    Hkv, H, D = 8, 64, 128
+    k = kv_bf16(rng, B, T, Hkv, D)
+    v = kv_bf16(rng, B, T, Hkv, D)
+    q = normal_bf16(rng, (B, H, D))
+    kd, vd, qd = to_torch_bf16(k), to_torch_bf16(v), to_torch_bf16(q)
+    kp, bt = _paged(torch, kd, page, rng)
+    vp = torch.empty_like(kp)
+    vp[bt.view(-1).long()] = za.make_batched_paged_kv_cache(vd, page)[0]
+    sl = None if seqlens is None else torch.tensor(seqlens, dtype=torch.int32, device="cuda")
+    cap = bt.shape[1] * page
+    kc = torch.zeros(B, cap, Hkv, D, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    kc[:, :T], vc[:, :T] = kd, vd
+    out, lse = za.flash_attn_with_kvcache_dense(qd.view(B, 1, H, D), kp, vp, cache_seqlens=sl,
+                                                num_splits=splits, return_softmax_lse=True,
+                                                block_table=bt)
+    outc, lsec = za.flash_attn_with_kvcache_dense(qd.view(B, 1, H, D), kc, vc, cache_seqlens=sl,
+                                                  num_splits=splits, return_softmax_lse=True)
+    torch.cuda.synchronize()
+    if seqlens is None:  # the contiguous cache runs to its capacity: compare on T tokens
+        sl_np = [T] * B
+        out, lse = za.flash_attn_with_kvcache_dense(
+            qd.view(B, 1, H, D), kp, vp, cache_seqlens=T, num_splits=splits,
+            return_softmax_lse=True, block_table=bt)
+        outc, lsec = za.flash_attn_with_kvcache_dense(
+            qd.view(B, 1, H, D), kc, vc, cache_seqlens=T, num_splits=splits,
+            return_softmax_lse=True)
+    else:
+        sl_np = seqlens
+    assert torch.equal(out.view(torch.int16), outc.view(torch.int16))
+    o = from_torch_bf16(out.view(B, H, D))
+    ref, ref_lse = zo.decode_attention_f64(q, k, v, seqlens=sl_np)
+    _check((q, k, v, o, lse.cpu().numpy(), o, lse.cpu().numpy(), ref, ref_lse), sl_np)
+
+
+def test_attention_dense_paged_rejects(torch_cuda):
+    import zipserv_asplos26_amd as zs
+    torch = torch_cuda
+    q = torch.zeros(1, 64, 128, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty_like(q)
+    kp = torch.zeros(4, 16, 8, 128, dtype=torch.bfloat16, device="cuda")
+    bt = torch.zeros(1, 4, dtype=torch.int32, device="cuda")
+    L = zs.lib()
+
+    def call(page=16, maxb=4, nblocks=4, T=64, table=bt):
+        return L.zs_decode_attention_dense_paged(
+            0, q.data_ptr(), kp.data_ptr(), kp.data_ptr(), 0 if table is None else table.data_ptr(),
+            maxb, nblocks, page, None, T, 1, 64, 8, 128, 0.1, out.data_ptr(), None, None, 0, 1)
+    assert call() == 0
+    torch.cuda.synchronize()
+    assert call(page=8) == zs._lib.ZS_E_UNSUPPORTED       # pages of whole medians only
+    assert call(T=65) == zs._lib.ZS_E_INVAL               # table too short for seqlen_k
+    assert call(table=None) == zs._lib.ZS_E_INVAL
+    assert call(nblocks=0) == zs._lib.ZS_E_INVAL
+
+
+@pytest.mark.parametrize("retiled", [False, True])
+def test_compress_kv_paged_staged(torch_cuda, retiled):
+    # layout "paged" (bench_zipserv_decode_attention.py:357-364,492-521): the
+    # compressed token-major cache decompresses to the reference's dense pages
+    # bit for bit, and attention over it (fused) equals the dense paged kernel
+    import zipserv_asplos26_amd.attention as za
+    torch = torch_cuda
+    rng = np.random.default_rng(23)
+    B, T, Hkv, H, D, page = 2, 300, 8, 64, 128, 16
+    kd = to_torch_bf16(kv_bf16(rng, B, T, Hkv, D))
+    vd = to_torch_bf16(kv_bf16(rng, B, T, Hkv, D))
+    qd = to_torch_bf16(normal_bf16(rng, (B, H, D)))
+    ck = za.compress_kv(kd, layout="paged", retiled=retiled, page_block_size=page)
+    cv = za.compress_kv(vd, layout="paged", retiled=retiled, page_block_size=page)
+    kp = za.decompress_to_batched_paged_kv(ck, B, Hkv, D, page)
+    vp = za.decompress_to_batched_paged_kv(cv, B, Hkv, D, page)
+    ref_pages, per_seq = za.make_batched_paged_kv_cache(kd, page)
+    assert torch.equal(kp.view(torch.int16), ref_pages.view(torch.int16))
+    bt = torch.arange(B * per_seq, dtype=torch.int32, device="cuda").view(B, per_seq)
+    # one split each: the same token chunks although seqlen_k differs (300 / 304)
+    out = za.flash_attn_with_kvcache_zipserv(qd.view(B, 1, H, D), ck, cv, Hkv, T, num_splits=1)
+    outp = za.flash_attn_with_kvcache_dense(qd.view(B, 1, H, D), kp, vp, cache_seqlens=T,
+                                            block_table=bt, num_splits=1)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), outp.view(torch.int16))

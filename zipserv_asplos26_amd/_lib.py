@@ -77,6 +77,9 @@ SIGNATURES = {
     "zs_decode_attention_dense": (
         C.c_int, [_p, _p, _p, _p, _p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                   C.c_float, _p, _p, _p, C.c_size_t, C.c_int]),
+    "zs_decode_attention_dense_paged": (
+        C.c_int, [_p, _p, _p, _p, _p, C.c_int, C.c_int, C.c_int, _p, C.c_int, C.c_int, C.c_int,
+                  C.c_int, C.c_int, C.c_float, _p, _p, _p, C.c_size_t, C.c_int]),
 }
 
 

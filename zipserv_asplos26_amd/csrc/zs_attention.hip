@@ -41,6 +41,7 @@ constexpr int kVBytes = 16 * kVRow;         // 16 tokens x 64 dims (+ pad)
 constexpr int kModeCanon = 0;    // canonical TCA-TBE streams
 constexpr int kModeDense = 1;    // dense bf16 caches
 constexpr int kModeRetiled = 2;  // re-tiled records (zs_rdecode.hpp)
+constexpr int kModePaged = 3;    // dense bf16 caches in pages through a block table
 
 template <int kMode>
 struct AttnLds {
@@ -62,7 +63,9 @@ struct AttnParams {
   const uint8_t* vexp;
   const int32_t* veo;
   const uint16_t* kd;           // dense caches [B][cap][Hkv][D] (dense kernel)
-  const uint16_t* vd;
+  const uint16_t* vd;           //   or pages [blocks][page][Hkv][D] (paged kernel)
+  const int32_t* block_table;   // [B][bt_stride] physical page of each logical page
+  int bt_stride, page;          // page: tokens per page, a multiple of 16
   int k_start, v_start;         // start_exp of K and V
   int k_bsr, k_hsr, v_bsr, v_hsr;  // batch / head strides in rows (compressed)
   int cap;                      // dense cache capacity (tokens)
@@ -124,7 +127,7 @@ constexpr int kCombineBytes = kItemWaves * 34 * 64 * 4;
 template <int kMode, int kWpi>
 __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
                              kMode == kModeRetiled ? 3 : 1) void attn_kernel(AttnParams p) {
-  constexpr bool kDense = kMode == kModeDense;
+  constexpr bool kDense = kMode == kModeDense || kMode == kModePaged;
   extern __shared__ __attribute__((aligned(16))) uint8_t attn_smem[];
   DecodeTables& T = *reinterpret_cast<DecodeTables*>(attn_smem);
   RTables& RT = *reinterpret_cast<RTables*>(attn_smem);
@@ -189,9 +192,25 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
   const uint8_t* bmv = l < 8 ? p.v.bm1 : (l < 16 ? p.v.bm2 : p.v.bm3);
 
   // Dense rows: token of lane l in median `med`, clamped to the valid range.
+  // Paged caches: a median (16 tokens from a multiple of 16) lies in one
+  // page; lane i of `pdelta` holds (physical - logical page) * page for
+  // median 64 * pchunk + i, loaded once per 64 medians, so the row of token t
+  // is t + pdelta[med].
+  int pdelta = 0, pchunk = -1;
   auto dense_row = [&](const uint16_t* base, int med) -> const uint16_t* {
     const int t = min(t0 + 16 * med + (l & 15), L - 1);
-    return base + (((int64_t)b * p.cap + t) * p.heads_k + h) * kHeadDim + 8 * (l >> 4);
+    if constexpr (kMode == kModePaged) {
+      const int ch = med >> 6;
+      if (ch != pchunk) {
+        const int lp = (t0 + 16 * min(64 * ch + l, nmed - 1)) / p.page;
+        pdelta = (p.block_table[(int64_t)b * p.bt_stride + lp] - lp) * p.page;
+        pchunk = ch;
+      }
+      const int64_t row = (int64_t)t + __builtin_amdgcn_readlane(pdelta, med & 63);
+      return base + (row * p.heads_k + h) * kHeadDim + 8 * (l >> 4);
+    } else {
+      return base + (((int64_t)b * p.cap + t) * p.heads_k + h) * kHeadDim + 8 * (l >> 4);
+    }
   };
 
   // One step: consume the fragments (a0, a1) of step type TY (0 = K0, 1 = K1,
@@ -823,4 +842,40 @@ extern "C" int zs_decode_attention_dense(void* stream, const uint16_t* q, const 
   p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
   return attn_launch<kModeDense>((hipStream_t)stream, p, workspace, workspace_bytes);
+}
+
+extern "C" int zs_decode_attention_dense_paged(
+    void* stream, const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+    const int32_t* block_table, int max_blocks_per_seq, int num_blocks, int page_block_size,
+    const int32_t* cache_seqlens, int seqlen_k, int batch, int num_heads, int num_heads_k,
+    int head_dim, float softmax_scale, uint16_t* out, float* softmax_lse, void* workspace,
+    size_t workspace_bytes, int num_splits) {
+  int stc = attn_common_checks(batch, num_heads, num_heads_k, head_dim, seqlen_k, num_splits, q,
+                               out);
+  if (stc != ZS_OK) return stc;
+  if (!k_cache || !v_cache || !block_table || num_blocks <= 0 || max_blocks_per_seq <= 0)
+    return ZS_E_INVAL;
+  if (page_block_size <= 0 || (page_block_size % 16)) return ZS_E_UNSUPPORTED;
+  if ((int64_t)max_blocks_per_seq * page_block_size < seqlen_k) return ZS_E_INVAL;
+  if ((int64_t)num_blocks * page_block_size > INT32_MAX) return ZS_E_OVERFLOW;
+  AttnParams p{};
+  p.kd = k_cache;
+  p.vd = v_cache;
+  p.block_table = block_table;
+  p.bt_stride = max_blocks_per_seq;
+  p.page = page_block_size;
+  p.q = q;
+  p.out = out;
+  p.lse = softmax_lse;
+  p.seqlens = cache_seqlens;
+  p.seqlen_k = seqlen_k;
+  p.batch = batch;
+  p.heads = num_heads;
+  p.heads_k = num_heads_k;
+  p.group = num_heads / num_heads_k;
+  p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k, false);
+  p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
+  p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
+  p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  return attn_launch<kModePaged>((hipStream_t)stream, p, workspace, workspace_bytes);
 }

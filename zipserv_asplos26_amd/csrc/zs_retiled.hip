@@ -320,24 +320,24 @@ __global__ __launch_bounds__(256) void rdecompress_kernel(const uint8_t* fixed,
 // ZipGEMM over the re-tiled layout, narrow batches.  Workgroup = WAVES waves
 // on F consecutive 16-row bands x one split-K slice x 16*NB columns; wave w
 // takes K tiles kb0+w, kb0+w+WAVES, ... of all F bands, so each X fragment
-// it loads feeds F records (X bytes per record / F).  Records are fetched
-// three tiles ahead into a register ring, their outlier bytes staged one tile
+// it loads feeds F records (X bytes per record / F).  Records are fetched D
+// tiles ahead into a register ring, their outlier bytes staged one tile
 // ahead, X one tile ahead.
 // ---------------------------------------------------------------------------
-template <int F, int NB, int WAVES>
+template <int F, int NB, int WAVES, int D>
 struct RGemmSmem {
-  static constexpr int kMain = (int)sizeof(RTables) + WAVES * 3 * F * kExpStage;
+  static constexpr int kMain = (int)sizeof(RTables) + WAVES * D * F * kExpStage;
   static constexpr int kRed = (WAVES / 2) * F * NB * 64 * 16;
   static constexpr int kBytes = kMain > kRed ? kMain : kRed;
 };
 
-template <int F, int NB, int WAVES>
+template <int F, int NB, int WAVES, int D>
 __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
                                                            const uint8_t* exps,
                                                            const int32_t* eoff, int start_exp,
                                                            const uint16_t* X, uint16_t* Y, int M,
                                                            int N, int K, int kb_per_split) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[RGemmSmem<F, NB, WAVES>::kBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[RGemmSmem<F, NB, WAVES, D>::kBytes];
   RTables& T = *reinterpret_cast<RTables*>(smem);
   build_r_tables(T, threadIdx.x, blockDim.x);
   const RExp ex = r_exp(start_exp);
@@ -345,8 +345,8 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
-  // stage s of band f: smem + sizeof(RTables) + ((w * 3 + s) * F + f) * kExpStage
-  uint8_t* stg = smem + sizeof(RTables) + w * 3 * F * kExpStage;
+  // stage s of band f: smem + sizeof(RTables) + ((w * D + s) * F + f) * kExpStage
+  uint8_t* stg = smem + sizeof(RTables) + w * D * F * kExpStage;
   const int bands = M >> 4;
   const int band0 = blockIdx.x * F;
   const int split = blockIdx.y;
@@ -378,8 +378,8 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
       oe0[f] = eoff[ri];
       oe1[f] = eoff[ri + 1];
     }
-    RStage R0[F], R1[F], R2[F];
-    RMeta M0[F], M1[F], M2[F];
+    RStage R[D][F];
+    RMeta MT[D][F];
     bf16x8 xc[2][NB], xn[2][NB];
 #define RZ_LOADX(J, DST)                                                          \
   {                                                                               \
@@ -424,17 +424,16 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
         }                                                                                  \
       }                                                                                    \
     }                                                                                      \
-    RZ_ISSUE(min((J) + 3, last), RC, MC);                                                  \
+    RZ_ISSUE(min((J) + D, last), RC, MC);                                                  \
   }
-    RZ_ISSUE(0, R0, M0);
-    RZ_ISSUE(min(1, last), R1, M1);
-    RZ_ISSUE(min(2, last), R2, M2);
+#pragma unroll
+    for (int k = 0; k < D; ++k) RZ_ISSUE(min(k, last), R[k], MT[k]);
     RZ_LOADX(0, xn);
-    RZ_STAGE(0, R0, M0);
-    for (int j = 0; j < n; j += 3) {
-      RZ_STEP(j, 0, 1, R0, M0, R1, M1);
-      RZ_STEP(j + 1, 1, 2, R1, M1, R2, M2);
-      RZ_STEP(j + 2, 2, 0, R2, M2, R0, M0);
+    RZ_STAGE(0, R[0], MT[0]);
+    for (int j = 0; j < n; j += D) {
+#pragma unroll
+      for (int k = 0; k < D; ++k)
+        RZ_STEP(j + k, k, (k + 1) % D, R[k], MT[k], R[(k + 1) % D], MT[(k + 1) % D]);
     }
 #undef RZ_STEP
 #undef RZ_STAGE
@@ -689,9 +688,9 @@ template <int F, int NB>
 static hipError_t launch_rgemm(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
                                const int32_t* eoff, int start_exp, const uint16_t* X,
                                uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split) {
-  constexpr int kWaves = 8;
+  constexpr int kWaves = 8, kDepth = 3;
   dim3 grid((M / 16 + F - 1) / F, split_k, (N + NB * 16 - 1) / (NB * 16));
-  hipLaunchKernelGGL((rgemm_kernel<F, NB, kWaves>), grid, dim3(kWaves * 64), 0, st, fixed, exps,
+  hipLaunchKernelGGL((rgemm_kernel<F, NB, kWaves, kDepth>), grid, dim3(kWaves * 64), 0, st, fixed, exps,
                      eoff, start_exp, X, Y, M, N, K, kb_per_split);
   return hipGetLastError();
 }
