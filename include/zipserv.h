@@ -306,6 +306,41 @@ int zs_decode_attention_dense_paged(void* stream, const uint16_t* q, const uint1
                                     float softmax_scale, uint16_t* out, float* softmax_lse,
                                     void* workspace, size_t workspace_bytes, int num_splits);
 
+/* ---------------------------------------------------------------------- */
+/* Container: one compressed matrix as a self-checking byte image (no       */
+/* counterpart in the reference, which keeps compressed matrices only in    */
+/* memory as seven tensors plus the meta tensor of                          */
+/* zipserv_decode_attention_ext.cu:250-262).  Host memory only.  Layout:    */
+/* a 256-byte header (magic "ZSRVCNTR", version 1, layout, shape, window,   */
+/* max counts, name, per-stream sizes and CRC-32C, header CRC-32C) and the  */
+/* streams, each zero-padded to 64 bytes (csrc/zs_container.cpp).           */
+/* ---------------------------------------------------------------------- */
+#define ZS_CONTAINER_CANONICAL 0 /* 7 streams: SM, FULL, bitmap1..3, median, global */
+#define ZS_CONTAINER_RETILED 1   /* 3 streams: fixed records, exponents, offsets    */
+
+typedef struct zs_container_desc {
+  int32_t layout; /* ZS_CONTAINER_*                                         */
+  int32_t rows, cols, logical_rows, logical_cols;
+  int32_t start_exp, max_high_freq_count, max_full_count;
+  int32_t num_streams;
+  int64_t stream_bytes[8];
+} zs_container_desc_t;
+
+/* CRC-32C (Castagnoli) of `bytes` bytes continuing from `crc` (0 to start). */
+uint32_t zs_crc32c(uint32_t crc, const void* data, int64_t bytes);
+/* Bytes of the container for `d`, or a negative ZS_E_* if `d` is invalid
+ * (stream sizes the shape fixes, window range, stream counts). */
+int64_t zs_container_bytes(const zs_container_desc_t* d);
+/* Writes the container into dst (>= zs_container_bytes).  streams[i]: host
+ * pointers to the stream bytes in table order.  name: up to 63 bytes. */
+int zs_container_write(const zs_container_desc_t* d, const char* name,
+                       const void* const* streams, void* dst, int64_t dst_bytes);
+/* Validates a container image (magic, version, CRCs, sizes, totals) and
+ * returns its descriptor, name (64 bytes) and each stream's byte offset in
+ * src.  ZS_E_INVAL for a damaged image, ZS_E_UNSUPPORTED for another version. */
+int zs_container_parse(const void* src, int64_t src_bytes, zs_container_desc_t* d,
+                       char* name_out, int64_t* stream_offsets);
+
 #ifdef __cplusplus
 }
 #endif

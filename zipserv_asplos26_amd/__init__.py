@@ -6,6 +6,7 @@ C-ABI of include/zipserv.h; this package is the Python host-side mirror of the
 reference's operator interfaces (see codec.py and attention.py).
 """
 from ._lib import LIB_PATH, ZipServError, build, lib  # noqa: F401
+from . import container  # noqa: F401
 from .codec import (  # noqa: F401
     HostCompressed,
     ZipservCompressed,
@@ -30,5 +31,5 @@ __all__ = [
     "ZipservRetiled", "compress_retiled", "decompress_retiled", "retile",
     "analyze_exponents", "compress", "compress_host", "compress_zipserv", "decompress",
     "decompress_zipserv", "decompress_zipserv_into", "make_zipserv_compressed", "to_device",
-    "zipgemm",
+    "zipgemm", "container",
 ]

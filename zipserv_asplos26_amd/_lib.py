@@ -80,7 +80,30 @@ SIGNATURES = {
     "zs_decode_attention_dense_paged": (
         C.c_int, [_p, _p, _p, _p, _p, C.c_int, C.c_int, C.c_int, _p, C.c_int, C.c_int, C.c_int,
                   C.c_int, C.c_int, C.c_float, _p, _p, _p, C.c_size_t, C.c_int]),
+    "zs_crc32c": (C.c_uint32, [C.c_uint32, _p, _i64]),
+    "zs_container_bytes": (_i64, [_p]),
+    "zs_container_write": (C.c_int, [_p, C.c_char_p, _p, _p, _i64]),
+    "zs_container_parse": (C.c_int, [_p, _i64, _p, _p, _p]),
 }
+
+ZS_CONTAINER_CANONICAL = 0
+ZS_CONTAINER_RETILED = 1
+
+
+class ContainerDesc(C.Structure):
+    """zs_container_desc_t of include/zipserv.h."""
+    _fields_ = [
+        ("layout", _i32),
+        ("rows", _i32),
+        ("cols", _i32),
+        ("logical_rows", _i32),
+        ("logical_cols", _i32),
+        ("start_exp", _i32),
+        ("max_high_freq_count", _i32),
+        ("max_full_count", _i32),
+        ("num_streams", _i32),
+        ("stream_bytes", _i64 * 8),
+    ]
 
 
 class ZipServError(RuntimeError):
