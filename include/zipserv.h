@@ -306,6 +306,20 @@ int zs_decode_attention_dense_paged(void* stream, const uint16_t* q, const uint1
                                     float softmax_scale, uint16_t* out, float* softmax_lse,
                                     void* workspace, size_t workspace_bytes, int num_splits);
 
+/* Stage profiler of the re-tiled record pipeline
+ * (kernel_benchmark/zipserv_tile_stage_bench_ext.cu measure_zipserv_tile_stages):
+ * one wave consumes records record0 + i*stride (mod num_records), waiting
+ * out every memory operation and reading the shader clock between the steps.
+ * d_out (11 int64, device): mean cycles of [bracket, offsets, fixed, exps,
+ * stage, decode, mfma, record] over `iters` iterations after `warmup`, then
+ * the loop's total shader cycles and its s_memrealtime ticks (100 MHz), then
+ * a value that keeps the products live.  d_x: 16 x 64 bf16 MFMA tile;
+ * d_frag: 64 x 16 bf16, the last record's decoded operands in lane order. */
+int zs_measure_record_stages(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
+                             const int32_t* d_eoff, uint8_t start_exp, int M, int K,
+                             int64_t record0, int64_t stride, int warmup, int iters,
+                             const uint16_t* d_x, int64_t* d_out, uint16_t* d_frag);
+
 /* ---------------------------------------------------------------------- */
 /* Container: one compressed matrix as a self-checking byte image (no       */
 /* counterpart in the reference, which keeps compressed matrices only in    */

@@ -80,6 +80,9 @@ SIGNATURES = {
     "zs_decode_attention_dense_paged": (
         C.c_int, [_p, _p, _p, _p, _p, C.c_int, C.c_int, C.c_int, _p, C.c_int, C.c_int, C.c_int,
                   C.c_int, C.c_int, C.c_float, _p, _p, _p, C.c_size_t, C.c_int]),
+    "zs_measure_record_stages": (
+        C.c_int, [_p, _p, _p, _p, C.c_uint8, C.c_int, C.c_int, _i64, _i64, C.c_int, C.c_int,
+                  _p, _p, _p]),
     "zs_crc32c": (C.c_uint32, [C.c_uint32, _p, _i64]),
     "zs_container_bytes": (_i64, [_p]),
     "zs_container_write": (C.c_int, [_p, C.c_char_p, _p, _p, _i64]),
