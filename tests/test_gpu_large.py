@@ -95,3 +95,25 @@ def test_retiled_kv_and_attention_past_int32(torch_cuda):
         o = out[b, 0].float()
         tol = 2e-3 + ref.abs() * 2.0 ** -7 + vb.abs().max() * 2.0 ** -9
         assert bool(((o - ref).abs() <= tol).all()), float((o - ref).abs().max())
+
+
+def test_retiled_zipgemm_x_past_2gib(torch_cuda):
+    # X of more than 2^31 bytes: zs_retiled_mm runs it as row blocks (its
+    # kernels address X with 32-bit offsets); every row block must match
+    import zipserv_asplos26_amd as zs_
+    torch = torch_cuda
+    M, K, N = 64, 4096, (1 << 18) + 48
+    assert N * K * 2 > 2**31 - 1
+    g = torch.Generator(device="cuda")
+    g.manual_seed(13)
+    w = (torch.randn(M, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(N, K, device="cuda", generator=g).to(torch.bfloat16)
+    r = zs_.compress_retiled(w)
+    y = zs_.zipgemm(r, x)
+    ref = torch.empty(N, M, dtype=torch.float32, device="cuda")
+    wf = w.float().t().contiguous()
+    for n0 in range(0, N, 1 << 16):
+        ref[n0:n0 + (1 << 16)] = x[n0:n0 + (1 << 16)].float() @ wf
+    torch.cuda.synchronize()
+    err = float((y.float() - ref).abs().max() / ref.abs().max())
+    assert err < 1e-2, err

@@ -182,25 +182,36 @@ struct RMeta {
 
 __device__ __forceinline__ bool r_staged(const RMeta& mt) { return mt.nw <= kExpWords; }
 
-// Fixed part of record `rec` (no dependency on the outlier offsets).
-__device__ __forceinline__ void r_issue_fixed(const uint8_t* fixed, int64_t rec, RStage& s) {
-  const int l = lane_id();
-  const uint8_t* f = fixed + rec * kRecBytes;
-  s.r.sm = *reinterpret_cast<const u32x4*>(f + 16 * l);
-  s.r.p32 = *reinterpret_cast<const uint32_t*>(f + kRecP32 + 4 * l);
-  s.r.p16 = *reinterpret_cast<const uint16_t*>(f + kRecP16 + 2 * l);
+// Raw buffer resource over [base, base + bytes): word 3 is the gfx9-family
+// value for untyped dword access (data format 32).  Loads through it take a
+// wave-uniform base in SGPRs plus a 32-bit lane offset, so they cost no VALU
+// address arithmetic, and lanes past `bytes` read zeros.
+constexpr int kBufWord3 = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t r_buffer(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufWord3);
 }
 
-// Outlier bytes [e0, e1) of a record, as dwords from e0 & ~3.
+// Fixed part of record `rec` (no dependency on the outlier offsets).
+__device__ __forceinline__ void r_issue_fixed(const uint8_t* fixed, int64_t rec, RStage& s) {
+  const uint32_t l = (uint32_t)lane_id();
+  const __amdgpu_buffer_rsrc_t r = r_buffer(fixed + rec * kRecBytes, kRecBytes);
+  s.r.sm = __builtin_amdgcn_raw_buffer_load_b128(r, 16u * l, 0, 0);
+  s.r.p32 = __builtin_amdgcn_raw_buffer_load_b32(r, kRecP32 + 4u * l, 0, 0);
+  s.r.p16 = __builtin_amdgcn_raw_buffer_load_b16(r, kRecP16 + 2u * l, 0, 0);
+}
+
+// Outlier bytes [e0, e1) of a record, as dwords from e0 & ~3 (lane l: dword
+// l; lanes past the record's dwords read zeros).
 __device__ __forceinline__ void r_issue_exps(const uint8_t* exps, int e0, int e1, RStage& s,
                                              RMeta& mt) {
-  const int l = lane_id();
+  const uint32_t l = (uint32_t)lane_id();
   const int ea0 = e0 & ~3;
   const int nw = (e1 - ea0 + 3) >> 2;
   mt.e0 = e0;
   mt.rel = e0 - ea0;
   mt.nw = nw;
-  s.ex = *reinterpret_cast<const uint32_t*>(exps + ea0 + (l < nw ? 4 * l : 0));
+  s.ex = __builtin_amdgcn_raw_buffer_load_b32(r_buffer(exps + ea0, 4u * (uint32_t)nw), 4u * l, 0,
+                                              0);
 }
 
 __device__ __forceinline__ void r_issue(const uint8_t* fixed, const uint8_t* exps, int64_t rec,

@@ -359,10 +359,14 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
 #pragma unroll
   for (int f = 0; f < F; ++f) rec0[f] = (int64_t)min(band0 + f, bands - 1) * KT + kb0 + w;
 
-  const uint16_t* xrow[NB];
+  // X fragments: a buffer resource at the tile's column (wave-uniform) plus
+  // this lane's 32-bit byte offset (row n, 8 columns), so the loads need no
+  // per-tile VALU address arithmetic (N <= 16 here: offsets far below 2^31).
+  uint32_t xoff[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
-    xrow[nb] = X + (int64_t)min(n0 + nb * 16 + (l & 15), N - 1) * K + 8 * (l >> 4);
+    xoff[nb] = 2u * ((uint32_t)min(n0 + nb * 16 + (l & 15), N - 1) * (uint32_t)K +
+                     8u * (uint32_t)(l >> 4));
   f32x4 acc[F * NB];
 #pragma unroll
   for (int i = 0; i < F * NB; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -383,10 +387,13 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
     bf16x8 xc[2][NB], xn[2][NB];
 #define RZ_LOADX(J, DST)                                                          \
   {                                                                               \
-    const int kk_ = (kb0 + w + (c0 + (J)) * WAVES) * 64;                          \
+    const __amdgpu_buffer_rsrc_t xr_ =                                            \
+        r_buffer(X + (int64_t)(kb0 + w + (c0 + (J)) * WAVES) * 64, 0x7FFFFFFFu);  \
     _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                        \
-      DST[0][nb_] = *reinterpret_cast<const bf16x8*>(xrow[nb_] + kk_);            \
-      DST[1][nb_] = *reinterpret_cast<const bf16x8*>(xrow[nb_] + kk_ + 32);       \
+      DST[0][nb_] = __builtin_bit_cast(                                           \
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr_, xoff[nb_], 0, 0));   \
+      DST[1][nb_] = __builtin_bit_cast(                                           \
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr_, xoff[nb_] + 64u, 0, 0)); \
     }                                                                             \
   }
 #define RZ_ISSUE(J, R, MT)                                                              \
@@ -496,7 +503,7 @@ struct RWideSmem {
   static constexpr int kBytes = kMain > kRed ? kMain : kRed;
 };
 
-template <int NB, int BANDS, int PH>
+template <int NB, int BANDS, int PH, int RD>
 __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8_t* fixed,
                                                               const uint8_t* exps,
                                                               const int32_t* eoff, int start_exp,
@@ -534,14 +541,16 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
 
   // X tile loads of this thread: chunk c = t + 64*BANDS*i, row c/8, 16-byte
   // column c%8 (128*NB chunks per tile; threads past them load and drop).
+  // Sources are 32-bit byte offsets from a buffer resource at the tile's
+  // column (the host keeps N * K * 2 below 2^31).
   constexpr int kXC = (2 * NB + BANDS - 1) / BANDS;  // chunks per thread
-  const uint16_t* xsrc[kXC];
+  uint32_t xsrc[kXC];
   int xdst[kXC];
 #pragma unroll
   for (int i = 0; i < kXC; ++i) {
     const int c = t + 64 * BANDS * i;
     const int row = min(c >> 3, 16 * NB - 1), cc = c & 7;
-    xsrc[i] = X + (int64_t)min(n0 + row, N - 1) * K + 8 * cc;
+    xsrc[i] = 2u * ((uint32_t)min(n0 + row, N - 1) * (uint32_t)K + 8u * (uint32_t)cc);
     xdst[i] = c < 128 * NB ? row * kXRow + 16 * cc : -1;
   }
   f32x4 acc[NB];
@@ -568,9 +577,9 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
     r_issue(fixed, exps, rowrec + tile_of(j), e0, e1, R, Mt);
   };
   auto xload = [&](int j, u32x4 (&XR)[kXC]) {
-    const int kk = tile_of(j) * 64;
+    const __amdgpu_buffer_rsrc_t xr = r_buffer(X + (int64_t)tile_of(j) * 64, 0x7FFFFFFFu);
 #pragma unroll
-    for (int i = 0; i < kXC; ++i) XR[i] = *reinterpret_cast<const u32x4*>(xsrc[i] + kk);
+    for (int i = 0; i < kXC; ++i) XR[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, xsrc[i], 0, 0);
   };
   auto xwrite = [&](uint8_t* xb, const u32x4 (&XR)[kXC]) {
 #pragma unroll
@@ -582,14 +591,15 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   if (span == 0) {  // empty split-K slice (uniform per workgroup)
     __syncthreads();
   } else {
-  RStage R0, R1;
-  RMeta M0, M1;
+  static_assert(RD == 2 || RD == 4, "record ring of 2 or 4 steps");
+  RStage R[RD];
+  RMeta MT[RD];
   u32x4 XA[kXC], XB[kXC];
-  issue(0, R0, M0);
-  issue(1, R1, M1);
+#pragma unroll
+  for (int k = 0; k < RD; ++k) issue(k, R[k], MT[k]);
   xload(0, XA);
   xload(1, XB);
-  r_stage(stage0, R0, M0);
+  r_stage(stage0, R[0], MT[0]);
   xwrite(xb0, XA);
   xload(2, XA);
   __syncthreads();  // decode tables and X tile 0 visible
@@ -599,7 +609,7 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
     const RStage cs_ = RC;                                                           \
     const RMeta cm_ = MC;                                                            \
     r_stage(NXT, RN, MN);                                                            \
-    issue((S) + 2, RC, MC);                                                          \
+    issue((S) + RD, RC, MC);                                                         \
     if ((S) < cnt) {                                                                 \
       u32x4 a0_, a1_;                                                                \
       r_decode_staged(T, ex, cs_, cm_, CUR, exps, a0_, a1_);                         \
@@ -619,9 +629,15 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   }
   // Step s reads X buffer s%2; X registers: XB holds step s+1, XA step s+2
   // at the start of an even step (roles swap on odd steps).
-  for (int s = 0; s < steps; s += 2) {
-    RW_STEP(s, stage0, stage1, xb0, R0, M0, R1, M1, XB, XB);
-    if (s + 1 < steps) RW_STEP(s + 1, stage1, stage0, xb1, R1, M1, R0, M0, XA, XA);
+  // Record ring: step s consumes R[s % RD] and refills it with step s + RD.
+  for (int s = 0; s < steps; s += RD) {
+    RW_STEP(s, stage0, stage1, xb0, R[0], MT[0], R[1], MT[1], XB, XB);
+    if (s + 1 < steps)
+      RW_STEP(s + 1, stage1, stage0, xb1, R[1], MT[1], R[2 % RD], MT[2 % RD], XA, XA);
+    if constexpr (RD == 4) {
+      if (s + 2 < steps) RW_STEP(s + 2, stage0, stage1, xb0, R[2], MT[2], R[3], MT[3], XB, XB);
+      if (s + 3 < steps) RW_STEP(s + 3, stage1, stage0, xb1, R[3], MT[3], R[0], MT[0], XA, XA);
+    }
   }
 #undef RW_STEP
   }
@@ -695,12 +711,14 @@ static hipError_t launch_rgemm(hipStream_t st, const uint8_t* fixed, const uint8
   return hipGetLastError();
 }
 
+constexpr int kWideDepth = 2;  // records in flight per wave (ring of RD steps)
+
 template <int NB, int BANDS, int PH>
 static hipError_t launch_rwide(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
                                const int32_t* eoff, int start_exp, const uint16_t* X,
                                uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split) {
   dim3 grid(M / (16 * BANDS), split_k, (N + NB * 16 - 1) / (NB * 16));
-  hipLaunchKernelGGL((rgemm_wide_kernel<NB, BANDS, PH>), grid, dim3(BANDS * PH * 64), 0, st, fixed,
+  hipLaunchKernelGGL((rgemm_wide_kernel<NB, BANDS, PH, kWideDepth>), grid, dim3(BANDS * PH * 64), 0, st, fixed,
                      exps, eoff, start_exp, X, Y, M, N, K, kb_per_split);
   return hipGetLastError();
 }
@@ -824,6 +842,18 @@ extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t
   if (split_k < 1 || split_k > KT) return ZS_E_INVAL;
   if (split_k > 1 && !ws) return ZS_E_INVAL;
   if ((int64_t)M * N * split_k > INT32_MAX * 2LL) return ZS_E_OVERFLOW;
+  if ((int64_t)N * K * 2 > INT32_MAX) {
+    // The kernels address X with 32-bit byte offsets: run row blocks of X
+    // and Y that stay below 2^31 bytes, one after another on the stream.
+    const int rows = std::max(16, (int)(INT32_MAX / (2LL * K)) / 16 * 16);
+    for (int n0 = 0; n0 < N; n0 += rows) {
+      const int st_ = zs_retiled_mm(stream, d_fixed, d_exps, d_eoff, start_exp,
+                                    B + (int64_t)n0 * K, C + (int64_t)n0 * M, M,
+                                    std::min(rows, N - n0), K, ws, split_k);
+      if (st_ != ZS_OK) return st_;
+    }
+    return ZS_OK;
+  }
   hipStream_t st = (hipStream_t)stream;
   const int se = (int)start_exp;
   hipError_t e;
