@@ -71,6 +71,22 @@ __device__ __forceinline__ void build_r_tables(RTables& T, int tid, int nthreads
   for (int i = tid; i < 2048; i += nthreads) dst[i] = src[i];
 }
 
+// The same table specialised to one window: entry .x holds the group's four
+// in-window exponent bytes (v_perm of EXP_HI:EXP_LO by the codes) instead of
+// the codes, which saves that v_perm per group in every decode.  Built while
+// copying the image (one v_perm per entry).
+__device__ __forceinline__ void build_r_tables_exp(RTables& T, int tid, int nthreads,
+                                                   uint32_t exp_lo, uint32_t exp_hi) {
+  const uint4* src = reinterpret_cast<const uint4*>(kRTabImage.w);
+  uint4* dst = reinterpret_cast<uint4*>(T.tb);
+  for (int i = tid; i < 2048; i += nthreads) {
+    uint4 v = src[i];
+    v.x = __builtin_amdgcn_perm(exp_hi, exp_lo, v.x);
+    v.z = __builtin_amdgcn_perm(exp_hi, exp_lo, v.z);
+    dst[i] = v;
+  }
+}
+
 // Exponent bytes start_exp + 0..3 and + 4..7 (mod 256).
 struct RExp {
   uint32_t lo, hi;
@@ -133,7 +149,7 @@ __device__ __forceinline__ void r_pairs(uint32_t E, uint32_t sm, uint32_t& a, ui
 
 // Decodes one record into the two MFMA A operands (half 0, half 1).  `exb`
 // holds the record's outlier bytes, the first one at byte `rel`.
-template <typename P>
+template <bool kExpTab = false, typename P>
 __device__ __forceinline__ void r_decode(const RTables& T, RExp ex, const RecRegs& r, P exb,
                                          int rel, u32x4& o0, u32x4& o1) {
   const uint32_t c1 = __builtin_amdgcn_alignbit(r.p16, r.p32, 24);
@@ -148,10 +164,15 @@ __device__ __forceinline__ void r_decode(const RTables& T, RExp ex, const RecReg
   // windows of the second groups: past the first groups' outliers
   const uint32_t a2 = (uint32_t)((((uint64_t)a1 << 32) | a0) >> (8 * n0));
   const uint32_t b2 = (uint32_t)((((uint64_t)b1 << 32) | b0) >> (8 * n2));
-  const uint32_t e0 = __builtin_amdgcn_perm(__builtin_amdgcn_perm(ex.hi, ex.lo, t0.x), a0, t0.y);
-  const uint32_t e1 = __builtin_amdgcn_perm(__builtin_amdgcn_perm(ex.hi, ex.lo, t1.x), a2, t1.y);
-  const uint32_t e2 = __builtin_amdgcn_perm(__builtin_amdgcn_perm(ex.hi, ex.lo, t2.x), b0, t2.y);
-  const uint32_t e3 = __builtin_amdgcn_perm(__builtin_amdgcn_perm(ex.hi, ex.lo, t3.x), b2, t3.y);
+  // in-window exponent bytes: straight from a window-specialised table, or
+  // the codes mapped through EXP_HI:EXP_LO
+  auto inwin = [&](uint32_t x) {
+    return kExpTab ? x : __builtin_amdgcn_perm(ex.hi, ex.lo, x);
+  };
+  const uint32_t e0 = __builtin_amdgcn_perm(inwin(t0.x), a0, t0.y);
+  const uint32_t e1 = __builtin_amdgcn_perm(inwin(t1.x), a2, t1.y);
+  const uint32_t e2 = __builtin_amdgcn_perm(inwin(t2.x), b0, t2.y);
+  const uint32_t e3 = __builtin_amdgcn_perm(inwin(t3.x), b2, t3.y);
   uint32_t d[8];
   r_pairs(e0, r.sm[0], d[0], d[1]);
   r_pairs(e1, r.sm[1], d[2], d[3]);
@@ -227,13 +248,14 @@ __device__ __forceinline__ void r_stage(uint8_t* st, const RStage& s, const RMet
   if (r_staged(mt) && l < mt.nw) *reinterpret_cast<uint32_t*>(st + 4 * l) = s.ex;
 }
 
+template <bool kExpTab = false>
 __device__ __forceinline__ void r_decode_staged(const RTables& T, RExp ex, const RStage& s,
                                                 const RMeta& mt, const uint8_t* st,
                                                 const uint8_t* exps, u32x4& o0, u32x4& o1) {
   if (r_staged(mt))
-    r_decode(T, ex, s.r, st, mt.rel, o0, o1);
+    r_decode<kExpTab>(T, ex, s.r, st, mt.rel, o0, o1);
   else
-    r_decode(T, ex, s.r, exps + mt.e0, 0, o0, o1);
+    r_decode<kExpTab>(T, ex, s.r, exps + mt.e0, 0, o0, o1);
 }
 
 }  // namespace zs

@@ -295,8 +295,8 @@ __global__ __launch_bounds__(256) void rdecompress_kernel(const uint8_t* fixed,
                                                           uint16_t* out, int M, int K) {
   __shared__ RTables T;
   __shared__ __attribute__((aligned(16))) uint8_t stg[4][kExpStage];
-  build_r_tables(T, threadIdx.x, blockDim.x);
   const RExp ex = r_exp(start_exp);
+  build_r_tables_exp(T, threadIdx.x, blockDim.x, ex.lo, ex.hi);
   __syncthreads();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(256) void rdecompress_kernel(const uint8_t* fixed,
     r_issue(fixed, exps, rec, eoff[rec], eoff[rec + 1], s, mt);
     r_stage(stg[w], s, mt);
     u32x4 o0, o1;
-    r_decode_staged(T, ex, s, mt, stg[w], exps, o0, o1);
+    r_decode_staged<true>(T, ex, s, mt, stg[w], exps, o0, o1);
     const int64_t band = rec / KT, kt = rec % KT;
     uint16_t* dst = out + (band * 16 + (l & 15)) * (int64_t)K + kt * 64 + 8 * (l >> 4);
     *reinterpret_cast<u32x4*>(dst) = o0;
@@ -339,8 +339,8 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
                                                            int N, int K, int kb_per_split) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[RGemmSmem<F, NB, WAVES, D>::kBytes];
   RTables& T = *reinterpret_cast<RTables*>(smem);
-  build_r_tables(T, threadIdx.x, blockDim.x);
   const RExp ex = r_exp(start_exp);
+  build_r_tables_exp(T, threadIdx.x, blockDim.x, ex.lo, ex.hi);
   __syncthreads();
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -420,7 +420,7 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
     if ((J) < n) {                                                                         \
       _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_) {                                   \
         u32x4 a0_, a1_;                                                                    \
-        r_decode_staged(T, ex, RC[f_], MC[f_], stg + ((SC) * F + f_) * kExpStage, exps, a0_, \
+        r_decode_staged<true>(T, ex, RC[f_], MC[f_], stg + ((SC) * F + f_) * kExpStage, exps, a0_, \
                         a1_);                                                              \
         _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                             \
           f32x4& c_ = acc[f_ * NB + nb_];                                                  \
@@ -512,8 +512,8 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
                                                               int kb_per_split) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[RWideSmem<NB, BANDS, PH>::kBytes];
   RTables& T = *reinterpret_cast<RTables*>(smem);
-  build_r_tables(T, threadIdx.x, blockDim.x);
   const RExp ex = r_exp(start_exp);
+  build_r_tables_exp(T, threadIdx.x, blockDim.x, ex.lo, ex.hi);
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
@@ -612,7 +612,7 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
     issue((S) + RD, RC, MC);                                                         \
     if ((S) < cnt) {                                                                 \
       u32x4 a0_, a1_;                                                                \
-      r_decode_staged(T, ex, cs_, cm_, CUR, exps, a0_, a1_);                         \
+      r_decode_staged<true>(T, ex, cs_, cm_, CUR, exps, a0_, a1_);                         \
       _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                         \
         const uint8_t* bp_ = XCUR + brd + nb_ * 16 * kXRow;                          \
         const bf16x8 b0_ = *reinterpret_cast<const bf16x8*>(bp_);                    \

@@ -67,8 +67,8 @@ __global__ __launch_bounds__(64) void rstage_kernel(const uint8_t* fixed, const 
                                                     int64_t* out, uint16_t* frag) {
   __shared__ RTables T;
   __shared__ __attribute__((aligned(16))) uint8_t stg[kExpStage];
-  build_r_tables(T, threadIdx.x, 64);
   const RExp ex = r_exp(start_exp);
+  build_r_tables_exp(T, threadIdx.x, 64, ex.lo, ex.hi);
   __syncthreads();
   const int l = lane_id();
   // X fragments for the MFMA step: 16 columns x 64 k (lane l: column l%16)
@@ -117,7 +117,7 @@ __global__ __launch_bounds__(64) void rstage_kernel(const uint8_t* fixed, const 
     u = stamp();
     acc[4] += u - t;
     t = u;
-    r_decode_staged(T, ex, st, mt, stg, exps, o0, o1);
+    r_decode_staged<true>(T, ex, st, mt, stg, exps, o0, o1);
     keep4(o0);
     keep4(o1);
     u = stamp();
@@ -138,7 +138,7 @@ __global__ __launch_bounds__(64) void rstage_kernel(const uint8_t* fixed, const 
               __builtin_amdgcn_readfirstlane(f1), s2, m2);
       r_stage(stg, s2, m2);
       u32x4 p0, p1;
-      r_decode_staged(T, ex, s2, m2, stg, exps, p0, p1);
+      r_decode_staged<true>(T, ex, s2, m2, stg, exps, p0, p1);
       c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(p0), x0, c, 0, 0, 0);
       c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(p1), x1, c, 0, 0, 0);
       keep(__float_as_uint(c[0]));
