@@ -337,16 +337,21 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
                                                            const int32_t* eoff, int start_exp,
                                                            const uint16_t* X, uint16_t* Y, int M,
                                                            int N, int K, int kb_per_split) {
+  // LDS: the waves' outlier stages first, then the decode table.  (With the
+  // stages at a small base, a window's dword reads fold their offsets into
+  // the instructions; the table reads take the large constant instead.)
   __shared__ __attribute__((aligned(16))) uint8_t smem[RGemmSmem<F, NB, WAVES, D>::kBytes];
-  RTables& T = *reinterpret_cast<RTables*>(smem);
+  constexpr int kTabAt = WAVES * D * F * kExpStage;
+  static_assert(kTabAt % 16 == 0, "table alignment");
+  RTables& T = *reinterpret_cast<RTables*>(smem + kTabAt);
   const RExp ex = r_exp(start_exp);
   build_r_tables_exp(T, threadIdx.x, blockDim.x, ex.lo, ex.hi);
   __syncthreads();
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
-  // stage s of band f: smem + sizeof(RTables) + ((w * D + s) * F + f) * kExpStage
-  uint8_t* stg = smem + sizeof(RTables) + w * D * F * kExpStage;
+  // stage s of band f: smem + ((w * D + s) * F + f) * kExpStage
+  uint8_t* stg = smem + w * D * F * kExpStage;
   const int bands = M >> 4;
   const int band0 = blockIdx.x * F;
   const int split = blockIdx.y;
