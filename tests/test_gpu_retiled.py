@@ -131,12 +131,16 @@ def test_retiled_zipgemm_two_bands_per_wave(torch_cuda, N):
     assert np.abs(y - ref).max() / np.abs(ref).max() <= 1e-2
 
 
-@pytest.mark.parametrize("N,split_k", [(20, 1), (64, 1), (128, 1), (40, 2)])
-def test_retiled_zipgemm_large_grid(torch_cuda, N, split_k):
-    # M / 64 * split_k >= 384 selects the two-phase 64-row kernel
+@pytest.mark.parametrize("N,split_k,M", [(20, 1, 24576), (64, 1, 24576), (128, 1, 24576),
+                                         (40, 2, 24576), (100, 1, 24576), (200, 1, 24576),
+                                         (128, 2, 20480), (128, 1, 24640)])
+def test_retiled_zipgemm_large_grid(torch_cuda, N, split_k, M):
+    # M / 64 * split_k >= 384 selects the two-phase 64-row kernel; N > 64 with
+    # M % 128 == 0 and >= 160 128-row workgroups the two-bands-per-wave one
+    # (M = 24640 is not a multiple of 128: the 64-row kernel)
     torch = torch_cuda
-    rng = np.random.default_rng(N * 3 + split_k)
-    M, K = 24576, 128
+    rng = np.random.default_rng(N * 3 + split_k + M)
+    K = 128
     W = weights_bf16(rng, (M, K), outlier_frac=0.01)
     X = zo.f32_to_bf16(rng.standard_normal((N, K), dtype=np.float32))
     r = zs.compress_retiled(to_torch_bf16(W))

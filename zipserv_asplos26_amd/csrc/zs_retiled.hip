@@ -718,6 +718,192 @@ static hipError_t launch_rgemm(hipStream_t st, const uint8_t* fixed, const uint8
 
 constexpr int kWideDepth = 2;  // records in flight per wave (ring of RD steps)
 
+// ---------------------------------------------------------------------------
+// Wide batches with two bands per wave: as rgemm_wide_kernel, but each wave
+// decodes the records of two bands for the same K tile and feeds every X
+// fragment it reads from LDS to both, halving the LDS bytes per record (the
+// X reads dominate the LDS traffic at N >= 64).  Workgroup = BANDS bands x PH
+// K phases, BANDS/2 waves per phase.
+// ---------------------------------------------------------------------------
+template <int NB, int BANDS, int PH>
+struct RWide2Smem {
+  static constexpr int kWP = BANDS / 2;                  // waves per phase
+  static constexpr int kStageBytes = kWP * PH * 2 * 2 * kExpStage;  // [wave][buf][band]
+  static constexpr int kX = PH * 2 * 16 * NB * kXRow;    // [phase][buffer] tiles
+  static constexpr int kMain = kStageBytes + kX + (int)sizeof(RTables);
+  static constexpr int kRed = (PH - 1) * kWP * 2 * NB * 64 * 16;
+  static constexpr int kBytes = kMain > kRed ? kMain : kRed;
+};
+
+template <int NB, int BANDS, int PH>
+__global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
+    const uint8_t* fixed, const uint8_t* exps, const int32_t* eoff, int start_exp,
+    const uint16_t* X, uint16_t* Y, int M, int N, int K, int kb_per_split) {
+  using S = RWide2Smem<NB, BANDS, PH>;
+  constexpr int WP = S::kWP;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[S::kBytes];
+  RTables& T = *reinterpret_cast<RTables*>(smem + S::kStageBytes + S::kX);
+  const RExp ex = r_exp(start_exp);
+  build_r_tables_exp(T, threadIdx.x, blockDim.x, ex.lo, ex.hi);
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = lane_id();
+  const int q = w % WP, p = w / WP;
+  const int t = threadIdx.x % (WP * 64);  // thread index within the phase
+  // stage (buffer b, band f) of this wave
+  uint8_t* stg = smem + w * 4 * kExpStage;
+  auto stage_of = [&](int b, int f) { return stg + (2 * b + f) * kExpStage; };
+  uint8_t* xbase = smem + S::kStageBytes + p * 2 * 16 * NB * kXRow;
+  uint8_t* xb0 = xbase;
+  uint8_t* xb1 = xbase + 16 * NB * kXRow;
+  const int band0 = blockIdx.x * BANDS + 2 * q;
+  const int split = blockIdx.y;
+  const int n0 = blockIdx.z * NB * 16;
+  const int KT = K >> 6;
+  const int kb0 = split * kb_per_split;
+  const int kb1 = min(kb0 + kb_per_split, KT);
+  const int span = max(kb1 - kb0, 0);
+  const int steps = (span + PH - 1) / PH;         // same for every phase
+  const int cnt = (span - p + PH - 1) / PH;       // valid tiles of this phase
+  auto tile_of = [&](int j) { return min(kb0 + PH * j + p, kb1 - 1); };
+  const int64_t rowrec[2] = {(int64_t)band0 * KT, (int64_t)(band0 + 1) * KT};
+
+  constexpr int kXC = (2 * NB + WP - 1) / WP;  // 16-byte X chunks per thread
+  uint32_t xsrc[kXC];
+  int xdst[kXC];
+#pragma unroll
+  for (int i = 0; i < kXC; ++i) {
+    const int c = t + 64 * WP * i;
+    const int row = min(c >> 3, 16 * NB - 1), cc = c & 7;
+    xsrc[i] = 2u * ((uint32_t)min(n0 + row, N - 1) * (uint32_t)K + 8u * (uint32_t)cc);
+    xdst[i] = c < 128 * NB ? row * kXRow + 16 * cc : -1;
+  }
+  f32x4 acc[2][NB];
+#pragma unroll
+  for (int f = 0; f < 2; ++f)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[f][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int brd = (l & 15) * kXRow + 16 * (l >> 4);
+
+  int oe0[2] = {0, 0}, oe1[2] = {0, 0}, ochunk = -1;
+  auto issue = [&](int j, RStage (&R)[2], RMeta (&Mt)[2]) {
+    const int c = j & ~63;
+    if (c != ochunk) {
+      ochunk = c;
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const int64_t ri = rowrec[f] + tile_of(c + l);
+        oe0[f] = eoff[ri];
+        oe1[f] = eoff[ri + 1];
+      }
+    }
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+      r_issue(fixed, exps, rowrec[f] + tile_of(j), __builtin_amdgcn_readlane(oe0[f], j - c),
+              __builtin_amdgcn_readlane(oe1[f], j - c), R[f], Mt[f]);
+  };
+  auto xload = [&](int j, u32x4 (&XR)[kXC]) {
+    const __amdgpu_buffer_rsrc_t xr = r_buffer(X + (int64_t)tile_of(j) * 64, 0x7FFFFFFFu);
+#pragma unroll
+    for (int i = 0; i < kXC; ++i) XR[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, xsrc[i], 0, 0);
+  };
+  auto xwrite = [&](uint8_t* xb, const u32x4 (&XR)[kXC]) {
+#pragma unroll
+    for (int i = 0; i < kXC; ++i)
+      if (2 * NB >= WP * (i + 1) || xdst[i] >= 0) *reinterpret_cast<u32x4*>(xb + xdst[i]) = XR[i];
+  };
+
+  if (span == 0) {
+    __syncthreads();
+  } else {
+    RStage R0[2], R1[2];
+    RMeta M0[2], M1[2];
+    u32x4 XA[kXC], XB[kXC];
+    issue(0, R0, M0);
+    issue(1, R1, M1);
+    xload(0, XA);
+    xload(1, XB);
+#pragma unroll
+    for (int f = 0; f < 2; ++f) r_stage(stage_of(0, f), R0[f], M0[f]);
+    xwrite(xb0, XA);
+    xload(2, XA);
+    __syncthreads();
+
+#define RW2_STEP(S_, BC, XCUR, RC, MC, RN, MN, XRN, XRC)                                  \
+  {                                                                                     \
+    RStage cs_[2] = {RC[0], RC[1]};                                                     \
+    RMeta cm_[2] = {MC[0], MC[1]};                                                      \
+    _Pragma("unroll") for (int f_ = 0; f_ < 2; ++f_)                                    \
+      r_stage(stage_of((BC) ^ 1, f_), RN[f_], MN[f_]);                                  \
+    issue((S_) + 2, RC, MC);                                                            \
+    if ((S_) < cnt) {                                                                   \
+      u32x4 a0_[2], a1_[2];                                                             \
+      _Pragma("unroll") for (int f_ = 0; f_ < 2; ++f_)                                  \
+        r_decode_staged<true>(T, ex, cs_[f_], cm_[f_], stage_of(BC, f_), exps, a0_[f_], \
+                              a1_[f_]);                                                 \
+      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                            \
+        const uint8_t* bp_ = XCUR + brd + nb_ * 16 * kXRow;                             \
+        const bf16x8 b0_ = *reinterpret_cast<const bf16x8*>(bp_);                       \
+        const bf16x8 b1_ = *reinterpret_cast<const bf16x8*>(bp_ + 64);                  \
+        _Pragma("unroll") for (int f_ = 0; f_ < 2; ++f_) {                              \
+          acc[f_][nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                       \
+              as_bf16x8(a0_[f_]), b0_, acc[f_][nb_], 0, 0, 0);                          \
+          acc[f_][nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                       \
+              as_bf16x8(a1_[f_]), b1_, acc[f_][nb_], 0, 0, 0);                          \
+        }                                                                               \
+      }                                                                                 \
+    }                                                                                   \
+    xwrite((XCUR) == xb0 ? xb1 : xb0, XRN);                                             \
+    xload((S_) + 3, XRC);                                                               \
+    __syncthreads();                                                                    \
+  }
+    for (int s2 = 0; s2 < steps; s2 += 2) {
+      RW2_STEP(s2, 0, xb0, R0, M0, R1, M1, XB, XB);
+      if (s2 + 1 < steps) RW2_STEP(s2 + 1, 1, xb1, R1, M1, R0, M0, XA, XA);
+    }
+#undef RW2_STEP
+  }
+
+  f32x4* red = reinterpret_cast<f32x4*>(smem);
+  if (p > 0) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        red[((((p - 1) * WP + q) * 2 + f) * NB + nb) * 64 + l] = acc[f][nb];
+  }
+  __syncthreads();
+  if (p == 0) {
+    uint16_t* out = Y + (int64_t)split * M * N;
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const int mrow = (band0 + f) * 16 + 4 * (l >> 4);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        f32x4 v = acc[f][nb];
+#pragma unroll
+        for (int pp = 1; pp < PH; ++pp) v += red[((((pp - 1) * WP + q) * 2 + f) * NB + nb) * 64 + l];
+        const int n = n0 + nb * 16 + (l & 15);
+        if (n < N) {
+          const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+          const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
+          *reinterpret_cast<uint2*>(out + (int64_t)n * M + mrow) = make_uint2(lo, hi);
+        }
+      }
+    }
+  }
+}
+
+template <int NB, int BANDS, int PH>
+static hipError_t launch_rwide2(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
+                                const int32_t* eoff, int start_exp, const uint16_t* X,
+                                uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split) {
+  dim3 grid(M / (16 * BANDS), split_k, (N + NB * 16 - 1) / (NB * 16));
+  hipLaunchKernelGGL((rgemm_wide2_kernel<NB, BANDS, PH>), grid, dim3(BANDS / 2 * PH * 64), 0, st,
+                     fixed, exps, eoff, start_exp, X, Y, M, N, K, kb_per_split);
+  return hipGetLastError();
+}
+
 template <int NB, int BANDS, int PH>
 static hipError_t launch_rwide(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
                                const int32_t* eoff, int start_exp, const uint16_t* X,
@@ -867,7 +1053,8 @@ extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t
   const int nb = (N + 15) / 16;
   // N > 16: 64-row workgroups sharing each X tile through LDS; four K phases
   // per workgroup (16 waves) when the grid is small, two when it already
-  // covers the GPU.  N <= 16: workgroups of 8 K phases over one or two bands.
+  // covers the GPU; N > 64 on large grids: 128-row workgroups with two bands
+  // per wave.  N <= 16: workgroups of 8 K phases over one or two bands.
   const int64_t wide_wgs = (int64_t)(M / 64) * split_k;
   if (nb >= 2) {
     const bool ph4 = wide_wgs < 384;
@@ -877,6 +1064,11 @@ extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t
     else if (nb <= 4)
       e = ph4 ? launch_rwide<4, 4, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split)
               : launch_rwide<4, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+    else if (M % 128 == 0 && (int64_t)(M / 128) * split_k * ((N + 127) / 128) >= 160)
+      // two bands per wave halve the LDS reads of X per record; they pay
+      // once the 128-row grid still has >= 160 workgroups (measured)
+      e = launch_rwide2<8, 8, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k,
+                                 kb_per_split);
     else
       e = launch_rwide<8, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
   } else {
