@@ -133,9 +133,10 @@ def test_retiled_zipgemm_two_bands_per_wave(torch_cuda, N):
 
 @pytest.mark.parametrize("N,split_k,M", [(20, 1, 24576), (64, 1, 24576), (128, 1, 24576),
                                          (40, 2, 24576), (100, 1, 24576), (200, 1, 24576),
-                                         (128, 2, 20480), (128, 1, 24640)])
+                                         (128, 2, 20480), (128, 1, 24640), (64, 1, 20480),
+                                         (50, 2, 20480)])
 def test_retiled_zipgemm_large_grid(torch_cuda, N, split_k, M):
-    # M / 64 * split_k >= 384 selects the two-phase 64-row kernel; N > 64 with
+    # M / 64 * split_k >= 384 selects the two-phase 64-row kernel; N > 32 with
     # M % 128 == 0 and >= 160 128-row workgroups the two-bands-per-wave one
     # (M = 24640 is not a multiple of 128: the 64-row kernel)
     torch = torch_cuda

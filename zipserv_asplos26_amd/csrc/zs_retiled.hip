@@ -1053,14 +1053,17 @@ extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t
   const int nb = (N + 15) / 16;
   // N > 16: 64-row workgroups sharing each X tile through LDS; four K phases
   // per workgroup (16 waves) when the grid is small, two when it already
-  // covers the GPU; N > 64 on large grids: 128-row workgroups with two bands
-  // per wave.  N <= 16: workgroups of 8 K phases over one or two bands.
+  // covers the GPU; N > 32 on large grids: 128-row workgroups with two
+  // bands per wave.  N <= 16: workgroups of 8 K phases over one or two bands.
   const int64_t wide_wgs = (int64_t)(M / 64) * split_k;
   if (nb >= 2) {
     const bool ph4 = wide_wgs < 384;
     if (nb <= 2)
       e = ph4 ? launch_rwide<2, 4, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split)
               : launch_rwide<2, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+    else if (nb <= 4 && M % 128 == 0 && (int64_t)(M / 128) * split_k >= 160)
+      e = launch_rwide2<4, 8, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k,
+                                 kb_per_split);
     else if (nb <= 4)
       e = ph4 ? launch_rwide<4, 4, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split)
               : launch_rwide<4, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
