@@ -367,11 +367,15 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
   // X fragments: a buffer resource at the tile's column (wave-uniform) plus
   // this lane's 32-bit byte offset (row n, 8 columns), so the loads need no
   // per-tile VALU address arithmetic (N <= 16 here: offsets far below 2^31).
+  // Lanes of rows n >= N get an offset past the resource's range: they read
+  // zeros without touching memory (at N = 1, 1/16 of the bytes a full
+  // fragment returns), and their output columns are dropped anyway.
   uint32_t xoff[NB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-    xoff[nb] = 2u * ((uint32_t)min(n0 + nb * 16 + (l & 15), N - 1) * (uint32_t)K +
-                     8u * (uint32_t)(l >> 4));
+  for (int nb = 0; nb < NB; ++nb) {
+    const int n = n0 + nb * 16 + (l & 15);
+    xoff[nb] = n < N ? 2u * ((uint32_t)n * (uint32_t)K + 8u * (uint32_t)(l >> 4)) : 0xFFFFFF00u;
+  }
   f32x4 acc[F * NB];
 #pragma unroll
   for (int i = 0; i < F * NB; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
