@@ -189,6 +189,23 @@ def test_retiled_zipgemm_splitk(torch_cuda, split_k, N):
     assert np.abs(y - ref).max() / np.abs(ref).max() <= 1e-2
 
 
+@pytest.mark.parametrize("N", [1, 16, 40, 128])
+def test_retiled_zipgemm_empty_split(torch_cuda, N):
+    """K = 320 (5 tiles) over 4 splits of 2 tiles: the last split has no
+    tiles at all and contributes zeros (every kernel width)."""
+    torch = torch_cuda
+    rng = np.random.default_rng(N + 7)
+    M, K, split_k = 256, 320, 4
+    W = weights_bf16(rng, (M, K), outlier_frac=0.01)
+    X = zo.f32_to_bf16(rng.standard_normal((N, K), dtype=np.float32))
+    r = zs.compress_retiled(to_torch_bf16(W))
+    Y = zs.zipgemm(r, to_torch_bf16(X), split_k=split_k)
+    torch.cuda.synchronize()
+    y = zo.bf16_to_f32(from_torch_bf16(Y))
+    ref = zo.bf16_to_f32(zo.gemm_splitk_bf16(W, X, split_k))
+    assert np.abs(y - ref).max() / np.abs(ref).max() <= 1e-2
+
+
 def test_retiled_unit_vectors_exact(torch_cuda):
     torch = torch_cuda
     rng = np.random.default_rng(9)

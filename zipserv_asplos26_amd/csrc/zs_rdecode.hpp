@@ -87,6 +87,35 @@ __device__ __forceinline__ void build_r_tables_exp(RTables& T, int tid, int nthr
   }
 }
 
+// The same copy in two steps for a workgroup of NT threads: every load of
+// the image first (one 16-byte chunk per NT threads each, all in flight
+// together), then the specialisation and the LDS writes.  A kernel issues
+// its first record loads before r_tab_load so that their latency and the
+// image's overlap.
+template <int NT>
+struct RTabRegs {
+  static_assert(2048 % NT == 0, "table chunks per thread");
+  uint4 v[2048 / NT];
+};
+template <int NT>
+__device__ __forceinline__ void r_tab_load(RTabRegs<NT>& t, int tid) {
+  const uint4* src = reinterpret_cast<const uint4*>(kRTabImage.w);
+#pragma unroll
+  for (int k = 0; k < 2048 / NT; ++k) t.v[k] = src[tid + k * NT];
+}
+template <int NT>
+__device__ __forceinline__ void r_tab_store_exp(RTables& T, const RTabRegs<NT>& t, int tid,
+                                                uint32_t exp_lo, uint32_t exp_hi) {
+  uint4* dst = reinterpret_cast<uint4*>(T.tb);
+#pragma unroll
+  for (int k = 0; k < 2048 / NT; ++k) {
+    uint4 v = t.v[k];
+    v.x = __builtin_amdgcn_perm(exp_hi, exp_lo, v.x);
+    v.z = __builtin_amdgcn_perm(exp_hi, exp_lo, v.z);
+    dst[tid + k * NT] = v;
+  }
+}
+
 // Exponent bytes start_exp + 0..3 and + 4..7 (mod 256).
 struct RExp {
   uint32_t lo, hi;

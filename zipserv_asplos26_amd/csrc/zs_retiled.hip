@@ -345,8 +345,6 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
   static_assert(kTabAt % 16 == 0, "table alignment");
   RTables& T = *reinterpret_cast<RTables*>(smem + kTabAt);
   const RExp ex = r_exp(start_exp);
-  build_r_tables_exp(T, threadIdx.x, blockDim.x, ex.lo, ex.hi);
-  __syncthreads();
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
@@ -360,9 +358,13 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
   const int kb0 = split * kb_per_split;
   const int kb1 = min(kb0 + kb_per_split, KT);
   const int cnt = kb1 - kb0 > w ? (kb1 - kb0 - w + WAVES - 1) / WAVES : 0;
-  int64_t rec0[F];  // record of this wave's tile 0, per band (past the end: last band)
+  // Record of this wave's tile 0 per band (past the end: last band), and the
+  // K tile of its X fragments.  A wave without tiles points both at tile 0
+  // of the band so that its (unused) start-up loads stay in bounds.
+  const int xt0 = cnt > 0 ? kb0 + w : 0;
+  int64_t rec0[F];
 #pragma unroll
-  for (int f = 0; f < F; ++f) rec0[f] = (int64_t)min(band0 + f, bands - 1) * KT + kb0 + w;
+  for (int f = 0; f < F; ++f) rec0[f] = (int64_t)min(band0 + f, bands - 1) * KT + xt0;
 
   // X fragments: a buffer resource at the tile's column (wave-uniform) plus
   // this lane's 32-bit byte offset (row n, 8 columns), so the loads need no
@@ -380,24 +382,25 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
 #pragma unroll
   for (int i = 0; i < F * NB; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int c0 = 0; c0 < cnt; c0 += 64) {
-    const int n = min(cnt - c0, 64);
-    const int last = n - 1;
-    // lane i: outlier offsets of tile c0 + i (clamped to the chunk), per band
-    int oe0[F], oe1[F];
-#pragma unroll
-    for (int f = 0; f < F; ++f) {
-      const int64_t ri = rec0[f] + (int64_t)(c0 + min(l, last)) * WAVES;
-      oe0[f] = eoff[ri];
-      oe1[f] = eoff[ri + 1];
-    }
-    RStage R[D][F];
-    RMeta MT[D][F];
-    bf16x8 xc[2][NB], xn[2][NB];
+  // Tiles go in chunks of up to 64 per wave (lane i holds the outlier
+  // offsets of tile c0 + i, clamped to the chunk, per band).
+  RStage R[D][F];
+  RMeta MT[D][F];
+  bf16x8 xc[2][NB], xn[2][NB];
+  int oe0[F], oe1[F];
+  int c0 = 0;
+#define RZ_OFFSETS()                                                        \
+  {                                                                         \
+    _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_) {                      \
+      const int64_t ri_ = rec0[f_] + (int64_t)(c0 + min(l, last)) * WAVES;  \
+      oe0[f_] = eoff[ri_];                                                  \
+      oe1[f_] = eoff[ri_ + 1];                                              \
+    }                                                                       \
+  }
 #define RZ_LOADX(J, DST)                                                          \
   {                                                                               \
     const __amdgpu_buffer_rsrc_t xr_ =                                            \
-        r_buffer(X + (int64_t)(kb0 + w + (c0 + (J)) * WAVES) * 64, 0x7FFFFFFFu);  \
+        r_buffer(X + (int64_t)(xt0 + (c0 + (J)) * WAVES) * 64, 0x7FFFFFFFu);      \
     _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                        \
       DST[0][nb_] = __builtin_bit_cast(                                           \
           bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr_, xoff[nb_], 0, 0));   \
@@ -412,6 +415,18 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
       r_issue(fixed, exps, rec0[f_] + (int64_t)(c0 + j_) * WAVES,                       \
               __builtin_amdgcn_readlane(oe0[f_], j_), __builtin_amdgcn_readlane(oe1[f_], j_), \
               R[f_], MT[f_]);                                                           \
+  }
+#define RZ_ISSUE_FIXED(J, R)                                                    \
+  {                                                                             \
+    _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_)                            \
+      r_issue_fixed(fixed, rec0[f_] + (int64_t)(c0 + (J)) * WAVES, R[f_]);      \
+  }
+#define RZ_ISSUE_EXPS(J, R, MT)                                                           \
+  {                                                                                       \
+    const int j_ = (J);                                                                   \
+    _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_)                                      \
+      r_issue_exps(exps, __builtin_amdgcn_readlane(oe0[f_], j_),                          \
+                   __builtin_amdgcn_readlane(oe1[f_], j_), R[f_], MT[f_]);                \
   }
 #define RZ_STAGE(S, R, MT)                                                     \
   {                                                                            \
@@ -442,20 +457,49 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
     }                                                                                      \
     RZ_ISSUE(min((J) + D, last), RC, MC);                                                  \
   }
+  // Start-up: chunk 0's outlier offsets, the decode table's image, the first
+  // records' fixed parts and the first X tile go out together; the records'
+  // outlier bytes follow as soon as the offsets are in (loads return in
+  // issue order), and the table is written to LDS after that.
+  // (No branches here: the wait counts the compiler places for the table
+  // writes stay exact.)
+  {
+    const int last = max(min(cnt, 64) - 1, 0);
+    RTabRegs<WAVES * 64> tab;
+    RZ_OFFSETS();
+    r_tab_load<WAVES * 64>(tab, threadIdx.x);
 #pragma unroll
-    for (int k = 0; k < D; ++k) RZ_ISSUE(min(k, last), R[k], MT[k]);
+    for (int k = 0; k < D; ++k) RZ_ISSUE_FIXED(min(k, last), R[k]);
     RZ_LOADX(0, xn);
+#pragma unroll
+    for (int k = 0; k < D; ++k) RZ_ISSUE_EXPS(min(k, last), R[k], MT[k]);
+    r_tab_store_exp<WAVES * 64>(T, tab, threadIdx.x, ex.lo, ex.hi);
+  }
+  __syncthreads();
+
+  for (; c0 < cnt; c0 += 64) {
+    const int n = min(cnt - c0, 64);
+    const int last = n - 1;
+    if (c0 > 0) {
+      RZ_OFFSETS();
+#pragma unroll
+      for (int k = 0; k < D; ++k) RZ_ISSUE(min(k, last), R[k], MT[k]);
+      RZ_LOADX(0, xn);
+    }
     RZ_STAGE(0, R[0], MT[0]);
     for (int j = 0; j < n; j += D) {
 #pragma unroll
       for (int k = 0; k < D; ++k)
         RZ_STEP(j + k, k, (k + 1) % D, R[k], MT[k], R[(k + 1) % D], MT[(k + 1) % D]);
     }
+  }
 #undef RZ_STEP
 #undef RZ_STAGE
+#undef RZ_ISSUE_EXPS
+#undef RZ_ISSUE_FIXED
 #undef RZ_ISSUE
 #undef RZ_LOADX
-  }
+#undef RZ_OFFSETS
 
   // Deterministic tree reduction of the WAVES partial accumulators in LDS.
   __syncthreads();
