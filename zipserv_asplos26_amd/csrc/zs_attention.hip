@@ -137,7 +137,10 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
     build_decode_tables(T, p.k_start, threadIdx.x, blockDim.x);
     build_e1(e1v, p.v_start, threadIdx.x, blockDim.x);
   } else if constexpr (kMode == kModeRetiled) {
-    build_r_tables(RT, threadIdx.x, blockDim.x);
+    constexpr int kNT = (kWpi == 1 ? kAttnWaves : kWpi) * 64;
+    RTabRegs<kNT> tab;
+    r_tab_load<kNT>(tab, threadIdx.x);
+    r_tab_store<kNT>(RT, tab, threadIdx.x);
   }
   const RExp kex = r_exp(p.k_start), vex = r_exp(p.v_start);
   __syncthreads();

@@ -104,6 +104,12 @@ __device__ __forceinline__ void r_tab_load(RTabRegs<NT>& t, int tid) {
   for (int k = 0; k < 2048 / NT; ++k) t.v[k] = src[tid + k * NT];
 }
 template <int NT>
+__device__ __forceinline__ void r_tab_store(RTables& T, const RTabRegs<NT>& t, int tid) {
+  uint4* dst = reinterpret_cast<uint4*>(T.tb);
+#pragma unroll
+  for (int k = 0; k < 2048 / NT; ++k) dst[tid + k * NT] = t.v[k];
+}
+template <int NT>
 __device__ __forceinline__ void r_tab_store_exp(RTables& T, const RTabRegs<NT>& t, int tid,
                                                 uint32_t exp_lo, uint32_t exp_hi) {
   uint4* dst = reinterpret_cast<uint4*>(T.tb);

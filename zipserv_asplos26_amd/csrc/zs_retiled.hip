@@ -296,7 +296,11 @@ __global__ __launch_bounds__(256) void rdecompress_kernel(const uint8_t* fixed,
   __shared__ RTables T;
   __shared__ __attribute__((aligned(16))) uint8_t stg[4][kExpStage];
   const RExp ex = r_exp(start_exp);
-  build_r_tables_exp(T, threadIdx.x, blockDim.x, ex.lo, ex.hi);
+  {
+    RTabRegs<256> tab;
+    r_tab_load<256>(tab, threadIdx.x);
+    r_tab_store_exp<256>(T, tab, threadIdx.x, ex.lo, ex.hi);
+  }
   __syncthreads();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
@@ -566,7 +570,6 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   __shared__ __attribute__((aligned(16))) uint8_t smem[RWideSmem<NB, BANDS, PH>::kBytes];
   RTables& T = *reinterpret_cast<RTables*>(smem);
   const RExp ex = r_exp(start_exp);
-  build_r_tables_exp(T, threadIdx.x, blockDim.x, ex.lo, ex.hi);
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
@@ -588,7 +591,8 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   const int steps = (span + PH - 1) / PH;         // same for every phase
   const int cnt = (span - p + PH - 1) / PH;       // valid tiles of this phase
   // K tile of step j of this phase, clamped into the slice (clamped steps
-  // only repeat an in-bounds load and skip the decode).
+  // only repeat an in-bounds load and skip the decode; an empty slice,
+  // kb0 >= KT, clamps to the last tile of the row).
   auto tile_of = [&](int j) { return min(kb0 + PH * j + p, kb1 - 1); };
   const int64_t rowrec = (int64_t)band * KT;
 
@@ -641,17 +645,33 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
         *reinterpret_cast<u32x4*>(xb + xdst[i]) = XR[i];
   };
 
-  if (span == 0) {  // empty split-K slice (uniform per workgroup)
-    __syncthreads();
-  } else {
   static_assert(RD == 2 || RD == 4, "record ring of 2 or 4 steps");
   RStage R[RD];
   RMeta MT[RD];
   u32x4 XA[kXC], XB[kXC];
+  // Start-up, branch-free (an empty slice runs it on clamped tiles and then
+  // no steps): the first outlier offsets, the decode table's image, the
+  // first records' fixed parts and two X tiles go out together; the outlier
+  // bytes follow as soon as the offsets land, then the table is written.
+  {
+    RTabRegs<BANDS * PH * 64> tab;
+    {
+      const int64_t ri = rowrec + tile_of(l);
+      oe0 = eoff[ri];
+      oe1 = eoff[ri + 1];
+      ochunk = 0;
+    }
+    r_tab_load<BANDS * PH * 64>(tab, threadIdx.x);
 #pragma unroll
-  for (int k = 0; k < RD; ++k) issue(k, R[k], MT[k]);
-  xload(0, XA);
-  xload(1, XB);
+    for (int k = 0; k < RD; ++k) r_issue_fixed(fixed, rowrec + tile_of(k), R[k]);
+    xload(0, XA);
+    xload(1, XB);
+#pragma unroll
+    for (int k = 0; k < RD; ++k)
+      r_issue_exps(exps, __builtin_amdgcn_readlane(oe0, k), __builtin_amdgcn_readlane(oe1, k),
+                   R[k], MT[k]);
+    r_tab_store_exp<BANDS * PH * 64>(T, tab, threadIdx.x, ex.lo, ex.hi);
+  }
   r_stage(stage0, R[0], MT[0]);
   xwrite(xb0, XA);
   xload(2, XA);
@@ -693,7 +713,6 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
     }
   }
 #undef RW_STEP
-  }
 
   // Phases 1..PH-1 hand their sums to phase 0 through LDS (added in phase
   // order, so the result is deterministic); phase 0 writes its band.
@@ -792,7 +811,6 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
   __shared__ __attribute__((aligned(16))) uint8_t smem[S::kBytes];
   RTables& T = *reinterpret_cast<RTables*>(smem + S::kStageBytes + S::kX);
   const RExp ex = r_exp(start_exp);
-  build_r_tables_exp(T, threadIdx.x, blockDim.x, ex.lo, ex.hi);
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
@@ -861,16 +879,40 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
       if (2 * NB >= WP * (i + 1) || xdst[i] >= 0) *reinterpret_cast<u32x4*>(xb + xdst[i]) = XR[i];
   };
 
-  if (span == 0) {
-    __syncthreads();
-  } else {
+  {
     RStage R0[2], R1[2];
     RMeta M0[2], M1[2];
     u32x4 XA[kXC], XB[kXC];
-    issue(0, R0, M0);
-    issue(1, R1, M1);
-    xload(0, XA);
-    xload(1, XB);
+    // Start-up, branch-free (an empty slice, kb0 >= KT, runs it on the
+    // clamped last tile and then no steps): offsets, table image, fixed parts
+    // and two X tiles in flight together; outlier bytes as soon as the
+    // offsets land; then the table is written.
+    {
+      RTabRegs<BANDS / 2 * PH * 64> tab;
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const int64_t ri = rowrec[f] + tile_of(l);
+        oe0[f] = eoff[ri];
+        oe1[f] = eoff[ri + 1];
+      }
+      ochunk = 0;
+      r_tab_load<BANDS / 2 * PH * 64>(tab, threadIdx.x);
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        r_issue_fixed(fixed, rowrec[f] + tile_of(0), R0[f]);
+        r_issue_fixed(fixed, rowrec[f] + tile_of(1), R1[f]);
+      }
+      xload(0, XA);
+      xload(1, XB);
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        r_issue_exps(exps, __builtin_amdgcn_readlane(oe0[f], 0),
+                     __builtin_amdgcn_readlane(oe1[f], 0), R0[f], M0[f]);
+        r_issue_exps(exps, __builtin_amdgcn_readlane(oe0[f], 1),
+                     __builtin_amdgcn_readlane(oe1[f], 1), R1[f], M1[f]);
+      }
+      r_tab_store_exp<BANDS / 2 * PH * 64>(T, tab, threadIdx.x, ex.lo, ex.hi);
+    }
 #pragma unroll
     for (int f = 0; f < 2; ++f) r_stage(stage_of(0, f), R0[f], M0[f]);
     xwrite(xb0, XA);
