@@ -208,6 +208,22 @@ int zs_retiled_decompress(void* stream, const uint8_t* d_fixed, const uint8_t* d
 int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
                   const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B, uint16_t* C, int M,
                   int N, int K, uint16_t* Reduction_Workspace, int Split_K);
+/* zs_retiled_mm with the split-K reduction inside the GEMM kernel (no
+ * counterpart in the reference, whose split-K always runs
+ * SplitK_Reduction, build/L_API.cuh:19-37): every workgroup stores its bf16
+ * partial tile into the workspace as above, and the last one of each output
+ * tile to finish adds the Split_K slices in split order and writes C -- the
+ * same sums and rounding as the two-kernel path, one launch instead of two.
+ * d_counters: zs_retiled_mm_counters(M, N) int32 arrival counters (4-byte
+ * aligned), zero-filled by the caller once, when allocated; every completed
+ * call leaves them zero.  Calls that may overlap in time (other streams)
+ * must not share counters or workspace.  The workspace must be 8-byte
+ * aligned.  With Split_K == 1 the counters are not touched. */
+int64_t zs_retiled_mm_counters(int M, int N);
+int zs_retiled_mm_fused(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
+                        const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B, uint16_t* C,
+                        int M, int N, int K, uint16_t* Reduction_Workspace, int Split_K,
+                        int32_t* d_counters);
 
 /* ---------------------------------------------------------------------- */
 /* Decode attention over a compressed KV cache                              */

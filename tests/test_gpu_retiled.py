@@ -237,3 +237,89 @@ def test_retiled_rejects_bad_args(torch_cuda):
     assert L.zs_retiled_mm(*args(sk=2)) == zs._lib.ZS_E_INVAL    # split-K needs a workspace
     assert L.zs_retiled_mm(*args(sk=3)) == zs._lib.ZS_E_INVAL    # more slices than K tiles
     assert L.zs_retiled_mm(*args(sk=0)) == zs._lib.ZS_E_INVAL
+
+
+# (M, K, N, split_k) -> the kernel zs_retiled_mm picks: narrow F = 1, narrow
+# F = 2, an empty last split, wide 4-phase, wide 2-phase, two-band wide
+# (4 and 8 column blocks), wide 8 column blocks.
+FUSED_CASES = [(1024, 1024, 1, 2), (6144, 512, 16, 4), (256, 320, 8, 4), (512, 2048, 32, 3),
+               (12288, 256, 32, 2), (10240, 256, 64, 2), (10240, 256, 128, 2), (512, 1024, 100, 3)]
+
+
+@pytest.mark.parametrize("M,K,N,split_k", FUSED_CASES)
+def test_retiled_zipgemm_fused_splitk(torch_cuda, M, K, N, split_k):
+    """In-kernel split-K reduction: bit-identical to the two-kernel path on
+    three calls in a row (the counters return to zero), within 1e-2 of the
+    split-K rounding model."""
+    torch = torch_cuda
+    rng = np.random.default_rng(M + K + N + split_k)
+    W = weights_bf16(rng, (M, K), outlier_frac=0.01)
+    X = zo.f32_to_bf16(rng.standard_normal((N, K), dtype=np.float32))
+    r = zs.compress_retiled(to_torch_bf16(W))
+    x = to_torch_bf16(X)
+    y2 = zs.zipgemm(r, x, split_k=split_k, fused=False)
+    cnt = torch.zeros(int(zs.lib().zs_retiled_mm_counters(M, N)), dtype=torch.int32, device="cuda")
+    for _ in range(3):
+        y1 = zs.zipgemm(r, x, split_k=split_k, counters=cnt)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(from_torch_bf16(y1), from_torch_bf16(y2))
+        assert int(cnt.abs().sum()) == 0
+    y = zo.bf16_to_f32(from_torch_bf16(y1))
+    ref = zo.bf16_to_f32(zo.gemm_splitk_bf16(W, X, split_k))
+    assert np.abs(y - ref).max() / np.abs(ref).max() <= 1e-2
+
+
+def test_retiled_zipgemm_fused_default_counters_and_graph(torch_cuda):
+    """The per-stream counter buffer (default path), calls of different
+    shapes sharing it, and a captured graph replayed with eager work between
+    replays: every result equals the two-kernel reduction's."""
+    torch = torch_cuda
+    rng = np.random.default_rng(5)
+    mats = [(zs.compress_retiled(to_torch_bf16(weights_bf16(rng, (M, K), outlier_frac=0.01))), K)
+            for M, K in ((2048, 1024), (512, 512))]
+    xs = [to_torch_bf16(zo.f32_to_bf16(rng.standard_normal((n, K), dtype=np.float32)))
+          for (r, K), n in zip(mats, (24, 3))]
+    refs = [zs.zipgemm(r, x, split_k=4, fused=False) for (r, _), x in zip(mats, xs)]
+    for _ in range(2):
+        for (r, _), x, ref in zip(mats, xs, refs):
+            torch.testing.assert_close(zs.zipgemm(r, x, split_k=4), ref, rtol=0, atol=0)
+    st = torch.cuda.Stream()
+    outs = [torch.empty_like(ref) for ref in refs]
+    with torch.cuda.stream(st):
+        for (r, _), x, o in zip(mats, xs, outs):   # counters for this stream, outside capture
+            zs.zipgemm(r, x, split_k=4, out=o)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            for (r, _), x, o in zip(mats, xs, outs):
+                zs.zipgemm(r, x, split_k=4, out=o)
+    for _ in range(3):
+        for o in outs:
+            o.fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        for o, ref in zip(outs, refs):
+            torch.testing.assert_close(o, ref, rtol=0, atol=0)
+        torch.ones(1 << 20, device="cuda").sum().item()   # eager work between replays
+
+
+def test_retiled_mm_fused_rejects_bad_args(torch_cuda):
+    torch = torch_cuda
+    L = zs.lib()
+    r = zs.compress_retiled(to_torch_bf16(weights_bf16(np.random.default_rng(0), (64, 128))))
+    x = torch.zeros(4, 128, dtype=torch.bfloat16, device="cuda")
+    y = torch.empty(4, 64, dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(2 * 4 * 64 + 8, dtype=torch.bfloat16, device="cuda")
+    cnt = torch.zeros(int(L.zs_retiled_mm_counters(64, 4)) + 1, dtype=torch.int32, device="cuda")
+    args = lambda sk=2, w=ws.data_ptr(), c=cnt.data_ptr(): (  # noqa: E731
+        0, r.fixed.data_ptr(), r.exps.data_ptr(), r.eoff.data_ptr(), r.start_exp, x.data_ptr(),
+        y.data_ptr(), 64, 4, 128, w, sk, c)
+    assert L.zs_retiled_mm_counters(64, 4) == 4 and L.zs_retiled_mm_counters(0, 4) == 0
+    assert L.zs_retiled_mm_fused(*args(c=None)) == zs._lib.ZS_E_INVAL       # no counters
+    assert L.zs_retiled_mm_fused(*args(c=cnt.data_ptr() + 2)) == zs._lib.ZS_E_INVAL
+    assert L.zs_retiled_mm_fused(*args(w=ws.data_ptr() + 4)) == zs._lib.ZS_E_INVAL
+    assert L.zs_retiled_mm_fused(*args(w=None)) == zs._lib.ZS_E_INVAL       # no workspace
+    assert L.zs_retiled_mm_fused(*args(sk=1, c=None, w=None)) == 0          # no split: none needed
+    assert L.zs_retiled_mm_fused(*args()) == 0
+    torch.cuda.synchronize()
+    assert int(cnt.abs().sum()) == 0

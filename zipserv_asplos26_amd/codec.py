@@ -365,6 +365,32 @@ def splitk_workspace(c, n: int, split_k: int):
     return torch.empty(nbytes // 2, dtype=torch.bfloat16, device=c.device)
 
 
+# Arrival counters of the in-kernel split-K reduction, one zero-filled int32
+# buffer per (device, stream): calls on one stream run one after another, so
+# they can share it, and every completed call leaves it zero.
+_SPLITK_COUNTERS = {}
+_MIN_COUNTERS = 1 << 16
+
+
+def splitk_counters(rows: int, n: int, device=None):
+    """The current stream's counter buffer for zs_retiled_mm_fused (at least
+    zs_retiled_mm_counters(rows, n) entries), or None while a graph is being
+    captured and no large enough buffer exists yet (a new one would be
+    allocated inside the graph's memory pool)."""
+    torch = _torch()
+    need = int(lib().zs_retiled_mm_counters(rows, n))
+    dev = torch.device(device) if device is not None else torch.device("cuda",
+                                                                       torch.cuda.current_device())
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    buf = _SPLITK_COUNTERS.get(key)
+    if buf is None or buf.numel() < need:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        buf = torch.zeros(max(need, _MIN_COUNTERS), dtype=torch.int32, device=dev)
+        _SPLITK_COUNTERS[key] = buf
+    return buf
+
+
 # ---------------------------------------------------------------------------
 # CDNA4 re-tiled layout (the library's device layout; see include/zipserv.h)
 # ---------------------------------------------------------------------------
@@ -475,9 +501,15 @@ def decompress_retiled(r: ZipservRetiled, out=None):
     return out
 
 
-def zipgemm(c, x, split_k: int = 1, out=None, workspace=None):
+def zipgemm(c, x, split_k: int = 1, out=None, workspace=None, fused: bool = True,
+            counters=None):
     """Y[N, M] = X[N, K] . W[M, K]^T (build/L_API.cuh:19-37 BF16TripleBitmap_MM_API).
-    `c` is a ZipservCompressed (canonical streams) or a ZipservRetiled."""
+    `c` is a ZipservCompressed (canonical streams) or a ZipservRetiled.
+
+    Split-K over the re-tiled layout adds the partial sums inside the GEMM
+    kernel (zs_retiled_mm_fused) when `fused`, with `counters` or the current
+    stream's buffer from splitk_counters(); same results as the two-kernel
+    reduction, which `fused=False` selects (as do the canonical streams)."""
     torch = _torch()
     _check_cuda(x, "x", torch.bfloat16)
     if x.dim() != 2 or x.shape[1] != c.cols:
@@ -489,6 +521,19 @@ def zipgemm(c, x, split_k: int = 1, out=None, workspace=None):
     if split_k > 1 and workspace is None:
         workspace = splitk_workspace(c, n, split_k)
     if retiled:
+        if split_k > 1 and fused and counters is None:
+            counters = splitk_counters(c.rows, n, x.device)
+        if split_k > 1 and fused and counters is not None:
+            if counters.dtype != torch.int32 or counters.device != x.device or \
+                    counters.numel() < lib().zs_retiled_mm_counters(c.rows, n):
+                raise ValueError("counters must be int32 on x's device with "
+                                 "zs_retiled_mm_counters(M, N) entries")
+            check("zs_retiled_mm_fused",
+                  lib().zs_retiled_mm_fused(_stream(), _dptr(c.fixed), _dptr(c.exps),
+                                            _dptr(c.eoff), c.start_exp & 0xFF, _dptr(x),
+                                            _dptr(out), c.rows, n, c.cols, _dptr(workspace),
+                                            split_k, _dptr(counters)))
+            return out
         check("zs_retiled_mm",
               lib().zs_retiled_mm(_stream(), _dptr(c.fixed), _dptr(c.exps), _dptr(c.eoff),
                                   c.start_exp & 0xFF, _dptr(x), _dptr(out), c.rows, n, c.cols,

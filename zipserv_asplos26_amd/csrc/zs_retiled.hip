@@ -321,6 +321,111 @@ __global__ __launch_bounds__(256) void rdecompress_kernel(const uint8_t* fixed,
 }
 
 // ---------------------------------------------------------------------------
+// In-kernel split-K reduction (zs_retiled_mm_fused).  Each workgroup stores
+// its bf16 partial tile into slice `split` of the workspace with
+// device-coherent stores (sc1: written through past the XCD's L2), waits
+// until they are complete, and counts its arrival in cnt[tile] with an
+// atomic add.  The workgroup that arrives last reads the split_k slices of
+// the tile with device-coherent loads, adds them in split order in fp32 --
+// the order and rounding of rsplitk_reduce_kernel, so the result is the
+// same -- writes C and returns the counter to zero for the next call.  No
+// workgroup waits for another, and no L2-wide writeback or invalidation
+// (an acquire-release count costs both per workgroup: measured 3-4x slower
+// on grids of ~1000 workgroups) is needed, because only these stores and
+// loads carry data between workgroups.
+// ---------------------------------------------------------------------------
+struct SplitFix {
+  uint16_t* C;   // final output [N][M]
+  int32_t* cnt;  // per-tile arrival counters; nullptr: no in-kernel reduction
+  int split_k;
+};
+
+__device__ __forceinline__ bool splitk_arrive(int32_t* c, int split_k) {
+  return __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == split_k - 1;
+}
+
+// Four bf16 of a partial tile; device-coherent when the tile is reduced
+// inside the kernel.
+__device__ __forceinline__ void store4(uint16_t* p, uint32_t lo, uint32_t hi, bool coherent) {
+  if (coherent)
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), (uint64_t)lo | ((uint64_t)hi << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
+}
+
+__device__ __forceinline__ void splitk_reset(int32_t* c) {
+  __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait until this wave's stores are complete (acknowledged at device
+// scope), before the barrier after which one wave counts the arrival.
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+
+__device__ __forceinline__ uint64_t load_agent(const uint16_t* p) {
+  return __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<uint16_t*>(p)),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// End of a split-K GEMM workgroup whose tile is rows [m0, m0 + ROWS) x
+// columns [n0, n0 + COLS) (waves with `wrote` stored their part of it into
+// slice blockIdx.y of ws).  Counts the arrival; the last workgroup of the
+// tile sums its split_k slices with all NT threads, 4 rows of one column
+// per item, every slice of an item loaded before the first add.
+template <int ROWS, int COLS, int NT>
+__device__ __forceinline__ void splitk_finish(const SplitFix& fx, const uint16_t* ws, int M, int N,
+                                              int m0, int n0, bool wrote) {
+  __shared__ int last_arrival;
+  if (wrote) wait_stores();
+  __syncthreads();
+  int32_t* c = fx.cnt + blockIdx.z * gridDim.x + blockIdx.x;
+  if (threadIdx.x == 0) last_arrival = splitk_arrive(c, fx.split_k);
+  __syncthreads();
+  if (!last_arrival) return;
+  constexpr int kQ = ROWS / 4;                     // items per column
+  constexpr int kPer = (kQ * COLS + NT - 1) / NT;  // items per thread
+  constexpr int kBatch = 4;                        // slices in flight per item
+  const int64_t mn = (int64_t)M * N;
+  const int S = fx.split_k;
+  int64_t off[kPer];
+  bool ok[kPer];
+  float a[kPer][4];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int it = threadIdx.x + NT * j;
+    const int n = n0 + it / kQ, m = m0 + 4 * (it % kQ);
+    ok[j] = it < kQ * COLS && n < N && m < M;
+    off[j] = ok[j] ? (int64_t)n * M + m : 0;
+    a[j][0] = a[j][1] = a[j][2] = a[j][3] = 0.f;
+  }
+  for (int k0 = 0; k0 < S; k0 += kBatch) {
+    uint64_t v[kPer][kBatch];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) v[j][k] = load_agent(ws + min(k0 + k, S - 1) * mn + off[j]);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k)
+        if (k0 + k < S) {
+          const uint32_t lo = (uint32_t)v[j][k], hi = (uint32_t)(v[j][k] >> 32);
+          a[j][0] += bf16_bits_to_f32(lo & 0xFFFFu);
+          a[j][1] += bf16_bits_to_f32(lo >> 16);
+          a[j][2] += bf16_bits_to_f32(hi & 0xFFFFu);
+          a[j][3] += bf16_bits_to_f32(hi >> 16);
+        }
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j)
+    if (ok[j])
+      *reinterpret_cast<uint2*>(fx.C + off[j]) =
+          make_uint2(f32_to_bf16_bits(a[j][0]) | (f32_to_bf16_bits(a[j][1]) << 16),
+                     f32_to_bf16_bits(a[j][2]) | (f32_to_bf16_bits(a[j][3]) << 16));
+  if (threadIdx.x == 0) splitk_reset(c);
+}
+
+// ---------------------------------------------------------------------------
 // ZipGEMM over the re-tiled layout, narrow batches.  Workgroup = WAVES waves
 // on F consecutive 16-row bands x one split-K slice x 16*NB columns; wave w
 // takes K tiles kb0+w, kb0+w+WAVES, ... of all F bands, so each X fragment
@@ -340,7 +445,8 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
                                                            const uint8_t* exps,
                                                            const int32_t* eoff, int start_exp,
                                                            const uint16_t* X, uint16_t* Y, int M,
-                                                           int N, int K, int kb_per_split) {
+                                                           int N, int K, int kb_per_split,
+                                                           SplitFix fx) {
   // LDS: the waves' outlier stages first, then the decode table.  (With the
   // stages at a small base, a window's dword reads fold their offsets into
   // the instructions; the table reads take the large constant instead.)
@@ -533,10 +639,12 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
           const int mrow = (band0 + f) * 16 + 4 * (l >> 4);
           const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
           const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
-          *reinterpret_cast<uint2*>(out + (int64_t)n * M + mrow) = make_uint2(lo, hi);
+          store4(out + (int64_t)n * M + mrow, lo, hi, fx.cnt != nullptr);
         }
       }
   }
+  if (fx.cnt)
+    splitk_finish<16 * F, 16 * NB, WAVES * 64>(fx, Y, M, N, band0 * 16, n0, w == 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -566,7 +674,7 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
                                                               const int32_t* eoff, int start_exp,
                                                               const uint16_t* X, uint16_t* Y,
                                                               int M, int N, int K,
-                                                              int kb_per_split) {
+                                                              int kb_per_split, SplitFix fx) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[RWideSmem<NB, BANDS, PH>::kBytes];
   RTables& T = *reinterpret_cast<RTables*>(smem);
   const RExp ex = r_exp(start_exp);
@@ -734,10 +842,13 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
       if (n < N) {
         const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
         const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
-        *reinterpret_cast<uint2*>(out + (int64_t)n * M + mrow) = make_uint2(lo, hi);
+        store4(out + (int64_t)n * M + mrow, lo, hi, fx.cnt != nullptr);
       }
     }
   }
+  if (fx.cnt)
+    splitk_finish<16 * BANDS, 16 * NB, BANDS * PH * 64>(fx, Y, M, N, blockIdx.x * BANDS * 16,
+                                                          n0, p == 0);
 }
 
 __global__ __launch_bounds__(256) void rsplitk_reduce_kernel(uint16_t* C, const uint16_t* WS,
@@ -775,11 +886,12 @@ static int r_grid(int64_t nrec, int waves_per_block) {
 template <int F, int NB>
 static hipError_t launch_rgemm(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
                                const int32_t* eoff, int start_exp, const uint16_t* X,
-                               uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split) {
+                               uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split,
+                               SplitFix fx) {
   constexpr int kWaves = 8, kDepth = 3;
   dim3 grid((M / 16 + F - 1) / F, split_k, (N + NB * 16 - 1) / (NB * 16));
   hipLaunchKernelGGL((rgemm_kernel<F, NB, kWaves, kDepth>), grid, dim3(kWaves * 64), 0, st, fixed, exps,
-                     eoff, start_exp, X, Y, M, N, K, kb_per_split);
+                     eoff, start_exp, X, Y, M, N, K, kb_per_split, fx);
   return hipGetLastError();
 }
 
@@ -805,7 +917,7 @@ struct RWide2Smem {
 template <int NB, int BANDS, int PH>
 __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
     const uint8_t* fixed, const uint8_t* exps, const int32_t* eoff, int start_exp,
-    const uint16_t* X, uint16_t* Y, int M, int N, int K, int kb_per_split) {
+    const uint16_t* X, uint16_t* Y, int M, int N, int K, int kb_per_split, SplitFix fx) {
   using S = RWide2Smem<NB, BANDS, PH>;
   constexpr int WP = S::kWP;
   __shared__ __attribute__((aligned(16))) uint8_t smem[S::kBytes];
@@ -977,30 +1089,35 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
         if (n < N) {
           const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
           const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
-          *reinterpret_cast<uint2*>(out + (int64_t)n * M + mrow) = make_uint2(lo, hi);
+          store4(out + (int64_t)n * M + mrow, lo, hi, fx.cnt != nullptr);
         }
       }
     }
   }
+  if (fx.cnt)
+    splitk_finish<16 * BANDS, 16 * NB, BANDS / 2 * PH * 64>(fx, Y, M, N, blockIdx.x * BANDS * 16,
+                                                              n0, p == 0);
 }
 
 template <int NB, int BANDS, int PH>
 static hipError_t launch_rwide2(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
                                 const int32_t* eoff, int start_exp, const uint16_t* X,
-                                uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split) {
+                                uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split,
+                                SplitFix fx) {
   dim3 grid(M / (16 * BANDS), split_k, (N + NB * 16 - 1) / (NB * 16));
   hipLaunchKernelGGL((rgemm_wide2_kernel<NB, BANDS, PH>), grid, dim3(BANDS / 2 * PH * 64), 0, st,
-                     fixed, exps, eoff, start_exp, X, Y, M, N, K, kb_per_split);
+                     fixed, exps, eoff, start_exp, X, Y, M, N, K, kb_per_split, fx);
   return hipGetLastError();
 }
 
 template <int NB, int BANDS, int PH>
 static hipError_t launch_rwide(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
                                const int32_t* eoff, int start_exp, const uint16_t* X,
-                               uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split) {
+                               uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split,
+                               SplitFix fx) {
   dim3 grid(M / (16 * BANDS), split_k, (N + NB * 16 - 1) / (NB * 16));
   hipLaunchKernelGGL((rgemm_wide_kernel<NB, BANDS, PH, kWideDepth>), grid, dim3(BANDS * PH * 64), 0, st, fixed,
-                     exps, eoff, start_exp, X, Y, M, N, K, kb_per_split);
+                     exps, eoff, start_exp, X, Y, M, N, K, kb_per_split, fx);
   return hipGetLastError();
 }
 
@@ -1112,9 +1229,11 @@ extern "C" int zs_retiled_decompress(void* stream, const uint8_t* d_fixed, const
   return status_of(hipGetLastError());
 }
 
-extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
-                             const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B,
-                             uint16_t* C, int M, int N, int K, uint16_t* ws, int split_k) {
+// Split-K partial sums go to ws; with `counters` the GEMM kernel itself adds
+// them (last workgroup per tile), without it rsplitk_reduce_kernel does.
+static int retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
+                      const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B, uint16_t* C,
+                      int M, int N, int K, uint16_t* ws, int split_k, int32_t* counters) {
   if (!shape_ok(M, K) || N <= 0 || !d_fixed || !d_exps || !d_eoff || !B || !C) return ZS_E_INVAL;
   if ((reinterpret_cast<uintptr_t>(d_fixed) & 15) || (reinterpret_cast<uintptr_t>(d_exps) & 15) ||
       (reinterpret_cast<uintptr_t>(B) & 15) || (K % 8))
@@ -1128,9 +1247,9 @@ extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t
     // and Y that stay below 2^31 bytes, one after another on the stream.
     const int rows = std::max(16, (int)(INT32_MAX / (2LL * K)) / 16 * 16);
     for (int n0 = 0; n0 < N; n0 += rows) {
-      const int st_ = zs_retiled_mm(stream, d_fixed, d_exps, d_eoff, start_exp,
-                                    B + (int64_t)n0 * K, C + (int64_t)n0 * M, M,
-                                    std::min(rows, N - n0), K, ws, split_k);
+      const int st_ = retiled_mm(stream, d_fixed, d_exps, d_eoff, start_exp,
+                                 B + (int64_t)n0 * K, C + (int64_t)n0 * M, M,
+                                 std::min(rows, N - n0), K, ws, split_k, counters);
       if (st_ != ZS_OK) return st_;
     }
     return ZS_OK;
@@ -1140,6 +1259,7 @@ extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t
   hipError_t e;
   const int kb_per_split = (KT - 1) / split_k + 1;
   uint16_t* out = split_k == 1 ? C : ws;
+  const SplitFix fx{C, split_k > 1 ? counters : nullptr, split_k};
   const int nb = (N + 15) / 16;
   // N > 16: 64-row workgroups sharing each X tile through LDS; four K phases
   // per workgroup (16 waves) when the grid is small, two when it already
@@ -1149,32 +1269,32 @@ extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t
   if (nb >= 2) {
     const bool ph4 = wide_wgs < 384;
     if (nb <= 2)
-      e = ph4 ? launch_rwide<2, 4, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split)
-              : launch_rwide<2, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+      e = ph4 ? launch_rwide<2, 4, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx)
+              : launch_rwide<2, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
     else if (nb <= 4 && M % 128 == 0 && (int64_t)(M / 128) * split_k >= 160)
       e = launch_rwide2<4, 8, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k,
-                                 kb_per_split);
+                                 kb_per_split, fx);
     else if (nb <= 4)
-      e = ph4 ? launch_rwide<4, 4, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split)
-              : launch_rwide<4, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+      e = ph4 ? launch_rwide<4, 4, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx)
+              : launch_rwide<4, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
     else if (M % 128 == 0 && (int64_t)(M / 128) * split_k * ((N + 127) / 128) >= 160)
       // two bands per wave halve the LDS reads of X per record; they pay
       // once the 128-row grid still has >= 160 workgroups (measured)
       e = launch_rwide2<8, 8, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k,
-                                 kb_per_split);
+                                 kb_per_split, fx);
     else
-      e = launch_rwide<8, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+      e = launch_rwide<8, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
   } else {
     // Two bands per wave halve the X bytes per record (the cost that grows
     // with N) but also the grid: for N > 8 once the grid keeps at least
     // 192 workgroups.
     if (N > 8 && M / 16 >= 384)
-      e = launch_rgemm<2, 1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+      e = launch_rgemm<2, 1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
     else
-      e = launch_rgemm<1, 1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split);
+      e = launch_rgemm<1, 1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
   }
   if (e != hipSuccess) return (int)e;
-  if (split_k > 1) {
+  if (split_k > 1 && !counters) {
     const int64_t mn = (int64_t)M * N;
     const int64_t threads = (mn + 7) / 8;
     hipLaunchKernelGGL(rsplitk_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256),
@@ -1182,4 +1302,27 @@ extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t
     e = hipGetLastError();
   }
   return status_of(e);
+}
+
+extern "C" int zs_retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
+                             const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B,
+                             uint16_t* C, int M, int N, int K, uint16_t* ws, int split_k) {
+  return retiled_mm(stream, d_fixed, d_exps, d_eoff, start_exp, B, C, M, N, K, ws, split_k,
+                    nullptr);
+}
+
+extern "C" int64_t zs_retiled_mm_counters(int M, int N) {
+  if (M <= 0 || N <= 0) return 0;
+  return (int64_t)((M + 15) / 16) * ((N + 15) / 16);
+}
+
+extern "C" int zs_retiled_mm_fused(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
+                                   const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B,
+                                   uint16_t* C, int M, int N, int K, uint16_t* ws, int split_k,
+                                   int32_t* counters) {
+  if (split_k > 1 && (!counters || (reinterpret_cast<uintptr_t>(counters) & 3) ||
+                      (reinterpret_cast<uintptr_t>(ws) & 7)))
+    return ZS_E_INVAL;
+  return retiled_mm(stream, d_fixed, d_exps, d_eoff, start_exp, B, C, M, N, K, ws, split_k,
+                    counters);
 }
