@@ -1,8 +1,9 @@
 """GPU parity of the CDNA4 re-tiled layout: encoders byte-identical to the
 oracle, decompress bit-exact, and ZipGEMM over the re-tiled layout identical
-(bit for bit, N <= 16) or equal up to fp32 summation order (N > 16, 64-row
-kernel) to ZipGEMM over the canonical streams it was built from, and within
-1e-2 relative error of the fp32-accumulated product."""
+(bit for bit, N <= 16 with 8-wave workgroups) or equal up to fp32 summation
+order (N > 16, and the 4-wave workgroups of N > 1 on >= 640 bands) to
+ZipGEMM over the canonical streams it was built from, and within 1e-2
+relative error of the fp32-accumulated product."""
 import numpy as np
 import pytest
 
@@ -109,14 +110,16 @@ def test_retiled_zipgemm_equals_canonical(torch_cuda, M, K, N):
     assert err <= 1e-2
 
 
+@pytest.mark.parametrize("M", [64 * 100, 64 * 193])
 @pytest.mark.parametrize("N", [1, 9, 16])
-def test_retiled_zipgemm_two_bands_per_wave(torch_cuda, N):
-    # N > 8 with M / 16 >= 384 selects two bands per wave.  Per band the
-    # summation order is unchanged, so the result is bit-identical to the
-    # canonical kernel.
+def test_retiled_zipgemm_two_bands_per_wave(torch_cuda, N, M):
+    # N > 8 with M / 16 >= 384 selects two bands per wave.  With 8 waves per
+    # workgroup the per-band summation order is the canonical kernel's, so
+    # the result is bit-identical; N > 1 on >= 640 bands (M = 12352) runs 4
+    # waves per workgroup, whose fp32 sums differ from it only in rounding.
     torch = torch_cuda
-    rng = np.random.default_rng(501 + N)
-    M, K = 64 * 193, 256
+    rng = np.random.default_rng(501 + N + M)
+    K = 256
     W = weights_bf16(rng, (M, K), outlier_frac=0.01)
     X = zo.f32_to_bf16(rng.standard_normal((N, K), dtype=np.float32))
     c = upload(zo.compress(W))
@@ -125,7 +128,11 @@ def test_retiled_zipgemm_two_bands_per_wave(torch_cuda, N):
     Yc = zs.zipgemm(c, x)
     Yr = zs.zipgemm(r, x)
     torch.cuda.synchronize()
-    np.testing.assert_array_equal(from_torch_bf16(Yr), from_torch_bf16(Yc))
+    if N == 1 or M // 16 < 640:
+        np.testing.assert_array_equal(from_torch_bf16(Yr), from_torch_bf16(Yc))
+    else:
+        a, b = zo.bf16_to_f32(from_torch_bf16(Yr)), zo.bf16_to_f32(from_torch_bf16(Yc))
+        assert np.all(np.abs(a - b) <= 2.0 ** -6 * np.maximum(np.abs(a), np.abs(b)) + 1e-6)
     ref = zo.gemm_f32(W, X)
     y = zo.bf16_to_f32(from_torch_bf16(Yr))
     assert np.abs(y - ref).max() / np.abs(ref).max() <= 1e-2
@@ -240,9 +247,10 @@ def test_retiled_rejects_bad_args(torch_cuda):
 
 
 # (M, K, N, split_k) -> the kernel zs_retiled_mm picks: narrow F = 1, narrow
-# F = 2, an empty last split, wide 4-phase, wide 2-phase, two-band wide
-# (4 and 8 column blocks), wide 8 column blocks.
-FUSED_CASES = [(1024, 1024, 1, 2), (6144, 512, 16, 4), (256, 320, 8, 4), (512, 2048, 32, 3),
+# F = 2, narrow 4-wave F = 1 and F = 2, an empty last split, wide 4-phase,
+# wide 2-phase, two-band wide (4 and 8 column blocks), wide 8 column blocks.
+FUSED_CASES = [(1024, 1024, 1, 2), (6144, 512, 16, 4), (10240, 512, 8, 2), (10240, 256, 12, 3),
+               (256, 320, 8, 4), (512, 2048, 32, 3),
                (12288, 256, 32, 2), (10240, 256, 64, 2), (10240, 256, 128, 2), (512, 1024, 100, 3)]
 
 

@@ -883,12 +883,12 @@ static int r_grid(int64_t nrec, int waves_per_block) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, 256 * 64));
 }
 
-template <int F, int NB>
+template <int F, int NB, int kWaves>
 static hipError_t launch_rgemm(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
                                const int32_t* eoff, int start_exp, const uint16_t* X,
                                uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split,
                                SplitFix fx) {
-  constexpr int kWaves = 8, kDepth = 3;
+  constexpr int kDepth = 3;
   dim3 grid((M / 16 + F - 1) / F, split_k, (N + NB * 16 - 1) / (NB * 16));
   hipLaunchKernelGGL((rgemm_kernel<F, NB, kWaves, kDepth>), grid, dim3(kWaves * 64), 0, st, fixed, exps,
                      eoff, start_exp, X, Y, M, N, K, kb_per_split, fx);
@@ -1287,11 +1287,17 @@ static int retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exp
   } else {
     // Two bands per wave halve the X bytes per record (the cost that grows
     // with N) but also the grid: for N > 8 once the grid keeps at least
-    // 192 workgroups.
+    // 192 workgroups.  Workgroups of 4 waves (16 per CU, twice the K tiles
+    // per wave) instead of 8 for N > 1 on grids of >= 640 bands (measured:
+    // 1-5 us faster at N = 8 / 16 on 10240, 14336 and 28672 rows, slower on
+    // smaller grids and mixed at N = 1).
+    const bool w4 = N > 1 && M / 16 >= 640;
     if (N > 8 && M / 16 >= 384)
-      e = launch_rgemm<2, 1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
+      e = w4 ? launch_rgemm<2, 1, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx)
+             : launch_rgemm<2, 1, 8>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
     else
-      e = launch_rgemm<1, 1>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
+      e = w4 ? launch_rgemm<1, 1, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx)
+             : launch_rgemm<1, 1, 8>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
   }
   if (e != hipSuccess) return (int)e;
   if (split_k > 1 && !counters) {
