@@ -476,17 +476,28 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
 #pragma unroll
   for (int f = 0; f < F; ++f) rec0[f] = (int64_t)min(band0 + f, bands - 1) * KT + xt0;
 
-  // X fragments: a buffer resource at the tile's column (wave-uniform) plus
-  // this lane's 32-bit byte offset (row n, 8 columns), so the loads need no
-  // per-tile VALU address arithmetic (N <= 16 here: offsets far below 2^31).
-  // Lanes of rows n >= N get an offset past the resource's range: they read
-  // zeros without touching memory (at N = 1, 1/16 of the bytes a full
-  // fragment returns), and their output columns are dropped anyway.
+  // Buffer resources built once: the records of each band from this wave's
+  // tile 0 on (tile j at scalar offset j * WAVES * kRecBytes), the whole
+  // outlier stream (bounded by its length + slack; eoff's last entry), and
+  // X (tile t at scalar offset 128 t).  Loads then carry no per-record
+  // descriptor or 64-bit base arithmetic.
+  __amdgpu_buffer_rsrc_t frs[F];
+#pragma unroll
+  for (int f = 0; f < F; ++f) frs[f] = r_buffer(fixed + rec0[f] * kRecBytes, (uint32_t)KT * kRecBytes);
+  const __amdgpu_buffer_rsrc_t ers =
+      r_buffer(exps, (uint32_t)eoff[(int64_t)bands * KT] + (uint32_t)ZS_STREAM_SLACK_BYTES);
+  // X fragments: this lane's 32-bit byte offset (row n, 8 columns; N <= 16
+  // here: offsets far below 2^31).  Lanes of rows n >= N get the offset
+  // 2^31, at or past the resource's range whether or not the scalar offset
+  // counts in the range check: they read zeros without touching memory (at
+  // N = 1, 1/16 of the bytes a full fragment returns), and their output
+  // columns are dropped anyway.
+  const __amdgpu_buffer_rsrc_t xrs = r_buffer(X, 0x80000000u);
   uint32_t xoff[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int n = n0 + nb * 16 + (l & 15);
-    xoff[nb] = n < N ? 2u * ((uint32_t)n * (uint32_t)K + 8u * (uint32_t)(l >> 4)) : 0xFFFFFF00u;
+    xoff[nb] = n < N ? 2u * ((uint32_t)n * (uint32_t)K + 8u * (uint32_t)(l >> 4)) : 0x80000000u;
   }
   f32x4 acc[F * NB];
 #pragma unroll
@@ -507,41 +518,37 @@ __global__ __launch_bounds__(WAVES * 64) void rgemm_kernel(const uint8_t* fixed,
       oe1[f_] = eoff[ri_ + 1];                                              \
     }                                                                       \
   }
-#define RZ_LOADX(J, DST)                                                          \
-  {                                                                               \
-    const __amdgpu_buffer_rsrc_t xr_ =                                            \
-        r_buffer(X + (int64_t)(xt0 + (c0 + (J)) * WAVES) * 64, 0x7FFFFFFFu);      \
-    _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                        \
-      DST[0][nb_] = __builtin_bit_cast(                                           \
-          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr_, xoff[nb_], 0, 0));   \
-      DST[1][nb_] = __builtin_bit_cast(                                           \
-          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr_, xoff[nb_] + 64u, 0, 0)); \
-    }                                                                             \
+#define RZ_LOADX(J, DST)                                                              \
+  {                                                                                   \
+    const uint32_t xs_ = (uint32_t)(xt0 + (c0 + (J)) * WAVES) * 128u;                 \
+    _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                            \
+      DST[0][nb_] = __builtin_bit_cast(                                               \
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[nb_], xs_, 0));     \
+      DST[1][nb_] = __builtin_bit_cast(                                               \
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[nb_] + 64u, xs_, 0)); \
+    }                                                                                 \
   }
-#define RZ_ISSUE(J, R, MT)                                                              \
-  {                                                                                     \
-    const int j_ = (J);                                                                 \
-    _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_)                                    \
-      r_issue(fixed, exps, rec0[f_] + (int64_t)(c0 + j_) * WAVES,                       \
-              __builtin_amdgcn_readlane(oe0[f_], j_), __builtin_amdgcn_readlane(oe1[f_], j_), \
-              R[f_], MT[f_]);                                                           \
-  }
-#define RZ_ISSUE_FIXED(J, R)                                                    \
-  {                                                                             \
-    _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_)                            \
-      r_issue_fixed(fixed, rec0[f_] + (int64_t)(c0 + (J)) * WAVES, R[f_]);      \
-  }
-#define RZ_ISSUE_EXPS(J, R, MT)                                                           \
+#define RZ_ISSUE_FIXED(J, R)                                                              \
   {                                                                                       \
-    const int j_ = (J);                                                                   \
-    _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_)                                      \
-      r_issue_exps(exps, __builtin_amdgcn_readlane(oe0[f_], j_),                          \
-                   __builtin_amdgcn_readlane(oe1[f_], j_), R[f_], MT[f_]);                \
+    const uint32_t fs_ = (uint32_t)((c0 + (J)) * WAVES) * (uint32_t)kRecBytes;            \
+    _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_) r_issue_fixed_r(frs[f_], fs_, R[f_]); \
   }
-#define RZ_STAGE(S, R, MT)                                                     \
-  {                                                                            \
-    _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_)                           \
-      r_stage(stg + ((S) * F + f_) * kExpStage, R[f_], MT[f_]);                \
+#define RZ_ISSUE_EXPS(J, R, MT)                                                    \
+  {                                                                                \
+    const int j_ = (J);                                                            \
+    _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_)                               \
+      r_issue_exps_r(ers, __builtin_amdgcn_readlane(oe0[f_], j_),                  \
+                     __builtin_amdgcn_readlane(oe1[f_], j_), R[f_], MT[f_]);       \
+  }
+#define RZ_ISSUE(J, R, MT) \
+  {                        \
+    RZ_ISSUE_FIXED(J, R);  \
+    RZ_ISSUE_EXPS(J, R, MT); \
+  }
+#define RZ_STAGE(S, R, MT)                                                                \
+  {                                                                                       \
+    _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_)                                      \
+      r_stage_all(stg + ((S) * F + f_) * kExpStage, R[f_]);                               \
   }
 #define RZ_STEP(J, SC, SN, RC, MC, RN, MN)                                                 \
   {                                                                                        \
