@@ -62,6 +62,7 @@ struct AttnParams {
   const uint8_t* vfix;
   const uint8_t* vexp;
   const int32_t* veo;
+  int k_nrec, v_nrec;           // re-tiled records of each cache (bounds start-up loads)
   const uint16_t* kd;           // dense caches [B][cap][Hkv][D] (dense kernel)
   const uint16_t* vd;           //   or pages [blocks][page][Hkv][D] (paged kernel)
   const int32_t* block_table;   // [B][bt_stride] physical page of each logical page
@@ -136,19 +137,21 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
   if constexpr (kMode == kModeCanon) {
     build_decode_tables(T, p.k_start, threadIdx.x, blockDim.x);
     build_e1(e1v, p.v_start, threadIdx.x, blockDim.x);
-  } else if constexpr (kMode == kModeRetiled) {
-    constexpr int kNT = (kWpi == 1 ? kAttnWaves : kWpi) * 64;
-    RTabRegs<kNT> tab;
-    r_tab_load<kNT>(tab, threadIdx.x);
-    r_tab_store<kNT>(RT, tab, threadIdx.x);
   }
+  // (re-tiled: the decode table is copied during the start-up further down)
   const RExp kex = r_exp(p.k_start), vex = r_exp(p.v_start);
-  __syncthreads();
+  if constexpr (kMode != kModeRetiled) __syncthreads();
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
-  const int item = kWpi == 1 ? blockIdx.x * kAttnWaves + w : blockIdx.x;
-  if (item >= p.batch * p.heads_k * p.splits) return;  // uniform when kWpi > 1
+  const int item0 = kWpi == 1 ? blockIdx.x * kAttnWaves + w : blockIdx.x;
+  const int nitems = p.batch * p.heads_k * p.splits;
+  if constexpr (kMode != kModeRetiled) {
+    if (item0 >= nitems) return;  // uniform when kWpi > 1
+  }
+  // (re-tiled: a wave past the last item runs the start-up on the last item,
+  // which every wave of the workgroup must reach, and returns after it)
+  const int item = min(item0, nitems - 1);
   const int sp = item % p.splits;
   const int h = (item / p.splits) % p.heads_k;
   const int b = item / (p.splits * p.heads_k);
@@ -268,6 +271,44 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
     }
   };
 
+  // Re-tiled start-up (branch-free, so the compiler's wait counts stay
+  // exact): the first chunk's outlier offsets and the fixed parts of steps
+  // 0..3 go out with the decode table's image; the outlier bytes follow as
+  // soon as the offsets land, then the table is written and the workgroup
+  // synchronises.  Waves without tokens fetch clamped, in-bounds records.
+  RStage R0, R1, R2, R3;
+  RMeta M0, M1, M2, M3;
+  int oe0 = 0, oe1 = 0;
+  auto rrec = [&](int j) {  // record of step j of the wave's range, clamped
+    const int ty = j & 3, med = j >> 2;
+    const int64_t r = (int64_t)(((ty < 2 ? k_rowbase : v_rowbase) >> 4) + med) * 2 + (ty & 1);
+    return (int64_t)max(min(r, (int64_t)(ty < 2 ? p.k_nrec : p.v_nrec) - 1), (int64_t)0);
+  };
+  if constexpr (kMode == kModeRetiled) {
+    constexpr int kNT = (kWpi == 1 ? kAttnWaves : kWpi) * 64;
+    const int lastc = max(min(4 * nmed, 64) - 1, 3);
+    {
+      const int j = min(l, lastc);
+      const int64_t rec = rrec(j);
+      const int32_t* eo = (j & 3) < 2 ? p.keo : p.veo;
+      oe0 = eo[rec];
+      oe1 = eo[rec + 1];
+    }
+    RTabRegs<kNT> tab;
+    r_tab_load<kNT>(tab, threadIdx.x);
+    r_issue_fixed(p.kfix, rrec(0), R0);
+    r_issue_fixed(p.kfix, rrec(1), R1);
+    r_issue_fixed(p.vfix, rrec(2), R2);
+    r_issue_fixed(p.vfix, rrec(3), R3);
+    r_issue_exps(p.kexp, __builtin_amdgcn_readlane(oe0, 0), __builtin_amdgcn_readlane(oe1, 0), R0, M0);
+    r_issue_exps(p.kexp, __builtin_amdgcn_readlane(oe0, 1), __builtin_amdgcn_readlane(oe1, 1), R1, M1);
+    r_issue_exps(p.vexp, __builtin_amdgcn_readlane(oe0, 2), __builtin_amdgcn_readlane(oe1, 2), R2, M2);
+    r_issue_exps(p.vexp, __builtin_amdgcn_readlane(oe0, 3), __builtin_amdgcn_readlane(oe1, 3), R3, M3);
+    r_tab_store<kNT>(RT, tab, threadIdx.x);
+    __syncthreads();
+    if (item0 >= nitems) return;  // uniform when kWpi > 1
+  }
+
   if (nmed > 0) {
     const int nstep = 4 * nmed;
     const int last = nstep - 1;
@@ -298,8 +339,7 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
       for (int c0 = 0; c0 < nstep; c0 += 64) {
         const int n = min(nstep - c0, 64);
         const int lastc = n - 1;
-        int oe0, oe1;
-        {
+        if (c0 > 0) {
           const int j = c0 + min(l, lastc);
           const int ty = j & 3, med = j >> 2;
           const int64_t rec = (int64_t)(((ty < 2 ? k_rowbase : v_rowbase) >> 4) + med) * 2 + (ty & 1);
@@ -307,8 +347,6 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
           oe0 = eo[rec];
           oe1 = eo[rec + 1];
         }
-        RStage R0, R1, R2, R3;
-        RMeta M0, M1, M2, M3;
 #define ZR_ISSUE(J, I, R, MT)                                                           \
   {                                                                                     \
     const int jj_ = (J);                                                                \
@@ -334,10 +372,12 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
                0, a0_, a1_);                                                            \
     consume((I), (c0 + (J)) >> 2, a0_, a1_);                                            \
   }
-        ZR_ISSUE(0, 0, R0, M0);  // n >= 4: a chunk holds whole medians
-        ZR_ISSUE(1, 1, R1, M1);
-        ZR_ISSUE(2, 2, R2, M2);
-        ZR_ISSUE(3, 3, R3, M3);
+        if (c0 > 0) {  // chunk 0's first steps were issued at start-up
+          ZR_ISSUE(0, 0, R0, M0);  // n >= 4: a chunk holds whole medians
+          ZR_ISSUE(1, 1, R1, M1);
+          ZR_ISSUE(2, 2, R2, M2);
+          ZR_ISSUE(3, 3, R3, M3);
+        }
         r_stage(stage0, R0, M0);
         for (int j = 0; j < n; j += 4) {
           ZR_STEP(j, 0, stage0, stage1, R0, M0, R1, M1);
@@ -775,6 +815,8 @@ extern "C" int zs_decode_attention_retiled(void* stream, const uint16_t* q,
   p.vfix = v->fixed;
   p.vexp = v->exps;
   p.veo = v->eoff;
+  p.k_nrec = k->rows / 16 * (k->cols / 64);
+  p.v_nrec = v->rows / 16 * (v->cols / 64);
   p.k_start = k->start_exp;
   p.v_start = v->start_exp;
   p.k_bsr = k->batch_stride_rows;
