@@ -1253,6 +1253,8 @@ static int retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exp
   const int KT = K / 64;
   if (split_k < 1 || split_k > KT) return ZS_E_INVAL;
   if (split_k > 1 && !ws) return ZS_E_INVAL;
+  // a band's records are addressed with 32-bit scalar offsets
+  if ((int64_t)KT * kRecBytes > (int64_t)UINT32_MAX) return ZS_E_OVERFLOW;
   if ((int64_t)M * N * split_k > INT32_MAX * 2LL) return ZS_E_OVERFLOW;
   if ((int64_t)N * K * 2 > INT32_MAX) {
     // The kernels address X with 32-bit byte offsets: run row blocks of X
