@@ -287,37 +287,102 @@ __global__ __launch_bounds__(256) void remit_canon_kernel(Streams s, int start_e
 }
 
 // ---------------------------------------------------------------------------
-// Decompress: 4 waves per workgroup, one record per wave step (grid-stride).
+// Decompress: a bounded grid of 8-wave workgroups (each copies the decode
+// table once); wave g of G takes records g, g + G, g + 2G, ... (consecutive
+// waves on consecutive records), fetched three ahead into a register ring
+// with their outlier offsets loaded 64 at a time, outlier bytes staged one
+// step ahead, and writes each decoded 16x64 tile as 16 rows of 128 bytes.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void rdecompress_kernel(const uint8_t* fixed,
-                                                          const uint8_t* exps,
-                                                          const int32_t* eoff, int start_exp,
-                                                          uint16_t* out, int M, int K) {
+constexpr int kDecWaves = 8, kDecDepth = 3;
+int device_cu_count();  // zs_gemm.hip
+
+__global__ __launch_bounds__(kDecWaves * 64) void rdecompress_kernel(const uint8_t* fixed,
+                                                                     const uint8_t* exps,
+                                                                     const int32_t* eoff,
+                                                                     int start_exp, uint16_t* out,
+                                                                     int M, int K) {
   __shared__ RTables T;
-  __shared__ __attribute__((aligned(16))) uint8_t stg[4][kExpStage];
+  __shared__ __attribute__((aligned(16))) uint8_t stg[kDecWaves][kDecDepth][kExpStage];
   const RExp ex = r_exp(start_exp);
-  {
-    RTabRegs<256> tab;
-    r_tab_load<256>(tab, threadIdx.x);
-    r_tab_store_exp<256>(T, tab, threadIdx.x, ex.lo, ex.hi);
-  }
-  __syncthreads();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
   const int KT = K >> 6;
   const int64_t nrec = (int64_t)(M >> 4) * KT;
-  for (int64_t rec = (int64_t)blockIdx.x * 4 + w; rec < nrec; rec += (int64_t)gridDim.x * 4) {
-    RStage s;
-    RMeta mt;
-    r_issue(fixed, exps, rec, eoff[rec], eoff[rec + 1], s, mt);
-    r_stage(stg[w], s, mt);
-    u32x4 o0, o1;
-    r_decode_staged<true>(T, ex, s, mt, stg[w], exps, o0, o1);
-    const int64_t band = rec / KT, kt = rec % KT;
-    uint16_t* dst = out + (band * 16 + (l & 15)) * (int64_t)K + kt * 64 + 8 * (l >> 4);
-    *reinterpret_cast<u32x4*>(dst) = o0;
-    *reinterpret_cast<u32x4*>(dst + 32) = o1;
+  const int64_t G = (int64_t)gridDim.x * kDecWaves;
+  const int64_t g = (int64_t)blockIdx.x * kDecWaves + w;
+  const int64_t cnt64 = g < nrec ? (nrec - g + G - 1) / G : 0;
+  const int cnt = (int)cnt64;  // records of this wave (the host keeps it < 2^31)
+  const __amdgpu_buffer_rsrc_t ers =
+      r_buffer(exps, (uint32_t)eoff[nrec] + (uint32_t)ZS_STREAM_SLACK_BYTES);
+  // record j of this wave; waves without records read record 0 (in bounds)
+  auto rec_of = [&](int j) { return cnt > 0 ? g + (int64_t)j * G : (int64_t)0; };
+
+  RStage R[kDecDepth];
+  RMeta MT[kDecDepth];
+  int oe0 = 0, oe1 = 0;
+  int c0 = 0;
+#define RD_OFFSETS(LAST)                                 \
+  {                                                      \
+    const int64_t ri_ = rec_of(c0 + min(l, (LAST)));     \
+    oe0 = eoff[ri_];                                     \
+    oe1 = eoff[ri_ + 1];                                 \
   }
+#define RD_FIXED(J, RR) r_issue_fixed(fixed, rec_of(c0 + (J)), RR)
+#define RD_EXPS(J, RR, MM)                                                        \
+  r_issue_exps_r(ers, __builtin_amdgcn_readlane(oe0, (J)),                       \
+                 __builtin_amdgcn_readlane(oe1, (J)), RR, MM)
+  // Start-up (branch-free): offsets, table image and the first records'
+  // fixed parts together; outlier bytes once the offsets land; then the
+  // table is written.
+  {
+    const int last = max(min(cnt, 64) - 1, 0);
+    RTabRegs<kDecWaves * 64> tab;
+    RD_OFFSETS(last);
+    r_tab_load<kDecWaves * 64>(tab, threadIdx.x);
+#pragma unroll
+    for (int k = 0; k < kDecDepth; ++k) RD_FIXED(min(k, last), R[k]);
+#pragma unroll
+    for (int k = 0; k < kDecDepth; ++k) RD_EXPS(min(k, last), R[k], MT[k]);
+    r_tab_store_exp<kDecWaves * 64>(T, tab, threadIdx.x, ex.lo, ex.hi);
+  }
+  __syncthreads();
+
+  for (; c0 < cnt; c0 += 64) {
+    const int n = min(cnt - c0, 64);
+    const int last = n - 1;
+    if (c0 > 0) {
+      RD_OFFSETS(last);
+#pragma unroll
+      for (int k = 0; k < kDecDepth; ++k) {
+        RD_FIXED(min(k, last), R[k]);
+        RD_EXPS(min(k, last), R[k], MT[k]);
+      }
+    }
+    r_stage_all(stg[w][0], R[0]);
+    for (int j = 0; j < n; j += kDecDepth) {
+#pragma unroll
+      for (int k = 0; k < kDecDepth; ++k) {
+        const int jj = j + k;
+        const int kn = (k + 1) % kDecDepth;
+        r_stage_all(stg[w][kn], R[kn]);
+        if (jj < n) {
+          u32x4 o0, o1;
+          r_decode_staged<true>(T, ex, R[k], MT[k], stg[w][k], exps, o0, o1);
+          const int64_t rec = rec_of(c0 + jj);
+          const int64_t band = rec / KT, kt = rec - band * KT;
+          uint16_t* dst = out + (band * 16 + (l & 15)) * (int64_t)K + kt * 64 + 8 * (l >> 4);
+          *reinterpret_cast<u32x4*>(dst) = o0;
+          *reinterpret_cast<u32x4*>(dst + 32) = o1;
+        }
+        const int jn = min(jj + kDecDepth, last);
+        RD_FIXED(jn, R[k]);
+        RD_EXPS(jn, R[k], MT[k]);
+      }
+    }
+  }
+#undef RD_EXPS
+#undef RD_FIXED
+#undef RD_OFFSETS
 }
 
 // ---------------------------------------------------------------------------
@@ -1236,7 +1301,10 @@ extern "C" int zs_retiled_decompress(void* stream, const uint8_t* d_fixed, const
   if ((reinterpret_cast<uintptr_t>(d_fixed) & 15) || (reinterpret_cast<uintptr_t>(d_exps) & 15))
     return ZS_E_INVAL;
   const int64_t nrec = (int64_t)(M / 16) * (K / 64);
-  hipLaunchKernelGGL(rdecompress_kernel, dim3(r_grid(nrec, 4)), dim3(256), 0,
+  // four workgroups (32 waves) per CU, each wave decoding every G-th record
+  const int grid = (int)std::max<int64_t>(1, std::min<int64_t>((nrec + kDecWaves - 1) / kDecWaves,
+                                                               (int64_t)device_cu_count() * 4));
+  hipLaunchKernelGGL(rdecompress_kernel, dim3(grid), dim3(kDecWaves * 64), 0,
                      (hipStream_t)stream, d_fixed, d_exps, d_eoff, (int)start_exp, out, M, K);
   return status_of(hipGetLastError());
 }
