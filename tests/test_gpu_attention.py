@@ -80,7 +80,10 @@ def test_attention_matches_oracle(torch_cuda, B, T, Hkv, H, splits):
 
 @pytest.mark.parametrize("B,T,Hkv,H,splits", [
     (1, 64, 8, 64, 1), (2, 100, 8, 64, 0), (2, 1000, 8, 64, 3), (1, 4096, 8, 64, 0),
-    (2, 700, 2, 32, 5), (2, 300, 4, 4, 2), (3, 257, 1, 8, 64)])
+    (2, 700, 2, 32, 5), (2, 300, 4, 4, 2), (3, 257, 1, 8, 64),
+    # 2065 items: one wave per item, the last workgroup holds one item and
+    # three idle waves; 128-token splits past T leave the last waves empty
+    (7, 3840, 5, 10, 59)])
 def test_attention_retiled_matches_oracle(torch_cuda, B, T, Hkv, H, splits):
     # same decoded K/V and arithmetic as the canonical path: identical to dense
     _check(_run(torch_cuda, B, T, Hkv, H, splits=splits, retiled=True))
