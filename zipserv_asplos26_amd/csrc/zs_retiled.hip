@@ -501,7 +501,7 @@ __device__ __forceinline__ void splitk_finish(const SplitFix& fx, const uint16_t
 template <int F, int NB, int WAVES, int D>
 struct RGemmSmem {
   static constexpr int kMain = (int)sizeof(RTables) + WAVES * D * F * kExpStage;
-  static constexpr int kRed = (WAVES / 2) * F * NB * 64 * 16;
+  static constexpr int kRed = (WAVES - 1) * F * NB * 64 * 16;
   static constexpr int kBytes = kMain > kRed ? kMain : kRed;
 };
 
@@ -685,21 +685,31 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
 #undef RZ_LOADX
 #undef RZ_OFFSETS
 
-  // Deterministic tree reduction of the WAVES partial accumulators in LDS.
+  // Deterministic reduction of the WAVES partial accumulators: waves 1.. hand
+  // theirs to wave 0 through LDS (after the decode, whose table and stages
+  // the LDS held), which adds them pairwise -- a[w] += a[w + h] for
+  // h = WAVES/2, ..., 1, the canonical kernel's tree order -- so the other
+  // waves are done after one exchange.
   __syncthreads();
   f32x4* red = reinterpret_cast<f32x4*>(smem);
+  if (w > 0) {
 #pragma unroll
-  for (int half = WAVES / 2; half >= 1; half /= 2) {
-    if (w >= half && w < 2 * half) {
+    for (int i = 0; i < F * NB; ++i) red[((w - 1) * F * NB + i) * 64 + l] = acc[i];
+  }
+  __syncthreads();
+  if (w == 0) {
 #pragma unroll
-      for (int i = 0; i < F * NB; ++i) red[((w - half) * F * NB + i) * 64 + l] = acc[i];
+    for (int i = 0; i < F * NB; ++i) {
+      f32x4 a[WAVES];
+      a[0] = acc[i];
+#pragma unroll
+      for (int v = 1; v < WAVES; ++v) a[v] = red[((v - 1) * F * NB + i) * 64 + l];
+#pragma unroll
+      for (int h = WAVES / 2; h >= 1; h /= 2)
+#pragma unroll
+        for (int v = 0; v < h; ++v) a[v] += a[v + h];
+      acc[i] = a[0];
     }
-    __syncthreads();
-    if (w < half) {
-#pragma unroll
-      for (int i = 0; i < F * NB; ++i) acc[i] += red[(w * F * NB + i) * 64 + l];
-    }
-    __syncthreads();
   }
   if (w == 0) {
     uint16_t* out = Y + (int64_t)split * M * N;
