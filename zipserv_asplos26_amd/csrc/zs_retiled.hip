@@ -787,11 +787,18 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   // kb0 >= KT, clamps to the last tile of the row).
   auto tile_of = [&](int j) { return min(kb0 + PH * j + p, kb1 - 1); };
   const int64_t rowrec = (int64_t)band * KT;
+  // Buffer resources built once (the band's records, the outlier stream, X);
+  // per-record and per-tile positions go into the load offsets.
+  const __amdgpu_buffer_rsrc_t frs = r_buffer(fixed + rowrec * kRecBytes, (uint32_t)KT * kRecBytes);
+  const __amdgpu_buffer_rsrc_t ers =
+      r_buffer(exps, (uint32_t)eoff[(int64_t)(M >> 4) * KT] + (uint32_t)ZS_STREAM_SLACK_BYTES);
+  const __amdgpu_buffer_rsrc_t xrs = r_buffer(X, 0x80000000u);
 
   // X tile loads of this thread: chunk c = t + 64*BANDS*i, row c/8, 16-byte
   // column c%8 (128*NB chunks per tile; threads past them load and drop).
-  // Sources are 32-bit byte offsets from a buffer resource at the tile's
-  // column (the host keeps N * K * 2 below 2^31).
+  // Sources are 32-bit byte offsets into X (rows clamped to N - 1), the
+  // tile's column goes into the scalar offset (the host keeps N * K * 2
+  // below 2^31).
   constexpr int kXC = (2 * NB + BANDS - 1) / BANDS;  // chunks per thread
   uint32_t xsrc[kXC];
   int xdst[kXC];
@@ -823,12 +830,13 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   auto issue = [&](int j, RStage& R, RMeta& Mt) {
     int e0, e1;
     offs(j, e0, e1);
-    r_issue(fixed, exps, rowrec + tile_of(j), e0, e1, R, Mt);
+    r_issue_fixed_r(frs, (uint32_t)tile_of(j) * kRecBytes, R);
+    r_issue_exps_r(ers, e0, e1, R, Mt);
   };
   auto xload = [&](int j, u32x4 (&XR)[kXC]) {
-    const __amdgpu_buffer_rsrc_t xr = r_buffer(X + (int64_t)tile_of(j) * 64, 0x7FFFFFFFu);
+    const uint32_t xs = (uint32_t)tile_of(j) * 128u;
 #pragma unroll
-    for (int i = 0; i < kXC; ++i) XR[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, xsrc[i], 0, 0);
+    for (int i = 0; i < kXC; ++i) XR[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xsrc[i], xs, 0);
   };
   auto xwrite = [&](uint8_t* xb, const u32x4 (&XR)[kXC]) {
 #pragma unroll
@@ -855,16 +863,16 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
     }
     r_tab_load<BANDS * PH * 64>(tab, threadIdx.x);
 #pragma unroll
-    for (int k = 0; k < RD; ++k) r_issue_fixed(fixed, rowrec + tile_of(k), R[k]);
+    for (int k = 0; k < RD; ++k) r_issue_fixed_r(frs, (uint32_t)tile_of(k) * kRecBytes, R[k]);
     xload(0, XA);
     xload(1, XB);
 #pragma unroll
     for (int k = 0; k < RD; ++k)
-      r_issue_exps(exps, __builtin_amdgcn_readlane(oe0, k), __builtin_amdgcn_readlane(oe1, k),
+      r_issue_exps_r(ers, __builtin_amdgcn_readlane(oe0, k), __builtin_amdgcn_readlane(oe1, k),
                    R[k], MT[k]);
     r_tab_store_exp<BANDS * PH * 64>(T, tab, threadIdx.x, ex.lo, ex.hi);
   }
-  r_stage(stage0, R[0], MT[0]);
+  r_stage_all(stage0, R[0]);
   xwrite(xb0, XA);
   xload(2, XA);
   __syncthreads();  // decode tables and X tile 0 visible
@@ -873,7 +881,7 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   {                                                                                  \
     const RStage cs_ = RC;                                                           \
     const RMeta cm_ = MC;                                                            \
-    r_stage(NXT, RN, MN);                                                            \
+    r_stage_all(NXT, RN);                                                            \
     issue((S) + RD, RC, MC);                                                         \
     if ((S) < cnt) {                                                                 \
       u32x4 a0_, a1_;                                                                \
@@ -1032,6 +1040,13 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
   const int cnt = (span - p + PH - 1) / PH;       // valid tiles of this phase
   auto tile_of = [&](int j) { return min(kb0 + PH * j + p, kb1 - 1); };
   const int64_t rowrec[2] = {(int64_t)band0 * KT, (int64_t)(band0 + 1) * KT};
+  // Buffer resources built once (each band's records, the outlier stream, X).
+  const __amdgpu_buffer_rsrc_t frs[2] = {
+      r_buffer(fixed + rowrec[0] * kRecBytes, (uint32_t)KT * kRecBytes),
+      r_buffer(fixed + rowrec[1] * kRecBytes, (uint32_t)KT * kRecBytes)};
+  const __amdgpu_buffer_rsrc_t ers =
+      r_buffer(exps, (uint32_t)eoff[(int64_t)(M >> 4) * KT] + (uint32_t)ZS_STREAM_SLACK_BYTES);
+  const __amdgpu_buffer_rsrc_t xrs = r_buffer(X, 0x80000000u);
 
   constexpr int kXC = (2 * NB + WP - 1) / WP;  // 16-byte X chunks per thread
   uint32_t xsrc[kXC];
@@ -1063,14 +1078,16 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
       }
     }
 #pragma unroll
-    for (int f = 0; f < 2; ++f)
-      r_issue(fixed, exps, rowrec[f] + tile_of(j), __builtin_amdgcn_readlane(oe0[f], j - c),
-              __builtin_amdgcn_readlane(oe1[f], j - c), R[f], Mt[f]);
+    for (int f = 0; f < 2; ++f) {
+      r_issue_fixed_r(frs[f], (uint32_t)tile_of(j) * kRecBytes, R[f]);
+      r_issue_exps_r(ers, __builtin_amdgcn_readlane(oe0[f], j - c),
+                     __builtin_amdgcn_readlane(oe1[f], j - c), R[f], Mt[f]);
+    }
   };
   auto xload = [&](int j, u32x4 (&XR)[kXC]) {
-    const __amdgpu_buffer_rsrc_t xr = r_buffer(X + (int64_t)tile_of(j) * 64, 0x7FFFFFFFu);
+    const uint32_t xs = (uint32_t)tile_of(j) * 128u;
 #pragma unroll
-    for (int i = 0; i < kXC; ++i) XR[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, xsrc[i], 0, 0);
+    for (int i = 0; i < kXC; ++i) XR[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xsrc[i], xs, 0);
   };
   auto xwrite = [&](uint8_t* xb, const u32x4 (&XR)[kXC]) {
 #pragma unroll
@@ -1098,22 +1115,22 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
       r_tab_load<BANDS / 2 * PH * 64>(tab, threadIdx.x);
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
-        r_issue_fixed(fixed, rowrec[f] + tile_of(0), R0[f]);
-        r_issue_fixed(fixed, rowrec[f] + tile_of(1), R1[f]);
+        r_issue_fixed_r(frs[f], (uint32_t)tile_of(0) * kRecBytes, R0[f]);
+        r_issue_fixed_r(frs[f], (uint32_t)tile_of(1) * kRecBytes, R1[f]);
       }
       xload(0, XA);
       xload(1, XB);
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
-        r_issue_exps(exps, __builtin_amdgcn_readlane(oe0[f], 0),
+        r_issue_exps_r(ers, __builtin_amdgcn_readlane(oe0[f], 0),
                      __builtin_amdgcn_readlane(oe1[f], 0), R0[f], M0[f]);
-        r_issue_exps(exps, __builtin_amdgcn_readlane(oe0[f], 1),
+        r_issue_exps_r(ers, __builtin_amdgcn_readlane(oe0[f], 1),
                      __builtin_amdgcn_readlane(oe1[f], 1), R1[f], M1[f]);
       }
       r_tab_store_exp<BANDS / 2 * PH * 64>(T, tab, threadIdx.x, ex.lo, ex.hi);
     }
 #pragma unroll
-    for (int f = 0; f < 2; ++f) r_stage(stage_of(0, f), R0[f], M0[f]);
+    for (int f = 0; f < 2; ++f) r_stage_all(stage_of(0, f), R0[f]);
     xwrite(xb0, XA);
     xload(2, XA);
     __syncthreads();
@@ -1123,7 +1140,7 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
     RStage cs_[2] = {RC[0], RC[1]};                                                     \
     RMeta cm_[2] = {MC[0], MC[1]};                                                      \
     _Pragma("unroll") for (int f_ = 0; f_ < 2; ++f_)                                    \
-      r_stage(stage_of((BC) ^ 1, f_), RN[f_], MN[f_]);                                  \
+      r_stage_all(stage_of((BC) ^ 1, f_), RN[f_]);                                      \
     issue((S_) + 2, RC, MC);                                                            \
     if ((S_) < cnt) {                                                                   \
       u32x4 a0_[2], a1_[2];                                                             \
