@@ -336,17 +336,13 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
       // Records fetched four steps ahead into registers; outlier bytes staged
       // one step ahead.  Steps K0,K1,V0,V1 of median `med` are the records
       // of its band in K (column tiles 0, 1), then in V.  Buffer resources
-      // from this wave's first K / V record and over the outlier streams are
-      // built once; a step's record goes into the scalar offset.
+      // from this wave's first K / V record are built once; a step's record
+      // goes into the scalar offset.
       const int64_t kr0 = (int64_t)(k_rowbase >> 4) * 2, vr0 = (int64_t)(v_rowbase >> 4) * 2;
       const __amdgpu_buffer_rsrc_t kfr =
           r_buffer(p.kfix + kr0 * kRecBytes, (uint32_t)((p.k_nrec - kr0) * kRecBytes));
       const __amdgpu_buffer_rsrc_t vfr =
           r_buffer(p.vfix + vr0 * kRecBytes, (uint32_t)((p.v_nrec - vr0) * kRecBytes));
-      const __amdgpu_buffer_rsrc_t ker =
-          r_buffer(p.kexp, (uint32_t)p.keo[p.k_nrec] + (uint32_t)ZS_STREAM_SLACK_BYTES);
-      const __amdgpu_buffer_rsrc_t ver =
-          r_buffer(p.vexp, (uint32_t)p.veo[p.v_nrec] + (uint32_t)ZS_STREAM_SLACK_BYTES);
       for (int c0 = 0; c0 < nstep; c0 += 64) {
         const int n = min(nstep - c0, 64);
         const int lastc = n - 1;
@@ -363,8 +359,8 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
     const int jj_ = (J);                                                                \
     const int med_ = (c0 + jj_) >> 2;                                                   \
     r_issue_fixed_r((I) < 2 ? kfr : vfr, (uint32_t)(med_ * 2 + ((I) & 1)) * kRecBytes, R); \
-    r_issue_exps_r((I) < 2 ? ker : ver, __builtin_amdgcn_readlane(oe0, jj_),            \
-                   __builtin_amdgcn_readlane(oe1, jj_), R, MT);                         \
+    r_issue_exps((I) < 2 ? p.kexp : p.vexp, __builtin_amdgcn_readlane(oe0, jj_),       \
+                 __builtin_amdgcn_readlane(oe1, jj_), R, MT);                           \
   }
 #define ZR_CLAMP(J, I) ((J) <= lastc ? (J) : ((lastc & ~3) | (I)))
 #define ZR_STEP(J, I, CUR, NXT, RC, MC, RN, MN)                                         \

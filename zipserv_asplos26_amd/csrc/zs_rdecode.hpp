@@ -276,30 +276,20 @@ __device__ __forceinline__ void r_issue(const uint8_t* fixed, const uint8_t* exp
   r_issue_exps(exps, e0, e1, s, mt);
 }
 
-// The same fetches through buffer resources built once per kernel (or per
-// band) instead of per record, so a record costs no 64-bit base arithmetic
-// and no descriptor set-up in the scalar unit.  `fixed_r` starts at some
-// record r0 and the scalar offset `soff` is (record - r0) * kRecBytes (every
-// byte addressed belongs to the record).  `exps_r` spans the whole outlier
-// stream, bounded by its length plus the slack; the record's first dword
-// goes into the lane offset, which the range check always covers, so lanes
-// past the record read neighbouring bytes or zeros, never past the
-// allocation.
+// The fixed part through a buffer resource built once per band instead of
+// per record, so a record costs no 64-bit base arithmetic and no descriptor
+// set-up in the scalar unit: `fixed_r` starts at some record r0 and the
+// scalar offset `soff` is (record - r0) * kRecBytes (every byte addressed
+// belongs to the record).  The outlier bytes keep a per-record resource
+// (r_issue_exps): bounded to the record, lanes past it touch no memory --
+// a resource over the whole stream, whose lanes read neighbouring bytes,
+// measured 1-10% slower.
 __device__ __forceinline__ void r_issue_fixed_r(__amdgpu_buffer_rsrc_t fixed_r, uint32_t soff,
                                                 RStage& s) {
   const uint32_t l = (uint32_t)lane_id();
   s.r.sm = __builtin_amdgcn_raw_buffer_load_b128(fixed_r, 16u * l, soff, 0);
   s.r.p32 = __builtin_amdgcn_raw_buffer_load_b32(fixed_r, kRecP32 + 4u * l, soff, 0);
   s.r.p16 = __builtin_amdgcn_raw_buffer_load_b16(fixed_r, kRecP16 + 2u * l, soff, 0);
-}
-__device__ __forceinline__ void r_issue_exps_r(__amdgpu_buffer_rsrc_t exps_r, int e0, int e1,
-                                               RStage& s, RMeta& mt) {
-  const uint32_t l = (uint32_t)lane_id();
-  const int ea0 = e0 & ~3;
-  mt.e0 = e0;
-  mt.rel = e0 - ea0;
-  mt.nw = (e1 - ea0 + 3) >> 2;
-  s.ex = __builtin_amdgcn_raw_buffer_load_b32(exps_r, 4u * l + (uint32_t)ea0, 0, 0);
 }
 
 // Stages all 64 dwords of a record's outlier fetch (the stage has room for

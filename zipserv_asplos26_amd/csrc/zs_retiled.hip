@@ -312,8 +312,6 @@ __global__ __launch_bounds__(kDecWaves * 64) void rdecompress_kernel(const uint8
   const int64_t g = (int64_t)blockIdx.x * kDecWaves + w;
   const int64_t cnt64 = g < nrec ? (nrec - g + G - 1) / G : 0;
   const int cnt = (int)cnt64;  // records of this wave (the host keeps it < 2^31)
-  const __amdgpu_buffer_rsrc_t ers =
-      r_buffer(exps, (uint32_t)eoff[nrec] + (uint32_t)ZS_STREAM_SLACK_BYTES);
   // record j of this wave; waves without records read record 0 (in bounds)
   auto rec_of = [&](int j) { return cnt > 0 ? g + (int64_t)j * G : (int64_t)0; };
 
@@ -329,7 +327,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void rdecompress_kernel(const uint8
   }
 #define RD_FIXED(J, RR) r_issue_fixed(fixed, rec_of(c0 + (J)), RR)
 #define RD_EXPS(J, RR, MM)                                                        \
-  r_issue_exps_r(ers, __builtin_amdgcn_readlane(oe0, (J)),                       \
+  r_issue_exps(exps, __builtin_amdgcn_readlane(oe0, (J)),                       \
                  __builtin_amdgcn_readlane(oe1, (J)), RR, MM)
   // Start-up (branch-free): offsets, table image and the first records'
   // fixed parts together; outlier bytes once the offsets land; then the
@@ -544,15 +542,12 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
   for (int f = 0; f < F; ++f) rec0[f] = (int64_t)min(band0 + f, bands - 1) * KT + xt0;
 
   // Buffer resources built once: the records of each band from this wave's
-  // tile 0 on (tile j at scalar offset j * WAVES * kRecBytes), the whole
-  // outlier stream (bounded by its length + slack; eoff's last entry), and
-  // X (tile t at scalar offset 128 t).  Loads then carry no per-record
-  // descriptor or 64-bit base arithmetic.
+  // tile 0 on (tile j at scalar offset j * WAVES * kRecBytes) and X (tile t
+  // at scalar offset 128 t), so those loads carry no per-record descriptor
+  // or 64-bit base arithmetic.
   __amdgpu_buffer_rsrc_t frs[F];
 #pragma unroll
   for (int f = 0; f < F; ++f) frs[f] = r_buffer(fixed + rec0[f] * kRecBytes, (uint32_t)KT * kRecBytes);
-  const __amdgpu_buffer_rsrc_t ers =
-      r_buffer(exps, (uint32_t)eoff[(int64_t)bands * KT] + (uint32_t)ZS_STREAM_SLACK_BYTES);
   // X fragments: this lane's 32-bit byte offset (row n, 8 columns; N <= 16
   // here: offsets far below 2^31).  Lanes of rows n >= N get the offset
   // 2^31, at or past the resource's range whether or not the scalar offset
@@ -604,7 +599,7 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
   {                                                                                \
     const int j_ = (J);                                                            \
     _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_)                               \
-      r_issue_exps_r(ers, __builtin_amdgcn_readlane(oe0[f_], j_),                  \
+      r_issue_exps(exps, __builtin_amdgcn_readlane(oe0[f_], j_),                  \
                      __builtin_amdgcn_readlane(oe1[f_], j_), R[f_], MT[f_]);       \
   }
 #define RZ_ISSUE(J, R, MT) \
@@ -792,11 +787,9 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   // kb0 >= KT, clamps to the last tile of the row).
   auto tile_of = [&](int j) { return min(kb0 + PH * j + p, kb1 - 1); };
   const int64_t rowrec = (int64_t)band * KT;
-  // Buffer resources built once (the band's records, the outlier stream, X);
+  // Buffer resources built once (the band's records, X);
   // per-record and per-tile positions go into the load offsets.
   const __amdgpu_buffer_rsrc_t frs = r_buffer(fixed + rowrec * kRecBytes, (uint32_t)KT * kRecBytes);
-  const __amdgpu_buffer_rsrc_t ers =
-      r_buffer(exps, (uint32_t)eoff[(int64_t)(M >> 4) * KT] + (uint32_t)ZS_STREAM_SLACK_BYTES);
   const __amdgpu_buffer_rsrc_t xrs = r_buffer(X, 0x80000000u);
 
   // X tile loads of this thread: chunk c = t + 64*BANDS*i, row c/8, 16-byte
@@ -836,7 +829,7 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
     int e0, e1;
     offs(j, e0, e1);
     r_issue_fixed_r(frs, (uint32_t)tile_of(j) * kRecBytes, R);
-    r_issue_exps_r(ers, e0, e1, R, Mt);
+    r_issue_exps(exps, e0, e1, R, Mt);
   };
   auto xload = [&](int j, u32x4 (&XR)[kXC]) {
     const uint32_t xs = (uint32_t)tile_of(j) * 128u;
@@ -873,7 +866,7 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
     xload(1, XB);
 #pragma unroll
     for (int k = 0; k < RD; ++k)
-      r_issue_exps_r(ers, __builtin_amdgcn_readlane(oe0, k), __builtin_amdgcn_readlane(oe1, k),
+      r_issue_exps(exps, __builtin_amdgcn_readlane(oe0, k), __builtin_amdgcn_readlane(oe1, k),
                    R[k], MT[k]);
     r_tab_store_exp<BANDS * PH * 64>(T, tab, threadIdx.x, ex.lo, ex.hi);
   }
@@ -1047,12 +1040,10 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
   const int cnt = (span - p + PH - 1) / PH;       // valid tiles of this phase
   auto tile_of = [&](int j) { return min(kb0 + PH * j + p, kb1 - 1); };
   const int64_t rowrec[2] = {(int64_t)band0 * KT, (int64_t)(band0 + 1) * KT};
-  // Buffer resources built once (each band's records, the outlier stream, X).
+  // Buffer resources built once (each band's records, X).
   const __amdgpu_buffer_rsrc_t frs[2] = {
       r_buffer(fixed + rowrec[0] * kRecBytes, (uint32_t)KT * kRecBytes),
       r_buffer(fixed + rowrec[1] * kRecBytes, (uint32_t)KT * kRecBytes)};
-  const __amdgpu_buffer_rsrc_t ers =
-      r_buffer(exps, (uint32_t)eoff[(int64_t)(M >> 4) * KT] + (uint32_t)ZS_STREAM_SLACK_BYTES);
   const __amdgpu_buffer_rsrc_t xrs = r_buffer(X, 0x80000000u);
 
   constexpr int kXC = (2 * NB + WP - 1) / WP;  // 16-byte X chunks per thread
@@ -1087,7 +1078,7 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
       r_issue_fixed_r(frs[f], (uint32_t)tile_of(j) * kRecBytes, R[f]);
-      r_issue_exps_r(ers, __builtin_amdgcn_readlane(oe0[f], j - c),
+      r_issue_exps(exps, __builtin_amdgcn_readlane(oe0[f], j - c),
                      __builtin_amdgcn_readlane(oe1[f], j - c), R[f], Mt[f]);
     }
   };
@@ -1129,9 +1120,9 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
       xload(1, XB);
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
-        r_issue_exps_r(ers, __builtin_amdgcn_readlane(oe0[f], 0),
+        r_issue_exps(exps, __builtin_amdgcn_readlane(oe0[f], 0),
                      __builtin_amdgcn_readlane(oe1[f], 0), R0[f], M0[f]);
-        r_issue_exps_r(ers, __builtin_amdgcn_readlane(oe0[f], 1),
+        r_issue_exps(exps, __builtin_amdgcn_readlane(oe0[f], 1),
                      __builtin_amdgcn_readlane(oe1[f], 1), R1[f], M1[f]);
       }
       r_tab_store_exp<BANDS / 2 * PH * 64>(T, tab, threadIdx.x, ex.lo, ex.hi);
