@@ -149,6 +149,14 @@ int zs_analyze_top_exponents_gpu(void* stream, const uint16_t* d_input, int64_t 
  * unchanged, so it returns the same window wherever both apply. */
 int zs_analyze_top_exponents_u64_gpu(void* stream, const uint16_t* d_input, int64_t numel,
                                      uint64_t* d_exponent_counts, int32_t* d_top_exponents);
+/* kernel_benchmark/utils.h:189-272 analyzeExponentDistribution_BF16 (the
+ * weights path's host window rule: seven strict-maximum passes, ties to the
+ * lowest exponent, no [0, 248] clamp) on the device, over the same 64-bit
+ * histogram as above: the window zs_analyze_exponents_host returns, without
+ * copying the matrix to the host.  The reference runs this rule on the CPU
+ * only; the two rules differ on sparse histograms (e.g. a single exponent). */
+int zs_analyze_exponents_weights_gpu(void* stream, const uint16_t* d_input, int64_t numel,
+                                     uint64_t* d_exponent_counts, int32_t* d_top_exponents);
 
 /* build/L_API.cuh:144-165 InitBF16MatrixTripleBitmap_GPU: device encoder
  * producing the canonical streams.  d_temp_sm / d_temp_full are accepted for
@@ -365,9 +373,13 @@ int64_t zs_container_bytes(const zs_container_desc_t* d);
  * pointers to the stream bytes in table order.  name: up to 63 bytes. */
 int zs_container_write(const zs_container_desc_t* d, const char* name,
                        const void* const* streams, void* dst, int64_t dst_bytes);
-/* Validates a container image (magic, version, CRCs, sizes, totals) and
- * returns its descriptor, name (64 bytes) and each stream's byte offset in
- * src.  ZS_E_INVAL for a damaged image, ZS_E_UNSUPPORTED for another version. */
+/* Validates a container image (magic, version, CRCs, sizes, and every offset
+ * against the bit-planes / codes it indexes: canonical global and median
+ * tile offsets, re-tiled per-record outlier offsets) and returns its
+ * descriptor, name (64 bytes) and each stream's byte offset in src.
+ * ZS_E_INVAL for a damaged or inconsistent image (CRC-valid images with bad
+ * offsets included), ZS_E_UNSUPPORTED for another version.  zs_container_write
+ * applies the same offset check to its input. */
 int zs_container_parse(const void* src, int64_t src_bytes, zs_container_desc_t* d,
                        char* name_out, int64_t* stream_offsets);
 

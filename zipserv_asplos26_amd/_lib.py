@@ -52,6 +52,7 @@ SIGNATURES = {
                                     C.c_int, _p, C.c_int]),
     "zs_analyze_top_exponents_gpu": (C.c_int, [_p, _p, _i64, _p, _p, _p]),
     "zs_analyze_top_exponents_u64_gpu": (C.c_int, [_p, _p, _i64, _p, _p]),
+    "zs_analyze_exponents_weights_gpu": (C.c_int, [_p, _p, _i64, _p, _p]),
     "zs_init_bf16_matrix_triple_bitmap_gpu": (
         C.c_int, [_p, _p, C.c_int, C.c_int, _p] + [_p] * 8 + [_p] * 2 + [_p] * 4 + [_p] * 4),
     "zs_retiled_num_records": (C.c_int64, [C.c_int, C.c_int]),

@@ -237,8 +237,47 @@ def _check_cuda(t, name, dtype=None):
         raise ValueError(f"{name} must be {dtype}")
 
 
-def compress_zipserv(input, logical_rows: int | None = None, logical_cols: int | None = None):
+WINDOW_RULES = ("kv", "weights")
+
+
+def _device_window(input, window, top, counts_u64=None):
+    """Writes the 7 window exponents of `input` into the int32 device tensor
+    `top` on the current stream.
+
+    window: "kv"      -- AnalyzeTopExponentsGPU's rule
+                         (zipserv_decode_attention_ext.cu:65-134), the
+                         reference's KV-cache compressor;
+            "weights" -- analyzeExponentDistribution_BF16's rule
+                         (kernel_benchmark/utils.h:189-272), the reference's
+                         weight path (same window as analyze_exponents());
+            7 ints    -- an explicit window (top[0] .. top[0] + 6).
+    """
+    torch = _torch()
+    L = lib()
+    if isinstance(window, str):
+        if window not in WINDOW_RULES:
+            raise ValueError(f"window must be one of {WINDOW_RULES} or 7 exponents")
+        counts = counts_u64 if counts_u64 is not None else torch.empty(
+            256, dtype=torch.int64, device=input.device)
+        fn = "zs_analyze_top_exponents_u64_gpu" if window == "kv" else \
+            "zs_analyze_exponents_weights_gpu"
+        check(fn, getattr(L, fn)(_stream(), _dptr(input), input.numel(), _dptr(counts),
+                                 _dptr(top)))
+        return
+    w = [int(v) for v in window]
+    if len(w) != 7 or any(w[i] != w[0] + i for i in range(7)):
+        raise ValueError("an explicit window is 7 consecutive exponents")
+    top.copy_(torch.tensor(w, dtype=torch.int32))
+
+
+def compress_zipserv(input, logical_rows: int | None = None, logical_cols: int | None = None,
+                     window="kv", _with_tiles: bool = False):
     """zipserv_decode_attention_ext.cpp:81-88 / .cu:157-265 on the GPU.
+
+    `window` picks the exponent-window rule (see _device_window): "kv" is the
+    reference compressor's own; "weights" reproduces the host encoder's
+    window (InitBF16MatrixTripleBitmap after analyzeExponentDistribution_BF16)
+    so the streams equal zs_init_bf16_matrix_triple_bitmap's bytes.
 
     Returns [sign_mantissa, compressed_full, bitmap1, bitmap2, bitmap3,
     tile_offsets_median, tile_offsets_global, meta] where meta is the int64
@@ -273,8 +312,12 @@ def compress_zipserv(input, logical_rows: int | None = None, logical_cols: int |
     counts = torch.empty(256, **i32)
     done = torch.empty(4, **i32)
     st = _stream()
-    check("zs_analyze_top_exponents_gpu",
-          L.zs_analyze_top_exponents_gpu(st, _dptr(input), mk, _dptr(counts), _dptr(top), _dptr(done)))
+    if isinstance(window, str) and window == "kv":
+        check("zs_analyze_top_exponents_gpu",
+              L.zs_analyze_top_exponents_gpu(st, _dptr(input), mk, _dptr(counts), _dptr(top),
+                                             _dptr(done)))
+    else:
+        _device_window(input, window, top)
     check("zs_init_bf16_matrix_triple_bitmap_gpu",
           L.zs_init_bf16_matrix_triple_bitmap_gpu(
               st, _dptr(input), rows, cols, _dptr(top), _dptr(sm), _dptr(fu), _dptr(b1),
@@ -294,7 +337,8 @@ def compress_zipserv(input, logical_rows: int | None = None, logical_cols: int |
     meta = torch.tensor([rows, cols, rows if logical_rows is None else logical_rows,
                          cols if logical_cols is None else logical_cols, max_hf, max_full,
                          start_exp, total_hf, total_full, ngt, inclusive], dtype=torch.int64)
-    return [sm, fu, b1, b2, b3, med, tog, meta]
+    parts = [sm, fu, b1, b2, b3, med, tog, meta]
+    return (parts, tiles) if _with_tiles else parts
 
 
 def make_zipserv_compressed(parts, layout: str = "by_kv_head") -> ZipservCompressed:
@@ -312,8 +356,12 @@ def make_zipserv_compressed(parts, layout: str = "by_kv_head") -> ZipservCompres
         layout=layout)
 
 
-def compress(input, logical_rows=None, logical_cols=None, layout="by_kv_head") -> ZipservCompressed:
-    return make_zipserv_compressed(compress_zipserv(input, logical_rows, logical_cols), layout)
+def compress(input, logical_rows=None, logical_cols=None, layout="by_kv_head",
+             window="kv") -> ZipservCompressed:
+    parts, tiles = compress_zipserv(input, logical_rows, logical_cols, window, _with_tiles=True)
+    c = make_zipserv_compressed(parts, layout)
+    c.tile_offsets = tiles  # per-small-tile (hf, full) counts; no kernel reads them
+    return c
 
 
 def decompress_zipserv_into(output, sign_mantissa, compressed_full, bitmap1, bitmap2, bitmap3,
@@ -367,8 +415,11 @@ def splitk_workspace(c, n: int, split_k: int):
 
 # Arrival counters of the in-kernel split-K reduction, one zero-filled int32
 # buffer per (device, stream): calls on one stream run one after another, so
-# they can share it, and every completed call leaves it zero.
+# they can share it, and every completed call leaves it zero.  A buffer that
+# a larger shape outgrows is retired, never freed: a HIP graph captured
+# earlier may still hold its address and replay into it.
 _SPLITK_COUNTERS = {}
+_RETIRED_COUNTERS = []
 _MIN_COUNTERS = 1 << 16
 
 
@@ -386,6 +437,8 @@ def splitk_counters(rows: int, n: int, device=None):
     if buf is None or buf.numel() < need:
         if torch.cuda.is_current_stream_capturing():
             return None
+        if buf is not None:
+            _RETIRED_COUNTERS.append(buf)
         buf = torch.zeros(max(need, _MIN_COUNTERS), dtype=torch.int32, device=dev)
         _SPLITK_COUNTERS[key] = buf
     return buf
@@ -428,9 +481,12 @@ def _retiled_alloc(rows, cols, total, dev):
     return fixed, exps, nrec
 
 
-def compress_retiled(input, logical_rows=None, logical_cols=None, layout="by_kv_head") -> ZipservRetiled:
-    """bf16 [rows, cols] on the GPU -> re-tiled layout (window chosen on the GPU
-    with the rule of zipserv_decode_attention_ext.cu:35-135)."""
+def compress_retiled(input, logical_rows=None, logical_cols=None, layout="by_kv_head",
+                     window="kv") -> ZipservRetiled:
+    """bf16 [rows, cols] on the GPU -> re-tiled layout.  The window is chosen on
+    the GPU, by default with the rule of zipserv_decode_attention_ext.cu:35-135
+    ("kv"); "weights" applies kernel_benchmark/utils.h:189-272 instead (see
+    _device_window)."""
     torch = _torch()
     _check_cuda(input, "input", torch.bfloat16)
     if input.dim() != 2:
@@ -447,9 +503,7 @@ def compress_retiled(input, logical_rows=None, logical_cols=None, layout="by_kv_
     total = torch.empty(1, dtype=torch.int64, device=dev)
     st = _stream()
     # 64-bit bins: the re-tiled layout takes matrices past 2^31 elements.
-    check("zs_analyze_top_exponents_u64_gpu",
-          L.zs_analyze_top_exponents_u64_gpu(st, _dptr(input), rows * cols, _dptr(counts),
-                                             _dptr(top)))
+    _device_window(input, window, top, counts)
     check("zs_compress_retiled_count_gpu",
           L.zs_compress_retiled_count_gpu(st, _dptr(input), rows, cols, _dptr(top), _dptr(cnt),
                                           _dptr(eoff), _dptr(total)))

@@ -71,6 +71,45 @@ __device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
+// Shared tail of both window rules (kernel_benchmark/utils.h:228-270,
+// zipserv_decode_attention_ext.cu:103-133): n found candidates (exponents),
+// filled up to 7 with 127 - i, sorted; the first candidate whose 7-exponent
+// window has only positive counts wins, else the start of the longest run of
+// consecutive candidates (clamped to [0, 248] by the GPU rule only).
+__device__ __forceinline__ void window_from_candidates(const int64_t* counts, int* cand, int n,
+                                                       bool clamp, int32_t* top) {
+  for (; n < 7; ++n) cand[n] = 127 - n;
+  for (int i = 1; i < 7; ++i) {
+    const int key = cand[i];
+    int j = i - 1;
+    while (j >= 0 && cand[j] > key) {
+      cand[j + 1] = cand[j];
+      --j;
+    }
+    cand[j + 1] = key;
+  }
+  for (int c = 0; c < 7; ++c) {
+    const int st = cand[c];
+    if (st < 0 || st + 6 > 255) continue;
+    bool all = true;
+    for (int i = 0; i < 7 && all; ++i) all = counts[st + i] > 0;
+    if (all) {
+      for (int i = 0; i < 7; ++i) top[i] = st + i;
+      return;
+    }
+  }
+  int best = cand[0], best_len = 1, run = 1;
+  for (int i = 1; i < 7; ++i) {
+    run = (cand[i] == cand[i - 1] + 1) ? run + 1 : 1;
+    if (run > best_len) {
+      best_len = run;
+      best = cand[i] - run + 1;
+    }
+  }
+  if (clamp) best = best < 0 ? 0 : (best > 248 ? 248 : best);
+  for (int i = 0; i < 7; ++i) top[i] = best + i;
+}
+
 // Window selection of zipserv_decode_attention_ext.cu:65-134: seven slots
 // start at count -1 (so zero counts can be taken); each exponent 0..255
 // replaces the first minimum slot on strictly greater count; candidates are
@@ -130,36 +169,49 @@ __global__ __launch_bounds__(64) void select_kernel(const C* counts_g, int32_t* 
   int cand[7], n = 0;
   for (int i = 0; i < 7; ++i)
     if (te[i] >= 0) cand[n++] = te[i];
-  for (; n < 7; ++n) cand[n] = 127 - n;
-  for (int i = 1; i < 7; ++i) {
-    const int key = cand[i];
-    int j = i - 1;
-    while (j >= 0 && cand[j] > key) {
-      cand[j + 1] = cand[j];
-      --j;
-    }
-    cand[j + 1] = key;
+  window_from_candidates(counts, cand, n, true, top);
+}
+
+// Window selection of kernel_benchmark/utils.h:189-272 (the host analyzer of
+// the weights path) on the device: seven passes each take the strictly
+// largest count not taken yet -- ties go to the lowest exponent and zero
+// counts are never taken -- missing candidates are filled with 127 - n, and
+// the tail is select_kernel's without the [0, 248] clamp.  One wave; lane i
+// holds exponents i, i + 64, i + 128, i + 192; a pass is one wave-wide
+// maximum of (count << 8 | 255 - exponent) over the exponents not taken.
+template <typename C>
+__global__ __launch_bounds__(64) void select_weights_kernel(const C* counts_g, int32_t* top) {
+  if (blockIdx.x != 0) return;
+  const int l = threadIdx.x;
+  __shared__ int64_t counts[256];
+  int64_t key[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t c = (int64_t)counts_g[64 * k + l];
+    counts[64 * k + l] = c;
+    // counts stay below 2^55 (numel < 2^63 / 256 is far past any tensor)
+    key[k] = c > 0 ? (c << 8) | (255 - (64 * k + l)) : 0;
   }
-  for (int c = 0; c < 7; ++c) {
-    const int st = cand[c];
-    if (st < 0 || st + 6 > 255) continue;
-    bool all = true;
-    for (int i = 0; i < 7 && all; ++i) all = counts[st + i] > 0;
-    if (all) {
-      for (int i = 0; i < 7; ++i) top[i] = st + i;
-      return;
+  __syncthreads();
+  int cand[7], n = 0;
+  for (int t = 0; t < 7; ++t) {
+    int64_t best = key[0];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) best = key[k] > best ? key[k] : best;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const int64_t o = __shfl_xor(best, off);
+      best = o > best ? o : best;
     }
+    if (best == 0) break;  // wave-uniform: no positive count left
+    const int e = 255 - (int)(best & 0xFF);
+    cand[n++] = e;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (64 * k + l == e) key[k] = 0;
   }
-  int best = cand[0], best_len = 1, run = 1;
-  for (int i = 1; i < 7; ++i) {
-    run = (cand[i] == cand[i - 1] + 1) ? run + 1 : 1;
-    if (run > best_len) {
-      best_len = run;
-      best = cand[i] - run + 1;
-    }
-  }
-  best = best < 0 ? 0 : (best > 248 ? 248 : best);
-  for (int i = 0; i < 7; ++i) top[i] = best + i;
+  if (l != 0) return;
+  window_from_candidates(counts, cand, n, false, top);
 }
 
 // Exponent -> code LUT in LDS (code 0 = outlier), as s_exp_lut of
@@ -490,7 +542,7 @@ static int hip_status(hipError_t e) { return e == hipSuccess ? ZS_OK : (int)e; }
 
 template <typename C>
 static int analyze(hipStream_t st, const uint16_t* d_input, int64_t numel, C* d_counts,
-                   int32_t* d_top) {
+                   int32_t* d_top, bool weights_rule = false) {
   // Enough workgroups to fill the chip, and at most 2^30 elements each.
   const int64_t blocks = std::max<int64_t>(
       std::min<int64_t>((numel + 2047) / 2048, (int64_t)device_cu_count() * 4),
@@ -500,7 +552,10 @@ static int analyze(hipStream_t st, const uint16_t* d_input, int64_t numel, C* d_
                      reinterpret_cast<int32_t*>(d_counts), (int)(256 * sizeof(C) / 4), 0);
   hipLaunchKernelGGL(hist_kernel<C>, dim3((unsigned)blocks), dim3(256), 0, st, d_input, numel,
                      d_counts);
-  hipLaunchKernelGGL(select_kernel<C>, dim3(1), dim3(64), 0, st, d_counts, d_top);
+  if (weights_rule)
+    hipLaunchKernelGGL(select_weights_kernel<C>, dim3(1), dim3(64), 0, st, d_counts, d_top);
+  else
+    hipLaunchKernelGGL(select_kernel<C>, dim3(1), dim3(64), 0, st, d_counts, d_top);
   return hip_status(hipGetLastError());
 }
 
@@ -519,6 +574,13 @@ extern "C" int zs_analyze_top_exponents_u64_gpu(void* stream, const uint16_t* d_
                                                 int32_t* d_top) {
   if (!d_input || numel <= 0 || !d_counts || !d_top) return ZS_E_INVAL;
   return analyze((hipStream_t)stream, d_input, numel, d_counts, d_top);
+}
+
+extern "C" int zs_analyze_exponents_weights_gpu(void* stream, const uint16_t* d_input,
+                                                 int64_t numel, uint64_t* d_counts,
+                                                 int32_t* d_top) {
+  if (!d_input || numel <= 0 || !d_counts || !d_top) return ZS_E_INVAL;
+  return analyze((hipStream_t)stream, d_input, numel, d_counts, d_top, true);
 }
 
 extern "C" int zs_init_bf16_matrix_triple_bitmap_gpu(
