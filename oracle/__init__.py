@@ -47,6 +47,8 @@ def lib():
             fn = getattr(L, name)
             fn.restype = C.c_int
             fn.argtypes = [p, C.c_int, C.c_int, p, p]
+        L.zso_compress_sse_mt.restype = C.c_int
+        L.zso_compress_sse_mt.argtypes = [p, C.c_int, C.c_int, p, p, C.c_int]
         L.zso_decompress.restype = C.c_int
         L.zso_decompress.argtypes = [p, C.c_int64, p, C.c_int64, p, p, p, p, C.c_int, C.c_int, C.c_int, p]
         L.zso_gemm_f32.argtypes = [p, p, C.c_int, C.c_int, C.c_int, p]
@@ -57,6 +59,8 @@ def lib():
         L.zso_gemm_splitk_bf16.argtypes = [p, p, C.c_int, C.c_int, C.c_int, C.c_int, p]
         L.zso_decode_attention_f64.argtypes = [p, p, p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                                p, C.c_double, p, p]
+        L.zso_decode_attention_absv_f64.argtypes = [p, p, p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                                    C.c_int, p, C.c_double, p, p, p]
         L.zso_compress_retiled.restype = C.c_int64
         L.zso_compress_retiled.argtypes = [p, C.c_int, C.c_int, C.c_int, p, p, p]
         L.zso_decompress_retiled.argtypes = [p, p, p, C.c_int, C.c_int, C.c_int, p]
@@ -169,28 +173,49 @@ def select_gpu(counts) -> list[int]:
     return top.tolist()
 
 
-def compress(a: np.ndarray, top=None, variant: str = "plain") -> Encoded:
-    """Encode a bf16 [M, K] matrix; variant in {plain, lut, sse}."""
+def _zeroed(n, dt):
+    """malloc + memset of the output buffers (the reference's encoder does both
+    inside its timed region, L_API.cu:350-357)."""
+    b = np.empty(n, dt)
+    b.fill(0)
+    return b
+
+
+def compress(a: np.ndarray, top=None, variant: str = "plain", threads: int = 0,
+             timings: dict | None = None) -> Encoded:
+    """Encode a bf16 [M, K] matrix; variant in {plain, lut, sse, sse_mt}
+    (sse_mt: the sse encoder over `threads` OpenMP threads, 0 = all).  With
+    `timings`, the output allocation (malloc + memset) and the encode are
+    timed separately into timings["alloc_s"] / timings["encode_s"]."""
+    import time
     a = np.ascontiguousarray(a, dtype=np.uint16)
     M, K = a.shape
     if top is None:
         top = analyze_cpu(a)
     topa = np.ascontiguousarray(top, dtype=np.int32)
     mk = M * K
+    t0 = time.perf_counter()
     bufs = dict(
-        sign_mantissa=np.zeros(mk + 16, np.uint8),
-        compressed_full=np.zeros(mk + 8, np.uint16),
-        bitmap1=np.zeros(mk // 64, np.uint64),
-        bitmap2=np.zeros(mk // 64, np.uint64),
-        bitmap3=np.zeros(mk // 64, np.uint64),
-        tile_offsets=np.zeros(2 * (mk // 64), np.int32),
-        tile_offsets_median=np.zeros(2 * (mk // 1024), np.int32),
-        tile_offsets_global=np.zeros(2 * (mk // 4096 + 1), np.int32),
+        sign_mantissa=_zeroed(mk + 16, np.uint8),
+        compressed_full=_zeroed(mk + 8, np.uint16),
+        bitmap1=_zeroed(mk // 64, np.uint64),
+        bitmap2=_zeroed(mk // 64, np.uint64),
+        bitmap3=_zeroed(mk // 64, np.uint64),
+        tile_offsets=_zeroed(2 * (mk // 64), np.int32),
+        tile_offsets_median=_zeroed(2 * (mk // 1024), np.int32),
+        tile_offsets_global=_zeroed(2 * (mk // 4096 + 1), np.int32),
     )
     enc = _Encoded(**{k: _ptr(v) for k, v in bufs.items()})
-    fn = {"plain": lib().zso_compress_plain, "lut": lib().zso_compress_lut,
-          "sse": lib().zso_compress_sse}[variant]
-    rc = fn(_ptr(a), M, K, _ptr(topa), C.byref(enc))
+    t1 = time.perf_counter()
+    if variant == "sse_mt":
+        rc = lib().zso_compress_sse_mt(_ptr(a), M, K, _ptr(topa), C.byref(enc), int(threads))
+    else:
+        fn = {"plain": lib().zso_compress_plain, "lut": lib().zso_compress_lut,
+              "sse": lib().zso_compress_sse}[variant]
+        rc = fn(_ptr(a), M, K, _ptr(topa), C.byref(enc))
+    if timings is not None:
+        timings["alloc_s"] = t1 - t0
+        timings["encode_s"] = time.perf_counter() - t1
     if rc < 0:
         raise ValueError(f"oracle compress failed for shape {a.shape}")
     return Encoded(
@@ -264,8 +289,11 @@ def gemm_splitk_bf16(W: np.ndarray, X: np.ndarray, split_k: int) -> np.ndarray:
     return Y
 
 
-def decode_attention_f64(q, k, v, seqlens=None, scale=None):
-    """q [B,H,D], k/v [B,T,Hkv,D] (bf16 bits) -> (out [B,H,D] f64, lse [B,H] f64)."""
+def decode_attention_f64(q, k, v, seqlens=None, scale=None, return_absv=False):
+    """q [B,H,D], k/v [B,T,Hkv,D] (bf16 bits) -> (out [B,H,D] f64, lse [B,H] f64),
+    plus absv [B,H,D] = sum_t p_t |v_t| (the softmax-weighted magnitude of V,
+    which bounds the effect of rounding the weights to bf16) when
+    `return_absv`."""
     q = np.ascontiguousarray(q, dtype=np.uint16)
     k = np.ascontiguousarray(k, dtype=np.uint16)
     v = np.ascontiguousarray(v, dtype=np.uint16)
@@ -276,9 +304,11 @@ def decode_attention_f64(q, k, v, seqlens=None, scale=None):
     sl = None if seqlens is None else np.ascontiguousarray(seqlens, dtype=np.int32)
     out = np.zeros((B, H, D), np.float64)
     lse = np.zeros((B, H), np.float64)
-    lib().zso_decode_attention_f64(_ptr(q), _ptr(k), _ptr(v), B, H, Hkv, T, D,
-                                   None if sl is None else _ptr(sl), float(scale), _ptr(out), _ptr(lse))
-    return out, lse
+    absv = np.zeros((B, H, D), np.float64) if return_absv else None
+    lib().zso_decode_attention_absv_f64(_ptr(q), _ptr(k), _ptr(v), B, H, Hkv, T, D,
+                                        None if sl is None else _ptr(sl), float(scale), _ptr(out),
+                                        _ptr(lse), None if absv is None else _ptr(absv))
+    return (out, lse, absv) if return_absv else (out, lse)
 
 
 REC_BYTES = 1408

@@ -300,6 +300,35 @@ static void scan_and_scatter(int ngt, const uint8_t* temp_sm, const uint16_t* te
     out->total_full = fl;
 }
 
+/* scan_and_scatter with the copies in parallel: the offsets (a serial scan
+ * over the global tiles) first, then every tile's streams copied at once. */
+static void scan_and_scatter_mt(int ngt, const uint8_t* temp_sm, const uint16_t* temp_full,
+                                const int32_t* gt_hf, const int32_t* gt_full, zso_encoded* out,
+                                int threads) {
+    int64_t hf = 0, fl = 0;
+    out->max_high_freq_count = 0;
+    out->max_full_count = 0;
+    out->tile_offsets_global[0] = 0;
+    out->tile_offsets_global[1] = 0;
+    for (int i = 0; i < ngt; ++i) {
+        hf += gt_hf[i];
+        fl += gt_full[i];
+        out->tile_offsets_global[(i + 1) * 2] = (int32_t)hf;
+        out->tile_offsets_global[(i + 1) * 2 + 1] = (int32_t)fl;
+        if (gt_hf[i] > out->max_high_freq_count) out->max_high_freq_count = gt_hf[i];
+        if (gt_full[i] > out->max_full_count) out->max_full_count = gt_full[i];
+    }
+#pragma omp parallel for schedule(static) num_threads(threads)
+    for (int i = 0; i < ngt; ++i) {
+        memcpy(out->sign_mantissa + out->tile_offsets_global[2 * i],
+               temp_sm + (size_t)i * (4096 + 15), (size_t)gt_hf[i]);
+        memcpy(out->compressed_full + out->tile_offsets_global[2 * i + 1],
+               temp_full + (size_t)i * (4096 + 7), (size_t)gt_full[i] * sizeof(uint16_t));
+    }
+    out->total_high_freq = hf;
+    out->total_full = fl;
+}
+
 /* Median-offset bookkeeping of pass 1 (csrc/L_API.cu:692-716): after each
  * 16-small-tile median except the last, record the cumulative counts. */
 static void median_step(int st, int thf, int tfull, int* cur_hf, int* cur_full, int* cum_hf,
@@ -406,7 +435,25 @@ static void init_compress_lut(void) {
     g_compress_lut_ready = 1;
 }
 
+static int compress_sse_impl(const uint16_t* a, int M, int K, const int top[7], zso_encoded* out,
+                             int threads);
+
 int zso_compress_sse(const uint16_t* a, int M, int K, const int top[7], zso_encoded* out) {
+    return compress_sse_impl(a, M, K, top, out, 1);
+}
+
+/* zso_compress_sse with pass 1 (per global tile, independent) and the pass-3
+ * copies spread over `threads` OpenMP threads (<= 0: all), as the
+ * reference's multi-threaded compress benchmarks parallelise over tiles
+ * (kernel_benchmark/README.md:255-257,
+ * bench_kv_cache_zipserv_compress_scaling.cu:681).  Same bytes. */
+int zso_compress_sse_mt(const uint16_t* a, int M, int K, const int top[7], zso_encoded* out,
+                        int threads) {
+    return compress_sse_impl(a, M, K, top, out, threads <= 0 ? omp_get_max_threads() : threads);
+}
+
+static int compress_sse_impl(const uint16_t* a, int M, int K, const int top[7], zso_encoded* out,
+                             int threads) {
     if (check_dims(M, K)) return -1;
     init_tile_pos();
     init_compress_lut();
@@ -424,6 +471,7 @@ int zso_compress_sse(const uint16_t* a, int M, int K, const int top[7], zso_enco
     const __m128i v_one = _mm_set1_epi16(1), v_ff = _mm_set1_epi16(0xFF);
     const __m128i v_80 = _mm_set1_epi16(0x80), v_7f = _mm_set1_epi16(0x7F);
     const __m128i v_zero = _mm_setzero_si128();
+#pragma omp parallel for schedule(static) num_threads(threads) if (threads > 1)
     for (int gt = 0; gt < ngt; ++gt) {
         const int grow = (gt / gtk) * 64, gcol = (gt % gtk) * 64;
         uint8_t* my_sm = temp_sm + (size_t)gt * (4096 + 15);
@@ -486,7 +534,11 @@ int zso_compress_sse(const uint16_t* a, int M, int K, const int top[7], zso_enco
         gt_hf[gt] = si;
         gt_full[gt] = fi;
     }
-    scan_and_scatter(ngt, temp_sm, temp_full, gt_hf, gt_full, out);
+    if (threads > 1) {
+        scan_and_scatter_mt(ngt, temp_sm, temp_full, gt_hf, gt_full, out, threads);
+    } else {
+        scan_and_scatter(ngt, temp_sm, temp_full, gt_hf, gt_full, out);
+    }
     free(temp_sm); free(temp_full); free(gt_hf); free(gt_full);
     return ngt;
 }
@@ -635,6 +687,16 @@ void zso_gemm_splitk_bf16(const uint16_t* W, const uint16_t* X, int M, int N, in
 void zso_decode_attention_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v, int B, int H,
                               int Hkv, int T, int D, const int32_t* seqlens, double scale,
                               double* out, double* lse) {
+    zso_decode_attention_absv_f64(q, k, v, B, H, Hkv, T, D, seqlens, scale, out, lse, NULL);
+}
+
+/* As zso_decode_attention_f64, plus absv[b][h][d] = sum_t p_t |v_t,d| with
+ * the softmax weights p_t (when absv is not NULL): the scale of the error
+ * that rounding the weights to bf16 before the P.V product can cause
+ * (|error| <= 2^-8 * absv for bf16's unit roundoff 2^-8). */
+void zso_decode_attention_absv_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v, int B,
+                                   int H, int Hkv, int T, int D, const int32_t* seqlens,
+                                   double scale, double* out, double* lse, double* absv) {
     const int G = H / Hkv;
     double* s = (double*)malloc((size_t)(T > 0 ? T : 1) * sizeof(double));
     for (int b = 0; b < B; ++b)
@@ -650,7 +712,9 @@ void zso_decode_attention_f64(const uint16_t* q, const uint16_t* k, const uint16
                 if (s[t] > mx) mx = s[t];
             }
             double* op = out + ((int64_t)b * H + h) * D;
+            double* ap = absv ? absv + ((int64_t)b * H + h) * D : NULL;
             for (int d = 0; d < D; ++d) op[d] = 0.0;
+            if (ap) for (int d = 0; d < D; ++d) ap[d] = 0.0;
             if (L <= 0) { lse[(int64_t)b * H + h] = -INFINITY; continue; }
             double den = 0.0;
             for (int t = 0; t < L; ++t) {
@@ -658,8 +722,10 @@ void zso_decode_attention_f64(const uint16_t* q, const uint16_t* k, const uint16
                 den += p;
                 const uint16_t* vp = v + (((int64_t)b * T + t) * Hkv + kh) * D;
                 for (int d = 0; d < D; ++d) op[d] += p * zso_bf16_to_f32(vp[d]);
+                if (ap) for (int d = 0; d < D; ++d) ap[d] += p * fabs((double)zso_bf16_to_f32(vp[d]));
             }
             for (int d = 0; d < D; ++d) op[d] /= den;
+            if (ap) for (int d = 0; d < D; ++d) ap[d] /= den;
             lse[(int64_t)b * H + h] = mx + log(den);
         }
     free(s);

@@ -61,6 +61,10 @@ int zso_compress_plain(const uint16_t* a, int M, int K, const int top[7], zso_en
 int zso_compress_lut(const uint16_t* a, int M, int K, const int top[7], zso_encoded* out);
 /* csrc/L_API.cu:773-1053 InitBF16MatrixTripleBitmap_Reuse_SIMD (SSE/SSSE3). */
 int zso_compress_sse(const uint16_t* a, int M, int K, const int top[7], zso_encoded* out);
+/* The same bytes with the global tiles spread over `threads` OpenMP threads
+ * (<= 0: all), the reference benchmarks' multi-threaded compress mode. */
+int zso_compress_sse_mt(const uint16_t* a, int M, int K, const int top[7], zso_encoded* out,
+                        int threads);
 
 /* kernel_benchmark/bench_kv_cache_zipserv_decompress_token_scaling.cu:2106-2218
  * DecompressZipServChunkCPU.  Returns 0, or -1 on an out-of-range stream read. */
@@ -96,6 +100,10 @@ void zso_gemm_splitk_bf16(const uint16_t* W, const uint16_t* X, int M, int N, in
 void zso_decode_attention_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                               int B, int H, int Hkv, int T, int D, const int32_t* seqlens,
                               double scale, double* out, double* lse);
+/* The same, plus absv[B][H][D] = sum_t p_t |v_t,d| (NULL: not computed). */
+void zso_decode_attention_absv_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                   int B, int H, int Hkv, int T, int D, const int32_t* seqlens,
+                                   double scale, double* out, double* lse, double* absv);
 
 #ifdef __cplusplus
 }

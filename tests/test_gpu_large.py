@@ -9,7 +9,10 @@ histogram whose largest bin itself exceeds INT32_MAX, a bit-exact
 compress -> decompress round trip of a 2.16 G-element KV cache, and decode
 attention over that cache, bit-identical to the same kernel over the dense
 cache and within 2e-3 (plus the bf16 rounding terms of test_gpu_attention)
-of an fp32 reference on sampled batch entries.
+of an fp32 reference on sampled batch entries, lse included.  The same at
+benchmark config 4's largest cache (B = 32, T = 128k: 2^32 elements per
+tensor, a fixed part past 4 GiB), and config-5 points (B = 8, T = 16k;
+B = 32, T = 32k) against the fp64 oracle on sampled batch entries.
 """
 import math
 
@@ -62,12 +65,39 @@ def _kv(torch, g, B, T, Hkv=8, D=128):
     return (torch.randn(B, T, Hkv, D, device="cuda", generator=g) * scale).to(torch.bfloat16)
 
 
-def test_retiled_kv_and_attention_past_int32(torch_cuda):
+def _fp32_reference(torch, q, k, v, b):
+    """fp32 decode attention of batch entry b (matmuls on contiguous fp32
+    operands): output [H, D], the natural-log lse [H] and absv [H, D] =
+    sum_t p_t |v_t| (the scale of the bf16 rounding of the weights)."""
+    Hkv, D = k.shape[2], k.shape[3]
+    H = q.shape[2]
+    G = H // Hkv
+    kb = k[b].float().permute(1, 2, 0).contiguous()          # [Hkv, D, T]
+    vb = v[b].float().permute(1, 0, 2).contiguous()          # [Hkv, T, D]
+    qb = q[b, 0].float().view(Hkv, G, D)
+    s = torch.matmul(qb, kb) / math.sqrt(D)                  # [Hkv, G, T]
+    lse = torch.logsumexp(s, dim=-1).view(H)
+    p = torch.softmax(s, dim=-1)
+    ref = torch.matmul(p, vb).view(H, D)
+    absv = torch.matmul(p, vb.abs()).view(H, D)
+    return ref, lse, absv
+
+
+def _check_sampled(torch, q, k, v, out, lse, batches):
+    for b in batches:
+        ref, ref_lse, absv = _fp32_reference(torch, q, k, v, b)
+        o = out[b, 0].float()
+        tol = 2e-3 + 2.0 ** -8 * ref.abs() + 2.0 ** -8 * absv  # zs_testutil.attention_tolerance
+        assert bool(((o - ref).abs() <= tol).all()), (b, float((o - ref).abs().max()))
+        assert bool(((lse[b] - ref_lse).abs() <= 1e-3 + 1e-4 * ref_lse.abs()).all()), b
+
+
+def _large_kv_case(torch, B, T, seed, check_canonical_refused):
     import zipserv_asplos26_amd.attention as za
-    torch = torch_cuda
-    B, T, Hkv, H, D = 64, 33000, 8, 64, 128
+    Hkv, H, D = 8, 64, 128
+    print(f"large KV case B={B} T={T}", flush=True)
     g = torch.Generator(device="cuda")
-    g.manual_seed(11)
+    g.manual_seed(seed)
     k = _kv(torch, g, B, T)
     mat, _, _ = za.pad_batched_kv_prefix_by_kv_head(k)
     assert mat.numel() > 2**31 - 1
@@ -75,26 +105,66 @@ def test_retiled_kv_and_attention_past_int32(torch_cuda):
     back = zs.decompress_retiled(rk)
     assert torch.equal(back.view(torch.int16), mat.view(torch.int16))  # bit-exact round trip
     del back, mat
-    with pytest.raises(zs.ZipServError):  # canonical streams: int32 offsets
-        za.compress_kv(k)
+    if check_canonical_refused:
+        with pytest.raises(zs.ZipServError):  # canonical streams: int32 offsets
+            za.compress_kv(k)
     v = _kv(torch, g, B, T)
     rv = za.compress_kv(v, retiled=True)
     q = torch.randn(B, 1, H, D, device="cuda", generator=g).to(torch.bfloat16)
-    out = za.flash_attn_with_kvcache_zipserv(q, rk, rv, Hkv, T)
+    out, lse = za.flash_attn_with_kvcache_zipserv(q, rk, rv, Hkv, T, return_softmax_lse=True)
+    outd, lsed = za.flash_attn_with_kvcache_dense(q, k, v, return_softmax_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), outd.view(torch.int16))
+    assert torch.equal(lse, lsed)
+    return q, k, v, rk, out, lse
+
+
+def test_retiled_kv_and_attention_past_int32(torch_cuda):
+    torch = torch_cuda
+    B = 64
+    q, k, v, _, out, lse = _large_kv_case(torch, B, 33000, 11, True)
+    _check_sampled(torch, q, k, v, out, lse, (0, 37, B - 1))
+
+
+def test_retiled_kv_past_4g_elements(torch_cuda):
+    # Benchmark config 4's largest cache: B = 32, T = 128k, 8 KV heads,
+    # head_dim 128 = 2^32 elements per K / V tensor (8 GiB bf16); its fixed
+    # part (5.6 GiB) is past the 32-bit range of a buffer resource, so the
+    # attention kernel's per-wave resources must saturate, not wrap.
+    torch = torch_cuda
+    B, T = 32, 131072
+    q, k, v, rk, out, lse = _large_kv_case(torch, B, T, 17, False)
+    assert rk.rows * rk.cols == 1 << 32
+    assert rk.fixed.numel() > (1 << 32)
+    _check_sampled(torch, q, k, v, out, lse, (0, 13, B - 1))
+
+
+@pytest.mark.parametrize("B,T", [(8, 16384), (32, 32768)])
+def test_attention_config5_points_against_oracle(torch_cuda, B, T):
+    # benchmark config 5 points on the re-tiled layout, sampled batch entries
+    # against the fp64 oracle with the per-element bound of test_gpu_attention
+    import zipserv_asplos26_amd.attention as za
+    from zs_testutil import attention_tolerance, from_torch_bf16
+    torch = torch_cuda
+    Hkv, H, D = 8, 64, 128
+    print(f"config-5 point B={B} T={T}", flush=True)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(B * 7 + T)
+    k, v = _kv(torch, g, B, T), _kv(torch, g, B, T)
+    q = torch.randn(B, 1, H, D, device="cuda", generator=g).to(torch.bfloat16)
+    rk, rv = za.compress_kv(k, retiled=True), za.compress_kv(v, retiled=True)
+    out, lse = za.flash_attn_with_kvcache_zipserv(q, rk, rv, Hkv, T, return_softmax_lse=True)
     outd = za.flash_attn_with_kvcache_dense(q, k, v)
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), outd.view(torch.int16))
-    # fp32 reference for sampled sequences (matmul on contiguous fp32 operands)
-    G = H // Hkv
-    for b in (0, 37, B - 1):
-        kb = k[b].float().permute(1, 2, 0).contiguous()          # [Hkv, D, T]
-        vb = v[b].float().permute(1, 0, 2).contiguous()          # [Hkv, T, D]
-        qb = q[b, 0].float().view(Hkv, G, D)
-        p = torch.softmax(torch.matmul(qb, kb) / math.sqrt(D), dim=-1)
-        ref = torch.matmul(p, vb).view(H, D)
-        o = out[b, 0].float()
-        tol = 2e-3 + ref.abs() * 2.0 ** -7 + vb.abs().max() * 2.0 ** -9
-        assert bool(((o - ref).abs() <= tol).all()), float((o - ref).abs().max())
+    for b in (0, B - 1):
+        qb = from_torch_bf16(q[b:b + 1, 0])
+        kb, vb = from_torch_bf16(k[b:b + 1]), from_torch_bf16(v[b:b + 1])
+        ref, ref_lse, absv = zo.decode_attention_f64(qb, kb, vb, return_absv=True)
+        o = zo.bf16_to_f32(from_torch_bf16(out[b:b + 1, 0])).astype(np.float64)
+        err = np.abs(o - ref)
+        assert np.all(err <= attention_tolerance(ref, absv)), (b, err.max())
+        np.testing.assert_allclose(lse[b:b + 1].cpu().numpy(), ref_lse, rtol=1e-4, atol=1e-3)
 
 
 def test_retiled_zipgemm_x_past_2gib(torch_cuda):

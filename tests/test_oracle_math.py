@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 
 import oracle as zo
-from zs_testutil import normal_bf16, weights_bf16
+from zs_testutil import kv_bf16, normal_bf16, weights_bf16
 
 
 def test_bf16_rounding_helpers():
@@ -138,3 +138,62 @@ def test_multithreaded_baseline_variants_match(threads):
     e = zo.compress(W)
     np.testing.assert_array_equal(zo.decompress_mt(e, threads), W)
     np.testing.assert_array_equal(zo.gemm_f32_mt(W, X, threads), zo.gemm_f32(W, X))
+
+
+def test_attention_absv_matches_numpy():
+    rng = np.random.default_rng(21)
+    B, T, Hkv, H, D = 2, 150, 4, 8, 128
+    q, k, v = normal_bf16(rng, (B, H, D)), kv_bf16(rng, B, T, Hkv, D), kv_bf16(rng, B, T, Hkv, D)
+    out, lse, absv = zo.decode_attention_f64(q, k, v, seqlens=[150, 40], return_absv=True)
+    qf, kf, vf = (zo.bf16_to_f32(a).astype(np.float64) for a in (q, k, v))
+    for b, L in ((0, 150), (1, 40)):
+        for h in range(H):
+            s = kf[b, :L, h // 2] @ qf[b, h] / np.sqrt(D)
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            np.testing.assert_allclose(absv[b, h], p @ np.abs(vf[b, :L, h // 2]), rtol=1e-12)
+            np.testing.assert_allclose(out[b, h], p @ vf[b, :L, h // 2], rtol=1e-9, atol=1e-12)
+
+
+def _kernel_like_attention(q, k, v):
+    """The GPU kernel's rounding on the CPU: online softmax over 16-token
+    steps, weights rounded to bf16 against the running maximum before the
+    P.V product (fp32 sum of the unrounded weights as the denominator), the
+    output rounded to bf16."""
+    B, H, D = q.shape
+    T, Hkv = k.shape[1], k.shape[2]
+    G = H // Hkv
+    qf, kf, vf = (zo.bf16_to_f32(a).astype(np.float64) for a in (q, k, v))
+    out = np.zeros((B, H, D))
+    for b in range(B):
+        for h in range(H):
+            s = kf[b, :, h // G] @ qf[b, h] / np.sqrt(D)
+            m, l, o = -np.inf, 0.0, np.zeros(D)
+            for c in range(0, T, 16):
+                sc = s[c:c + 16]
+                mn = max(m, sc.max())
+                a = np.exp(m - mn) if m > -np.inf else 0.0
+                p = np.exp(sc - mn).astype(np.float32)
+                pb = zo.bf16_to_f32(zo.f32_to_bf16(p)).astype(np.float64)
+                l, o, m = l * a + float(p.sum()), o * a + pb @ vf[b, c:c + 16, h // G], mn
+            out[b, h] = zo.bf16_to_f32(zo.f32_to_bf16((o / l).astype(np.float32)))
+    return out
+
+
+def test_attention_bound_binds_on_planted_errors():
+    # The bound test_gpu_attention applies, at the config-5 shape (B = 1,
+    # T = 4096, GQA 64 / 8) on that test's seed-0 data: the kernel's own
+    # rounding stays inside it, while an oracle run that drops the last token
+    # or scales the scores by one bf16 ulp (2^-8) falls outside it.
+    from zs_testutil import attention_tolerance, kv_bf16 as kv
+    rng = np.random.default_rng(0)
+    B, T, Hkv, H, D = 1, 4096, 8, 64, 128
+    k, v = kv(rng, B, T, Hkv, D), kv(rng, B, T, Hkv, D)
+    q = normal_bf16(rng, (B, H, D))
+    ref, _, absv = zo.decode_attention_f64(q, k, v, return_absv=True)
+    tol = attention_tolerance(ref, absv)
+    assert np.all(np.abs(_kernel_like_attention(q, k, v) - ref) <= tol)
+    dropped, _ = zo.decode_attention_f64(q, k, v, seqlens=[T - 1])
+    assert np.any(np.abs(dropped - ref) > tol)
+    scaled, _ = zo.decode_attention_f64(q, k, v, scale=(1 + 2.0 ** -8) / np.sqrt(D))
+    assert np.any(np.abs(scaled - ref) > tol)

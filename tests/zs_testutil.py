@@ -55,3 +55,13 @@ def to_torch_bf16(a, device="cuda"):
 def from_torch_bf16(t):
     import torch
     return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def attention_tolerance(ref, absv):
+    """Per-element bound for bf16 decode attention against the fp64 oracle:
+    2e-3 absolute, plus bf16's unit roundoff 2^-8 of
+    the output (its final rounding) and of absv = sum_t p_t |v_t| (the
+    softmax weights rounded to bf16 before the P.V product, as FlashAttention
+    does, flash_fwd_kernel.h:892-1074: each weight moves by at most 2^-8 of
+    itself).  Arithmetic in fp32 adds far less than 2e-3 at these sizes."""
+    return 2e-3 + 2.0 ** -8 * np.abs(ref) + 2.0 ** -8 * absv

@@ -340,9 +340,9 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
       // goes into the scalar offset.
       const int64_t kr0 = (int64_t)(k_rowbase >> 4) * 2, vr0 = (int64_t)(v_rowbase >> 4) * 2;
       const __amdgpu_buffer_rsrc_t kfr =
-          r_buffer(p.kfix + kr0 * kRecBytes, (uint32_t)((p.k_nrec - kr0) * kRecBytes));
+          r_buffer(p.kfix + kr0 * kRecBytes, r_range((p.k_nrec - kr0) * kRecBytes));
       const __amdgpu_buffer_rsrc_t vfr =
-          r_buffer(p.vfix + vr0 * kRecBytes, (uint32_t)((p.v_nrec - vr0) * kRecBytes));
+          r_buffer(p.vfix + vr0 * kRecBytes, r_range((p.v_nrec - vr0) * kRecBytes));
       for (int c0 = 0; c0 < nstep; c0 += 64) {
         const int n = min(nstep - c0, 64);
         const int lastc = n - 1;

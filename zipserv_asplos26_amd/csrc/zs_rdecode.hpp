@@ -247,6 +247,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t r_buffer(const void* base, uin
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufWord3);
 }
 
+// Range of a buffer resource over `bytes` bytes (> 0), saturated to the
+// 32-bit field: every offset a kernel passes through a resource is below
+// 2^32, so a saturated range still covers all of them, where a truncated one
+// (bytes mod 2^32) would turn in-bounds reads past it into zeros.
+__device__ __forceinline__ uint32_t r_range(int64_t bytes) {
+  return bytes >= (int64_t)UINT32_MAX ? UINT32_MAX : (uint32_t)bytes;
+}
+
 // Fixed part of record `rec` (no dependency on the outlier offsets).
 __device__ __forceinline__ void r_issue_fixed(const uint8_t* fixed, int64_t rec, RStage& s) {
   const uint32_t l = (uint32_t)lane_id();
