@@ -45,3 +45,15 @@ def test_size_queries():
     assert L.zs_compressed_bytes(4096, 4096, 100, 10) == 100 + 20 + 24 * mk // 64 + 8 * mk // 1024 + 8 * (mk // 4096 + 1)
     assert L.zs_version().startswith(b"zipserv")
     assert L.zs_status_string(-1) == b"invalid argument"
+
+
+def test_retiled_mm_refuses_k_past_row_blocks():
+    # X of N*K*2 > 2^31 bytes runs as row blocks of X; with K > 2^26 not even
+    # a 16-row block fits 2^31 bytes, which must be refused up front
+    # (ZS_E_OVERFLOW) rather than split again.  Fake, aligned pointers: the
+    # call returns during argument checks, before touching memory or a GPU.
+    L = zs.lib()
+    fake = 1 << 20
+    K = (1 << 26) + 64
+    assert L.zs_retiled_mm(None, fake, fake, fake, 120, fake, fake, 64, 16, K, None, 1) == \
+        _lib.ZS_E_OVERFLOW

@@ -119,3 +119,90 @@ def test_container_golden_image():
     image = np.fromfile(os.path.join(here, "container_v1.zsc"), np.uint8)
     _same(ct.from_bytes(image), zs.compress_host(matrix))
     np.testing.assert_array_equal(ct.to_bytes(zs.compress_host(matrix), "golden"), image)
+
+
+def _reseal(b):
+    """Recompute every stream CRC and the header CRC of a container image, so
+    a planted change passes the CRC checks and only the offset checks remain."""
+    b = b.copy()
+    n = int(b[20:24].view(np.uint32)[0])
+    off = 256
+    for i in range(n):
+        size = int(b[128 + 16 * i: 136 + 16 * i].view(np.uint64)[0])
+        crc = _crc(b[off: off + size].tobytes()) if size else 0
+        b[136 + 16 * i: 140 + 16 * i] = np.array([crc], np.uint32).view(np.uint8)
+        off += (size + 63) // 64 * 64
+    b[52:56] = 0
+    b[52:56] = np.array([_crc(b[:256].tobytes())], np.uint32).view(np.uint8)
+    return b
+
+
+def _stream_at(b, i):
+    off = 256
+    for j in range(i):
+        off += (int(b[128 + 16 * j: 136 + 16 * j].view(np.uint64)[0]) + 63) // 64 * 64
+    return off
+
+
+def _retiled_host(seed=6, shape=(128, 192), frac=0.05):
+    import oracle as zo
+    rng = np.random.default_rng(seed)
+    W = weights_bf16(rng, shape, outlier_frac=frac)
+    r = zo.compress_retiled(W, zo.analyze_gpu(W)[0] - 1)
+    return zs.ZipservRetiled(r.fixed, r.exps, r.eoff, r.rows, r.cols, r.rows, r.cols,
+                             r.start_exp, r.exps.size, r.compressed_bytes())
+
+
+def test_container_reseal_keeps_good_images():
+    # the CRC rewrite alone changes nothing: a resealed good image still loads
+    h = _host_matrix(7)
+    _same(ct.from_bytes(_reseal(ct.to_bytes(h))), h)
+    b = ct.to_bytes(_retiled_host())
+    np.testing.assert_array_equal(_reseal(b), b)
+    d, _, streams, _ = ct._parse(b)
+    assert d.layout == zs._lib.ZS_CONTAINER_RETILED and len(streams) == 3
+
+
+@pytest.mark.parametrize("plant", ["eoff0", "swap", "over1024", "code"])
+def test_container_rejects_crc_valid_bad_retiled_offsets(plant):
+    # a CRC-valid image whose outlier offsets disagree with the record codes
+    # would steer the decoders past the exponent stream: rejected on load
+    r = _retiled_host()
+    b = ct.to_bytes(r)
+    fx, eo = _stream_at(b, 0), _stream_at(b, 2)
+    eoff = b[eo: eo + 4 * r.eoff.size].view(np.int32)
+    bad = b.copy()
+    beoff = bad[eo: eo + 4 * r.eoff.size].view(np.int32)
+    if plant == "eoff0":
+        beoff[:] = eoff + 1                      # not starting at 0 (last offset moved too)
+    elif plant == "swap":
+        i = int(np.argmax(np.diff(eoff) > 0))    # a record with outliers
+        beoff[i + 1] = eoff[i]                   # its bytes handed to the next record
+    elif plant == "over1024":
+        beoff[1:] = eoff[1:] + 2000              # a record with 2000 "outliers"
+    else:
+        # one in-window code turned into an outlier code, offsets untouched
+        p32 = bad[fx + 1024: fx + 1028].view(np.uint32)
+        codes = int(p32[0])
+        k = next(i for i in range(8) if (codes >> (3 * i)) & 7)
+        p32[0] = codes & ~(7 << (3 * k))
+    with pytest.raises(zs.ZipServError):
+        ct.from_bytes(_reseal(bad), device="cpu")
+
+
+@pytest.mark.parametrize("plant", ["global", "median", "pad"])
+def test_container_rejects_crc_valid_bad_canonical_offsets(plant):
+    h = _host_matrix(8, (128, 192), 0.05)
+    b = ct.to_bytes(h)
+    bad = b.copy()
+    if plant == "global":
+        tog = bad[_stream_at(b, 6): _stream_at(b, 6) + 4 * h.tile_offsets_global.size].view(np.int32)
+        tog[2] += 16                              # GT 1 starts 16 SM bytes late
+    elif plant == "median":
+        tom = bad[_stream_at(b, 5): _stream_at(b, 5) + 4 * h.tile_offsets_median.size].view(np.int32)
+        tom[2] += 1                               # median 1 of GT 0 off by one
+    else:
+        tog = bad[_stream_at(b, 6): _stream_at(b, 6) + 4 * h.tile_offsets_global.size].view(np.int32)
+        tog[2:] += 1                              # padding no longer a multiple of 16
+    with pytest.raises(zs.ZipServError):
+        ct.from_bytes(_reseal(bad))

@@ -37,11 +37,13 @@ def test_three_encoders_agree(shape, frac, seed):
     rng = np.random.default_rng(seed)
     W = weights_bf16(rng, shape, outlier_frac=frac)
     e = [zo.compress(W, variant=v) for v in ("plain", "lut", "sse")]
+    # the multi-threaded sse encoder (CPU baseline on all cores) as well
+    e.append(zo.compress(W, variant="sse_mt", threads=3))
     for f in FIELDS:
-        np.testing.assert_array_equal(getattr(e[0], f), getattr(e[1], f), err_msg=f)
-        np.testing.assert_array_equal(getattr(e[0], f), getattr(e[2], f), err_msg=f)
-    assert e[0].max_high_freq_count == e[1].max_high_freq_count == e[2].max_high_freq_count
-    assert e[0].max_full_count == e[1].max_full_count == e[2].max_full_count
+        for i in (1, 2, 3):
+            np.testing.assert_array_equal(getattr(e[0], f), getattr(e[i], f), err_msg=f)
+    assert len({x.max_high_freq_count for x in e}) == 1
+    assert len({x.max_full_count for x in e}) == 1
 
 
 def test_uniform_ones_known_answer():

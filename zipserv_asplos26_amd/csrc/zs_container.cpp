@@ -113,19 +113,63 @@ int check_desc(const zs_container_desc_t* d) {
   return ZS_OK;
 }
 
-// The totals recorded in the last offsets must equal the free streams' sizes.
-int check_totals(const zs_container_desc_t* d, const uint8_t* const* s) {
+// Every offset the kernels follow must agree with the bit-planes / codes it
+// indexes, or a decoder would read past its streams: the last offsets equal
+// the free streams' sizes, and
+//  * canonical: tile_offsets_global starts at (0, 0) and steps by each global
+//    tile's in-window / outlier counts (from its bitmaps) padded to 16 / 8;
+//    tile_offsets_median holds the unpadded counts before each median tile;
+//  * re-tiled: eoff starts at 0 and steps by each record's outlier count
+//    (the elements whose 3-bit code is 0).
+int check_offsets(const zs_container_desc_t* d, const uint8_t* const* s) {
   if (d->layout == ZS_CONTAINER_CANONICAL) {
     const int64_t ngt = (int64_t)d->rows * d->cols / 4096;
-    int32_t last[2];
-    std::memcpy(last, s[6] + 8 * ngt, 8);
-    if (last[0] != d->stream_bytes[0] || 2 * (int64_t)last[1] != d->stream_bytes[1])
-      return ZS_E_INVAL;
+    const uint8_t* bm[3] = {s[2], s[3], s[4]};
+    int64_t hf_at = 0, fu_at = 0;
+    for (int64_t g = 0; g <= ngt; ++g) {
+      int32_t tog[2];
+      std::memcpy(tog, s[6] + 8 * g, 8);
+      if (tog[0] != hf_at || tog[1] != fu_at) return ZS_E_INVAL;
+      if (g == ngt) break;
+      int32_t before = 0;
+      for (int m = 0; m < 4; ++m) {
+        int32_t tom[2];
+        std::memcpy(tom, s[5] + 8 * (4 * g + m), 8);
+        if (tom[0] != before || tom[1] != 1024 * m - before) return ZS_E_INVAL;
+        for (int t = 0; t < 16; ++t) {
+          const int64_t tile = 64 * g + 16 * m + t;
+          uint64_t b[3];
+          for (int k = 0; k < 3; ++k) std::memcpy(&b[k], bm[k] + 8 * tile, 8);
+          before += __builtin_popcountll(b[0] | b[1] | b[2]);
+        }
+      }
+      hf_at += (before + 15) & ~15;
+      fu_at += (4096 - before + 7) & ~7;
+      if (hf_at > INT32_MAX || fu_at > INT32_MAX) return ZS_E_INVAL;
+    }
+    if (hf_at != d->stream_bytes[0] || 2 * fu_at != d->stream_bytes[1]) return ZS_E_INVAL;
   } else {
     const int64_t nrec = (int64_t)d->rows * d->cols / 1024;
-    int32_t last;
-    std::memcpy(&last, s[2] + 4 * nrec, 4);
-    if (last != d->stream_bytes[1]) return ZS_E_INVAL;
+    int64_t at = 0;
+    for (int64_t r = 0; r <= nrec; ++r) {
+      int32_t e;
+      std::memcpy(&e, s[2] + 4 * r, 4);
+      if (e != at) return ZS_E_INVAL;
+      if (r == nrec) break;
+      const uint8_t* rec = s[0] + r * 1408;
+      int n = 0;
+      for (int l = 0; l < 64; ++l) {
+        uint32_t p32;
+        uint16_t p16;
+        std::memcpy(&p32, rec + 1024 + 4 * l, 4);
+        std::memcpy(&p16, rec + 1280 + 2 * l, 2);
+        const uint64_t codes = (uint64_t)p32 | ((uint64_t)p16 << 32);  // 16 codes x 3 bits
+        for (int i = 0; i < 16; ++i) n += ((codes >> (3 * i)) & 7u) == 0;
+      }
+      at += n;
+      if (at > INT32_MAX) return ZS_E_INVAL;
+    }
+    if (at != d->stream_bytes[1]) return ZS_E_INVAL;
   }
   return ZS_OK;
 }
@@ -156,7 +200,7 @@ int zs_container_write(const zs_container_desc_t* d, const char* name,
     if (!streams[i] && d->stream_bytes[i] > 0) return ZS_E_INVAL;
   const uint8_t* s[kMaxStreams];
   for (int i = 0; i < d->num_streams; ++i) s[i] = static_cast<const uint8_t*>(streams[i]);
-  if (check_totals(d, s) != ZS_OK) return ZS_E_INVAL;
+  if (check_offsets(d, s) != ZS_OK) return ZS_E_INVAL;
   uint8_t* out = static_cast<uint8_t*>(dst);
   uint8_t* h = out;
   std::memset(h, 0, kHeader);
@@ -226,7 +270,7 @@ int zs_container_parse(const void* src, int64_t src_bytes, zs_container_desc_t* 
     if (stream_offsets) stream_offsets[i] = off;
     off += pad64(t.stream_bytes[i]);
   }
-  if (check_totals(&t, s) != ZS_OK) return ZS_E_INVAL;
+  if (check_offsets(&t, s) != ZS_OK) return ZS_E_INVAL;
   *d = t;
   if (name_out) {
     std::memcpy(name_out, h + 64, 63);

@@ -1352,7 +1352,9 @@ static int retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exp
   if ((int64_t)N * K * 2 > INT32_MAX) {
     // The kernels address X with 32-bit byte offsets: run row blocks of X
     // and Y that stay below 2^31 bytes, one after another on the stream.
-    const int rows = std::max(16, (int)(INT32_MAX / (2LL * K)) / 16 * 16);
+    const int rows = (int)(INT32_MAX / (2LL * K)) / 16 * 16;
+    // a row block of fewer than 16 rows would not fit either (K > 2^26)
+    if (rows < 16) return ZS_E_OVERFLOW;
     for (int n0 = 0; n0 < N; n0 += rows) {
       const int st_ = retiled_mm(stream, d_fixed, d_exps, d_eoff, start_exp,
                                  B + (int64_t)n0 * K, C + (int64_t)n0 * M, M,
