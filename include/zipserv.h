@@ -232,6 +232,21 @@ int zs_retiled_mm_fused(void* stream, const uint8_t* d_fixed, const uint8_t* d_e
                         const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B, uint16_t* C,
                         int M, int N, int K, uint16_t* Reduction_Workspace, int Split_K,
                         int32_t* d_counters);
+/* zs_retiled_mm_fused that allocates nothing and takes no workspace: no
+ * counterpart in the reference; it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The split-K partial slabs and arrival counters live in a
+ * static device array of the library, 32 MiB of partials + 64 Ki counters,
+ * one copy per GPU held until the process ends: Split_K > 1 requires
+ * Split_K * M * N * 2 <= 32 MiB and zs_retiled_mm_counters(M, N) <= 65536,
+ * else ZS_E_OVERFLOW before any launch.  The first call on a device looks
+ * the array up and clears its counters on `stream` (make it outside graph
+ * capture); every completed call leaves them zero.  All calls on one GPU
+ * share the array: calls that overlap in time on one GPU (other streams,
+ * other threads) race and must not be issued. */
+int zs_retiled_mm_fused_noalloc(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
+                                const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B,
+                                uint16_t* C, int M, int N, int K, int Split_K);
 
 /* ---------------------------------------------------------------------- */
 /* Decode attention over a compressed KV cache                              */

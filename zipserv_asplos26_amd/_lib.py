@@ -69,6 +69,8 @@ SIGNATURES = {
     "zs_retiled_mm_counters": (C.c_int64, [C.c_int, C.c_int]),
     "zs_retiled_mm_fused": (C.c_int, [_p, _p, _p, _p, C.c_uint8, _p, _p, C.c_int, C.c_int,
                                       C.c_int, _p, C.c_int, _p]),
+    "zs_retiled_mm_fused_noalloc": (C.c_int, [_p, _p, _p, _p, C.c_uint8, _p, _p, C.c_int,
+                                              C.c_int, C.c_int, C.c_int]),
     "zs_decode_attention": (
         C.c_int, [_p, _p, _p, _p, _p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                   _p, _p, _p, C.c_size_t, C.c_int]),

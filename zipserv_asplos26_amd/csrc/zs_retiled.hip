@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "../../include/zipserv.h"
 #include "zs_device.hpp"
@@ -1440,4 +1441,68 @@ extern "C" int zs_retiled_mm_fused(void* stream, const uint8_t* d_fixed, const u
     return ZS_E_INVAL;
   return retiled_mm(stream, d_fixed, d_exps, d_eoff, start_exp, B, C, M, N, K, ws, split_k,
                     counters);
+}
+
+// ---------------------------------------------------------------------------
+// zs_retiled_mm_fused without caller buffers: the split-K partial slabs and
+// arrival counters live in `scratch`, a file-scope device array (one copy per
+// GPU, at its own address, held until the process ends).  Host code reaches
+// it only through the address hipGetSymbolAddress returns for the current
+// device (the array's name in host code is not a device address).
+// ---------------------------------------------------------------------------
+namespace zs {
+constexpr int64_t kScratchSlabBytes = 32ll << 20;  // bf16 partials [S][N][M]
+constexpr int64_t kScratchCounters = 1 << 16;      // int32 arrival counters
+constexpr int64_t kScratchBytes = kScratchSlabBytes + 4 * kScratchCounters;
+constexpr int kScratchMaxDevices = 64;
+
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+__global__ void zero_i32_kernel(int32_t* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// Per-device address of `scratch`, looked up (and its counters cleared on
+// `st`) by the first call on that device.  0 / a hipError_t status.
+static int scratch_of(hipStream_t st, uint8_t** out) {
+  static std::mutex mu;
+  static uint8_t* addr[kScratchMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kScratchMaxDevices) return ZS_E_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    int32_t* cnt = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(p) + kScratchSlabBytes);
+    hipLaunchKernelGGL(zero_i32_kernel, dim3((unsigned)(kScratchCounters / 256)), dim3(256), 0,
+                       st, cnt, kScratchCounters);
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    addr[dev] = static_cast<uint8_t*>(p);
+  }
+  *out = addr[dev];
+  return ZS_OK;
+}
+}  // namespace zs
+
+extern "C" int zs_retiled_mm_fused_noalloc(void* stream, const uint8_t* d_fixed,
+                                           const uint8_t* d_exps, const int32_t* d_eoff,
+                                           uint8_t start_exp, const uint16_t* B, uint16_t* C,
+                                           int M, int N, int K, int split_k) {
+  if (M <= 0 || N <= 0 || split_k < 1) return ZS_E_INVAL;
+  if (split_k > 1) {
+    // the partial slabs [split_k][N][M] and the tile counters must fit
+    if ((int64_t)split_k * M * N * 2 > kScratchSlabBytes) return ZS_E_OVERFLOW;
+    if (zs_retiled_mm_counters(M, N) > kScratchCounters) return ZS_E_OVERFLOW;
+  }
+  uint8_t* base = nullptr;
+  const int st = scratch_of((hipStream_t)stream, &base);
+  if (st != ZS_OK) return st;
+  uint16_t* ws = split_k > 1 ? reinterpret_cast<uint16_t*>(base) : nullptr;
+  int32_t* cnt = split_k > 1 ? reinterpret_cast<int32_t*>(base + kScratchSlabBytes) : nullptr;
+  return retiled_mm(stream, d_fixed, d_exps, d_eoff, start_exp, B, C, M, N, K, ws, split_k, cnt);
 }
