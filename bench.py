@@ -34,6 +34,8 @@ NS = [1, 8, 16, 32, 64, 128]
 SPLITS = [1, 2, 4]
 HBM_PEAK_GBS = 8000.0
 CALIB_BYTES = 256 << 20
+COLD_BYTES = 1 << 30      # compressed bytes rotated per (shape, N) timing
+COLD_MIN_COPIES = 16
 
 
 def parse():
@@ -45,13 +47,17 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
-    ap.add_argument("--reps", type=int, default=20, help="graph replays per (shape, N) in the per-kernel timing")
     ap.add_argument("--splits", default="1,2,4",
                     help="split-K values tried per (shape, N); the fastest is used")
     ap.add_argument("--no-c3", action="store_true", help="skip the 80-layer Llama-3.1-70B sweep")
     ap.add_argument("--no-attention", action="store_true", help="skip the decode-attention sweep")
     ap.add_argument("--no-kv", action="store_true", help="skip the KV-cache codec sweep")
     return ap.parse_args()
+
+
+def progress(msg):
+    """One progress line on stderr (the JSON result alone goes to stdout)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def capture(torch, stream, fn):
@@ -116,6 +122,8 @@ def bench_c3(torch, zs, stream, gen, dev):
     comp, enc_t, enc_bytes = [], 0.0, 0
     dense = []
     for li in range(C3_LAYERS):
+        if li % 20 == 0:
+            progress(f"config 3: compressing layer {li} of {C3_LAYERS}")
         layer = []
         for name, M, K in C3_SHAPES:
             w = (torch.randn(M, K, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
@@ -134,6 +142,7 @@ def bench_c3(torch, zs, stream, gen, dev):
     dense_bytes = C3_LAYERS * sum(2 * M * K for _, M, K in C3_SHAPES)
     rows = []
     for N in C3_NS:
+        progress(f"config 3: N={N}")
         xs = {K: torch.randn(N, K, device=dev, generator=gen).to(torch.bfloat16)
               for K in {k for _, _, k in C3_SHAPES}}
         ys = {M: torch.empty(N, M, device=dev, dtype=torch.bfloat16) for M in {m for _, m, _ in C3_SHAPES}}
@@ -196,12 +205,17 @@ def bench_attention(torch, zs, stream, gen, dev):
     import zipserv_asplos26_amd.attention as za
     rows = []
     for B, T in ATTN_CASES:
+        progress(f"config 5: attention B={B} T={T}")
         k = kv_tensor(torch, gen, dev, B, T)
         v = kv_tensor(torch, gen, dev, B, T)
         q = torch.randn(B, 1, 64, 128, device=dev, generator=gen).to(torch.bfloat16)
         canonical = k.numel() <= 2**31 - 1
         ck, cv = (za.compress_kv(k), za.compress_kv(v)) if canonical else (None, None)
         rk, rv = za.compress_kv(k, retiled=True), za.compress_kv(v, retiled=True)
+        # staged comparator (bench_zipserv_decode_attention.py:752-796): token-major
+        # compressed caches decompressed into a dense workspace, then the dense kernel
+        sk_, sv_ = (za.compress_kv(k, layout="token_major", retiled=True),
+                    za.compress_kv(v, layout="token_major", retiled=True))
         torch.cuda.synchronize()
         reps = 10
         tc = timed(torch, stream, [capture(torch, stream, lambda: [
@@ -211,19 +225,32 @@ def bench_attention(torch, zs, stream, gen, dev):
             za.flash_attn_with_kvcache_zipserv(q, rk, rv, 8, T) for _ in range(reps)])], 3, 1) / (3 * reps)
         td = timed(torch, stream, [capture(torch, stream, lambda: [
             za.flash_attn_with_kvcache_dense(q, k, v) for _ in range(reps)])], 3, 1) / (3 * reps)
+        ts = timed(torch, stream, [capture(torch, stream, lambda: [
+            za.flash_attn_with_kvcache_zipserv(q, sk_, sv_, 8, T) for _ in range(reps)])], 3, 1) / (
+            3 * reps)
         comp = rk.compressed_bytes + rv.compressed_bytes
         dense = 2 * k.numel() * 2
         rows.append({"B": B, "T": T, "zip_us": round(tz * 1e6, 2),
                      "canonical_us": round(tc * 1e6, 2) if tc else None,
                      "dense_us": round(td * 1e6, 2),
-                     "speedup": round(td / tz, 3), "ratio": round(dense / comp, 4),
+                     "staged_us": round(ts * 1e6, 2),
+                     "speedup": round(td / tz, 3), "speedup_vs_staged": round(ts / tz, 3),
+                     "ratio": round(dense / comp, 4),
                      "comp_TBps": round((comp + 2 * 2 * B * 64 * 128) / tz / 1e12, 3),
                      "dense_TBps": round((dense + 2 * 2 * B * 64 * 128) / td / 1e12, 3)})
-        del k, v, q, ck, cv, rk, rv
+        del k, v, q, ck, cv, rk, rv, sk_, sv_
         torch.cuda.empty_cache()
     return {"heads": 64, "heads_k": 8, "head_dim": 128, "kv": "N(0,1) x lognormal(0,1) per channel",
-            "note": "reps captured in one HIP graph; time per call; zip_us = re-tiled KV, "
-                    "canonical_us = canonical TCA-TBE KV", "cases": rows}
+            "note": "reps captured in one HIP graph; time per call; zip_us = fused over re-tiled "
+                    "head-major KV, canonical_us = fused over canonical TCA-TBE KV, staged_us = "
+                    "token-major re-tiled KV decompressed into a workspace then the dense kernel, "
+                    "dense_us = the dense kernel over bf16 KV", "cases": rows}
+
+
+# Benchmark config 4 (B 1-32, 8 KV heads, T 1k-128k, D 128); (32, 128k) is
+# 2^32 elements per tensor.
+KV_CASES = [(1, 1024), (1, 32768), (1, 131072), (8, 32768), (8, 131072), (32, 16384),
+            (32, 131072)]
 
 
 def bench_kv(torch, zs, dev, gen):
@@ -252,27 +279,37 @@ def bench_kv(torch, zs, dev, gen):
         return time.perf_counter() - t0, res
 
     rows = []
-    for B, T in [(1, 32768), (8, 32768), (32, 16384)]:
+    for B, T in KV_CASES:
+        progress(f"config 4: KV codec B={B} T={T}")
         x = kv_tensor(torch, gen, dev, B, T)
         mat, _, _ = za.pad_batched_kv_prefix_by_kv_head(x)
         mat = mat.contiguous()
+        del x
         nbytes = mat.numel() * 2
         out = torch.empty_like(mat)
-        tc, c = host_clock(lambda: zs.compress(mat))
+        # canonical streams hold int32 offsets: caches past 2^31 elements
+        # are re-tiled only
+        canonical = mat.numel() <= 2**31 - 1 - 16 * (mat.numel() // 4096)
+        row = {"B": B, "T": T, "elements": mat.numel()}
+        if canonical:
+            tc, c = host_clock(lambda: zs.compress(mat))
+            td = clock(lambda: zs.decompress_zipserv_into(
+                out, *c.streams(), c.rows, c.cols, c.max_high_freq_count, c.max_full_count,
+                c.start_exp))
+            row.update({"ratio": round(nbytes / c.compressed_bytes, 4),
+                        "compress_GBps": round(nbytes / tc / 1e9, 2),
+                        "decompress_GBps": round(nbytes / td / 1e9, 2),
+                        "bit_exact": bool(torch.equal(out.view(torch.int16), mat.view(torch.int16)))})
+            del c
         tr, r = host_clock(lambda: zs.compress_retiled(mat))
-        td = clock(lambda: zs.decompress_zipserv_into(
-            out, *c.streams(), c.rows, c.cols, c.max_high_freq_count, c.max_full_count, c.start_exp))
-        exact = bool(torch.equal(out.view(torch.int16), mat.view(torch.int16)))
         tdr = clock(lambda: zs.decompress_retiled(r, out))
-        exact_r = bool(torch.equal(out.view(torch.int16), mat.view(torch.int16)))
-        rows.append({"B": B, "T": T, "ratio": round(nbytes / c.compressed_bytes, 4),
-                     "ratio_retiled": round(nbytes / r.compressed_bytes, 4),
-                     "compress_GBps": round(nbytes / tc / 1e9, 2),
-                     "compress_retiled_GBps": round(nbytes / tr / 1e9, 2),
-                     "decompress_GBps": round(nbytes / td / 1e9, 2),
-                     "decompress_retiled_GBps": round(nbytes / tdr / 1e9, 2),
-                     "bit_exact": exact, "bit_exact_retiled": exact_r})
-        del x, mat, c, r, out
+        row.update({"ratio_retiled": round(nbytes / r.compressed_bytes, 4),
+                    "compress_retiled_GBps": round(nbytes / tr / 1e9, 2),
+                    "decompress_retiled_GBps": round(nbytes / tdr / 1e9, 2),
+                    "bit_exact_retiled": bool(torch.equal(out.view(torch.int16),
+                                                          mat.view(torch.int16)))})
+        rows.append(row)
+        del mat, r, out
         torch.cuda.empty_cache()
     return {"layout": "by_kv_head",
             "compress_timing": "host clock around one call incl. its size sync",
@@ -316,6 +353,22 @@ def traffic_from_profile(kernel):
                 return {"bytes_per_launch": int(line.rsplit(":", 1)[1].strip()),
                         "source": os.path.relpath(path, ROOT)}
     return None
+
+
+def clone_retiled(r):
+    """A second resident copy of a re-tiled matrix (distinct addresses)."""
+    import dataclasses
+    return dataclasses.replace(r, fixed=r.fixed.clone(), exps=r.exps.clone(), eoff=r.eoff.clone())
+
+
+def clone_canonical(c):
+    """A second resident copy of canonical device streams."""
+    import dataclasses
+    return dataclasses.replace(
+        c, sign_mantissa=c.sign_mantissa.clone(), compressed_full=c.compressed_full.clone(),
+        bitmap1=c.bitmap1.clone(), bitmap2=c.bitmap2.clone(), bitmap3=c.bitmap3.clone(),
+        tile_offsets_median=c.tile_offsets_median.clone(),
+        tile_offsets_global=c.tile_offsets_global.clone())
 
 
 def make_layer(torch, zs, gen, dev):
@@ -449,6 +502,7 @@ def main():
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
 
+    progress("config 2: compressing layers")
     t0 = time.perf_counter()
     layers = [make_layer(torch, zs, gen, dev) for _ in range(args.layers)]
     torch.cuda.synchronize()
@@ -485,8 +539,23 @@ def main():
 
     stream = torch.cuda.Stream()
 
+    # HBM-cold copies per shape (see the per-launch timing below): the
+    # layers' own matrices plus clones, >= COLD_MIN_COPIES and >= COLD_BYTES
+    # of compressed weights, so one launch's weights were last touched more
+    # than 1 GiB of traffic earlier (past the 256 MB Infinity Cache).
+    colds = []
+    for si, (name, M, K) in enumerate(SHAPES):
+        comp = layers[0][si][5].compressed_bytes
+        nc = max(COLD_MIN_COPIES, -(-COLD_BYTES // comp))
+        cold = [L[si] for L in layers]
+        while len(cold) < nc:
+            _, _, _, w0, c0, r0 = layers[len(cold) % len(layers)][si]
+            cold.append((name, M, K, w0.clone(), clone_canonical(c0), clone_retiled(r0)))
+        colds.append(cold)
+    torch.cuda.synchronize()
+
     # Split-K per (shape, N): the reference sweeps Split_K in {1, 2, 4}
-    # (benchmark config 2); the fastest on this GPU is kept for the step.
+    # (benchmark config 2); the fastest on this GPU (cold weights) is kept.
     splits, wss = {}, {}
     for si, (name, M, K) in enumerate(SHAPES):
         for N in NS:
@@ -494,9 +563,9 @@ def main():
             for sk in [int(v) for v in args.splits.split(",")]:
                 ws = zs.codec.splitk_workspace(layers[0][si][5], N, sk)
                 def srun(si=si, N=N, M=M, K=K, sk=sk, ws=ws):
-                    for r in range(args.reps):
-                        zs.zipgemm(layers[r % len(layers)][si][5], xs[(N, K)], split_k=sk,
-                                   out=outs[(N, M)], workspace=ws)
+                    for cp in colds[si]:
+                        zs.zipgemm(cp[5], xs[(N, K)], split_k=sk, out=outs[(N, M)],
+                                   workspace=ws)
                 t = timed(torch, stream, [capture(torch, stream, srun)], 2, 1)
                 if best is None or t < best[0]:
                     best = (t, sk, ws)
@@ -529,18 +598,25 @@ def main():
         t_dense = timed(torch, stream, dg, args.steps, args.warmup)
         result_dense = step_bytes * args.steps / t_dense / 1e12
 
-    # Per-(shape, N) kernel timing: `reps` launches in one graph, cycling
-    # through the resident layers, timed with events on the replay stream
-    # around each of 9 replays; zip_us is the median replay, p10/p90 beside it.
+    # Per-(shape, N) kernel timing, HBM-cold: one graph launches the shape
+    # once on each of `nc` distinct resident copies (the layers' own plus
+    # clones, >= 16 and >= COLD_BYTES of compressed weights, so a launch's
+    # weights were last touched > 1 GiB of traffic ago, past the 256 MB
+    # Infinity Cache), timed with events on the replay stream around each of
+    # 9 replays; zip_us is the median replay / nc, p10/p90 beside it.  The
+    # dense and canonical comparators rotate their own copies the same way.
     per = []
     sum_alg_bytes, sum_kernel_s = 0.0, 0.0
     for si, (name, M, K) in enumerate(SHAPES):
+        progress(f"config 2: per-launch timing {name} {M}x{K}")
+        cold = colds[si]
+        nc = len(cold)
         for N in NS:
             def zrun(si=si, N=N, M=M, K=K):
-                for r in range(args.reps):
-                    zs.zipgemm(layers[r % len(layers)][si][5], xs[(N, K)], split_k=splits[(si, N)],
+                for cp in cold:
+                    zs.zipgemm(cp[5], xs[(N, K)], split_k=splits[(si, N)],
                                out=outs[(N, M)], workspace=wss[(si, N)])
-            dz = [t / args.reps for t in timed_dist(torch, stream, capture(torch, stream, zrun), 9, 1)]
+            dz = [t / nc for t in timed_dist(torch, stream, capture(torch, stream, zrun), 9, 1)]
             tz = pct(dz, 50)
             comp = layers[0][si][5].compressed_bytes
             sk = splits[(si, N)]
@@ -548,11 +624,11 @@ def main():
             sum_alg_bytes += alg
             sum_kernel_s += tz
             def crun(si=si, N=N, M=M, K=K):
-                for r in range(args.reps):
-                    zs.zipgemm(layers[r % len(layers)][si][4], xs[(N, K)], out=outs[(N, M)])
-            tc = timed(torch, stream, [capture(torch, stream, crun)], 3, 1) / (3 * args.reps)
+                for cp in cold:
+                    zs.zipgemm(cp[4], xs[(N, K)], out=outs[(N, M)])
+            tc = timed(torch, stream, [capture(torch, stream, crun)], 3, 1) / (3 * nc)
             row = {"shape": name, "M": M, "K": K, "N": N, "kernel": kernel_name(N, M, sk),
-                   "split_k": sk,
+                   "split_k": sk, "cold_copies": nc,
                    "canonical_us": round(tc * 1e6, 3),
                    "zip_us": round(tz * 1e6, 3),
                    "zip_us_p10": round(pct(dz, 10) * 1e6, 3),
@@ -565,13 +641,15 @@ def main():
                    "mfma_frac": round(2 * M * N * K / tz / 2.5e15, 4)}
             if not args.no_dense:
                 def drun(si=si, N=N, M=M, K=K):
-                    for r in range(args.reps):
-                        torch.matmul(xs[(N, K)], layers[r % len(layers)][si][3].t(), out=outs[(N, M)])
-                td = pct([t / args.reps for t in
+                    for cp in cold:
+                        torch.matmul(xs[(N, K)], cp[3].t(), out=outs[(N, M)])
+                td = pct([t / nc for t in
                           timed_dist(torch, stream, capture(torch, stream, drun), 9, 1)], 50)
                 row["dense_us"] = round(td * 1e6, 2)
                 row["speedup"] = round(td / tz, 3)
             per.append(row)
+    del colds, cold
+    torch.cuda.empty_cache()
 
     ratio = sum(2 * M * K for _, M, K in SHAPES) / sum(r.compressed_bytes for *_, r in layers[0])
     ratio_canonical = (sum(2 * M * K for _, M, K in SHAPES)
@@ -641,6 +719,7 @@ def main():
         "setup_s": round(setup_s, 2),
     }
     if not args.no_cpu_baseline:
+        progress("CPU baseline (config 1)")
         out["cpu_baseline"] = cpu_baseline()
     del layers, xs, outs
     torch.cuda.empty_cache()
