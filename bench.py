@@ -52,7 +52,48 @@ def parse():
     ap.add_argument("--no-c3", action="store_true", help="skip the 80-layer Llama-3.1-70B sweep")
     ap.add_argument("--no-attention", action="store_true", help="skip the decode-attention sweep")
     ap.add_argument("--no-kv", action="store_true", help="skip the KV-cache codec sweep")
+    ap.add_argument("--eager", default=None, metavar="M,K,N,SPLIT[,ITERS]",
+                    help="profiling mode: only launch ZipGEMM of one shape eagerly ITERS times "
+                         "(default 32) over HBM-cold copies (for rocprofv3 counter runs, which "
+                         "see no graph replays), then print its mean time")
     return ap.parse_args()
+
+
+def eager_gemm(spec):
+    """--eager: one (M, K, N, split-K) ZipGEMM launched eagerly over rotated
+    cold copies of N(0, 0.02) bf16 weights (re-tiled layout), preceded by the
+    256 MiB negation bench.py uses to calibrate the HBM counters."""
+    import torch
+
+    import zipserv_asplos26_amd as zs
+    v = [int(x) for x in spec.split(",")]
+    M, K, N, sk = v[:4]
+    iters = v[4] if len(v) > 4 else 32
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    w = (torch.randn(M, K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    r = zs.compress_retiled(w, window="weights")
+    del w
+    copies = [r] + [clone_retiled(r) for _ in range(max(COLD_MIN_COPIES, -(-COLD_BYTES // r.compressed_bytes)) - 1)]
+    x = torch.randn(N, K, device=dev, generator=g).to(torch.bfloat16)
+    y = torch.empty(N, M, device=dev, dtype=torch.bfloat16)
+    ws = zs.codec.splitk_workspace(r, N, sk)
+    ca = torch.empty(CALIB_BYTES // 2, device=dev, dtype=torch.bfloat16).fill_(1.0)
+    torch.neg(ca, out=torch.empty_like(ca))
+    for c in copies[:4]:
+        zs.zipgemm(c, x, split_k=sk, out=y, workspace=ws)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(iters):
+        zs.zipgemm(copies[i % len(copies)], x, split_k=sk, out=y, workspace=ws)
+    e.record()
+    torch.cuda.synchronize()
+    t = s.elapsed_time(e) / 1e3 / iters
+    print(json.dumps({"eager": {"M": M, "K": K, "N": N, "split_k": sk, "iters": iters,
+                                "copies": len(copies), "us": round(t * 1e6, 3),
+                                "comp_TBps": round(r.compressed_bytes / t / 1e12, 3)}}))
 
 
 def progress(msg):
@@ -499,6 +540,9 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.eager:
+        eager_gemm(args.eager)
+        return
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
 

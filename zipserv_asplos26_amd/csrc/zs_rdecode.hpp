@@ -255,13 +255,21 @@ __device__ __forceinline__ uint32_t r_range(int64_t bytes) {
   return bytes >= (int64_t)UINT32_MAX ? UINT32_MAX : (uint32_t)bytes;
 }
 
+// Cache policy of the record and outlier-byte loads: non-temporal (the
+// gfx950 `nt` bit of the buffer instruction).  Every compressed byte is read
+// once per launch; a plain streaming read of HBM measured 6.25 TB/s on
+// MI355X against 7.0 TB/s with nt, and the re-tiled kernels run 0-7% faster
+// with it.  X, the decode table and the offsets keep the default policy
+// (they are re-read from L2).
+constexpr int kStreamPolicy = 2;
+
 // Fixed part of record `rec` (no dependency on the outlier offsets).
 __device__ __forceinline__ void r_issue_fixed(const uint8_t* fixed, int64_t rec, RStage& s) {
   const uint32_t l = (uint32_t)lane_id();
   const __amdgpu_buffer_rsrc_t r = r_buffer(fixed + rec * kRecBytes, kRecBytes);
-  s.r.sm = __builtin_amdgcn_raw_buffer_load_b128(r, 16u * l, 0, 0);
-  s.r.p32 = __builtin_amdgcn_raw_buffer_load_b32(r, kRecP32 + 4u * l, 0, 0);
-  s.r.p16 = __builtin_amdgcn_raw_buffer_load_b16(r, kRecP16 + 2u * l, 0, 0);
+  s.r.sm = __builtin_amdgcn_raw_buffer_load_b128(r, 16u * l, 0, kStreamPolicy);
+  s.r.p32 = __builtin_amdgcn_raw_buffer_load_b32(r, kRecP32 + 4u * l, 0, kStreamPolicy);
+  s.r.p16 = __builtin_amdgcn_raw_buffer_load_b16(r, kRecP16 + 2u * l, 0, kStreamPolicy);
 }
 
 // Outlier bytes [e0, e1) of a record, as dwords from e0 & ~3 (lane l: dword
@@ -275,7 +283,7 @@ __device__ __forceinline__ void r_issue_exps(const uint8_t* exps, int e0, int e1
   mt.rel = e0 - ea0;
   mt.nw = nw;
   s.ex = __builtin_amdgcn_raw_buffer_load_b32(r_buffer(exps + ea0, 4u * (uint32_t)nw), 4u * l, 0,
-                                              0);
+                                              kStreamPolicy);
 }
 
 __device__ __forceinline__ void r_issue(const uint8_t* fixed, const uint8_t* exps, int64_t rec,
@@ -295,9 +303,9 @@ __device__ __forceinline__ void r_issue(const uint8_t* fixed, const uint8_t* exp
 __device__ __forceinline__ void r_issue_fixed_r(__amdgpu_buffer_rsrc_t fixed_r, uint32_t soff,
                                                 RStage& s) {
   const uint32_t l = (uint32_t)lane_id();
-  s.r.sm = __builtin_amdgcn_raw_buffer_load_b128(fixed_r, 16u * l, soff, 0);
-  s.r.p32 = __builtin_amdgcn_raw_buffer_load_b32(fixed_r, kRecP32 + 4u * l, soff, 0);
-  s.r.p16 = __builtin_amdgcn_raw_buffer_load_b16(fixed_r, kRecP16 + 2u * l, soff, 0);
+  s.r.sm = __builtin_amdgcn_raw_buffer_load_b128(fixed_r, 16u * l, soff, kStreamPolicy);
+  s.r.p32 = __builtin_amdgcn_raw_buffer_load_b32(fixed_r, kRecP32 + 4u * l, soff, kStreamPolicy);
+  s.r.p16 = __builtin_amdgcn_raw_buffer_load_b16(fixed_r, kRecP16 + 2u * l, soff, kStreamPolicy);
 }
 
 // Stages all 64 dwords of a record's outlier fetch (the stage has room for

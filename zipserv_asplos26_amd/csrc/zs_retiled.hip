@@ -495,18 +495,77 @@ __device__ __forceinline__ void splitk_finish(const SplitFix& fx, const uint16_t
 // takes K tiles kb0+w, kb0+w+WAVES, ... of all F bands, so each X fragment
 // it loads feeds F records (X bytes per record / F).  Records are fetched D
 // tiles ahead into a register ring, their outlier bytes staged one tile
-// ahead, X one tile ahead.
+// ahead.
+//
+// X, two ways (XD):
+//  * XD == 0: each lane loads its two 16-byte MFMA B fragments one tile
+//    ahead (2 KB returned per tile whatever N is; rows past N read zeros);
+//  * XD > 0 (N <= 2 * XD, one column block): the wave loads just the tile's
+//    2*XD batch rows (XD dwords per lane, issued with the records of the same
+//    tile, D tiles ahead), writes them to its LDS X stage and reads the B
+//    fragments from there.  At N = 1 that is 256 bytes through the texture
+//    path per tile instead of 2 KB -- the texture address / data units are
+//    ~80% busy in this kernel (counters at 28672 x 8192, N = 1) -- and since
+//    vector-memory loads complete in issue order, an X load issued with the
+//    records no longer makes the MFMA wait for records issued after it.
+//    Same operands, same sums: results are bit-identical to XD == 0.
 // ---------------------------------------------------------------------------
-template <int F, int NB, int WAVES, int D>
+template <int F, int NB, int WAVES, int D, int XD>
 struct RGemmSmem {
-  static constexpr int kMain = (int)sizeof(RTables) + WAVES * D * F * kExpStage;
+  static constexpr int kXPitch = 144;                            // X stage row pitch
+  static constexpr int kXRows = 2 * XD;                          // rows one X load covers
+  static constexpr int kXStage = XD > 0 ? kXRows * kXPitch : 0;  // bytes per wave
+  static constexpr int kXAt = WAVES * D * F * kExpStage;
+  static constexpr int kTabAt = (kXAt + WAVES * kXStage + 15) / 16 * 16;
+  static constexpr int kMain = kTabAt + (int)sizeof(RTables);
   static constexpr int kRed = (WAVES - 1) * F * NB * 64 * 16;
   static constexpr int kBytes = kMain > kRed ? kMain : kRed;
 };
 
+// X tile of the staged-X path: lane l carries XD dwords, bytes 4*XD*l ..
+// of the 2*XD x 64 bf16 tile in row-major order.
+template <int XD>
+struct XFrag {
+  uint32_t d[XD > 0 ? XD : 1];
+};
+template <int XD>
+__device__ __forceinline__ void x_load(__amdgpu_buffer_rsrc_t xrs, uint32_t voff, uint32_t soff,
+                                       XFrag<XD>& x) {
+  if constexpr (XD == 1) {
+    x.d[0] = __builtin_amdgcn_raw_buffer_load_b32(xrs, voff, soff, 0);
+  } else if constexpr (XD == 2) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(xrs, voff, soff, 0);
+    x.d[0] = v[0];
+    x.d[1] = v[1];
+  } else {
+    static_assert(XD % 4 == 0, "X loads of 1, 2 or a multiple of 4 dwords");
+#pragma unroll
+    for (int q = 0; q < XD / 4; ++q) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, voff + 16u * q, soff, 0);
+      x.d[4 * q] = v[0];
+      x.d[4 * q + 1] = v[1];
+      x.d[4 * q + 2] = v[2];
+      x.d[4 * q + 3] = v[3];
+    }
+  }
+}
+template <int XD>
+__device__ __forceinline__ void x_stage(uint8_t* p, const XFrag<XD>& x) {
+  if constexpr (XD == 1) {
+    *reinterpret_cast<uint32_t*>(p) = x.d[0];
+  } else if constexpr (XD == 2) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(x.d[0], x.d[1]);
+  } else {
+#pragma unroll
+    for (int q = 0; q < XD / 4; ++q)
+      *reinterpret_cast<u32x4*>(p + 16 * q) =
+          u32x4{x.d[4 * q], x.d[4 * q + 1], x.d[4 * q + 2], x.d[4 * q + 3]};
+  }
+}
+
 // Launch bounds: one band per wave in 8-wave workgroups is held to 80 VGPRs
-// (6 waves per SIMD, three workgroups per CU) with its 4-deep record ring.
-template <int F, int NB, int WAVES, int D>
+// (6 waves per SIMD, three workgroups per CU).
+template <int F, int NB, int WAVES, int D, int XD>
 __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rgemm_kernel(const uint8_t* fixed,
                                                            const uint8_t* exps,
                                                            const int32_t* eoff, int start_exp,
@@ -516,8 +575,10 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
   // LDS: the waves' outlier stages first, then the decode table.  (With the
   // stages at a small base, a window's dword reads fold their offsets into
   // the instructions; the table reads take the large constant instead.)
-  __shared__ __attribute__((aligned(16))) uint8_t smem[RGemmSmem<F, NB, WAVES, D>::kBytes];
-  constexpr int kTabAt = WAVES * D * F * kExpStage;
+  using SM = RGemmSmem<F, NB, WAVES, D, XD>;
+  static_assert(XD == 0 || NB == 1, "the staged-X path covers one 16-column block");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[SM::kBytes];
+  constexpr int kTabAt = SM::kTabAt;
   static_assert(kTabAt % 16 == 0, "table alignment");
   RTables& T = *reinterpret_cast<RTables*>(smem + kTabAt);
   const RExp ex = r_exp(start_exp);
@@ -562,6 +623,18 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
     const int n = n0 + nb * 16 + (l & 15);
     xoff[nb] = n < N ? 2u * ((uint32_t)n * (uint32_t)K + 8u * (uint32_t)(l >> 4)) : 0x80000000u;
   }
+  // Staged X: this lane loads row xrow, bytes xcol.. of the tile (rows past N
+  // read zeros) and writes them to the wave's stage; it reads its B fragment
+  // at batch row l % 16, clamped into the stage (output columns past N are
+  // dropped).
+  const int xrow = (XD * l) >> 5, xcol = (4 * XD * l) & 127;
+  const uint32_t xloff = n0 + xrow < N
+                             ? 2u * (uint32_t)(n0 + xrow) * (uint32_t)K + (uint32_t)xcol
+                             : 0x80000000u;
+  uint8_t* xst = smem + SM::kXAt + w * SM::kXStage;
+  uint8_t* xst_w = xst + xrow * SM::kXPitch + xcol;
+  const uint8_t* xst_r =
+      xst + min(l & 15, (XD > 0 ? SM::kXRows : 1) - 1) * SM::kXPitch + 16 * (l >> 4);
   f32x4 acc[F * NB];
 #pragma unroll
   for (int i = 0; i < F * NB; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -570,7 +643,8 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
   // offsets of tile c0 + i, clamped to the chunk, per band).
   RStage R[D][F];
   RMeta MT[D][F];
-  bf16x8 xc[2][NB], xn[2][NB];
+  bf16x8 xc[2][NB], xn[2][NB];  // XD == 0: B fragments of this tile and the next
+  XFrag<XD> xr[D];              // XD > 0: X tiles of the ring's steps
   int oe0[F], oe1[F];
   int c0 = 0;
 #define RZ_OFFSETS()                                                        \
@@ -591,6 +665,8 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
           bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[nb_] + 64u, xs_, 0)); \
     }                                                                                 \
   }
+#define RZ_LOADXS(J, DST)                                                             \
+  x_load<XD>(xrs, xloff, (uint32_t)(xt0 + (c0 + (J)) * WAVES) * 128u, DST)
 #define RZ_ISSUE_FIXED(J, R)                                                              \
   {                                                                                       \
     const uint32_t fs_ = (uint32_t)((c0 + (J)) * WAVES) * (uint32_t)kRecBytes;            \
@@ -615,12 +691,19 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
   }
 #define RZ_STEP(J, SC, SN, RC, MC, RN, MN)                                                 \
   {                                                                                        \
-    _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                                 \
-      xc[0][nb_] = xn[0][nb_];                                                             \
-      xc[1][nb_] = xn[1][nb_];                                                             \
+    if constexpr (XD == 0) {                                                               \
+      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                               \
+        xc[0][nb_] = xn[0][nb_];                                                           \
+        xc[1][nb_] = xn[1][nb_];                                                           \
+      }                                                                                    \
+      RZ_LOADX(min((J) + 1, last), xn);                                                    \
     }                                                                                      \
-    RZ_LOADX(min((J) + 1, last), xn);                                                      \
     RZ_STAGE(SN, RN, MN);                                                                  \
+    if constexpr (XD > 0) {                                                                \
+      x_stage<XD>(xst_w, xr[SC]);                                                          \
+      xc[0][0] = *reinterpret_cast<const bf16x8*>(xst_r);                                  \
+      xc[1][0] = *reinterpret_cast<const bf16x8*>(xst_r + 64);                             \
+    }                                                                                      \
     if ((J) < n) {                                                                         \
       _Pragma("unroll") for (int f_ = 0; f_ < F; ++f_) {                                   \
         u32x4 a0_, a1_;                                                                    \
@@ -636,6 +719,7 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
       }                                                                                    \
     }                                                                                      \
     RZ_ISSUE(min((J) + D, last), RC, MC);                                                  \
+    if constexpr (XD > 0) RZ_LOADXS(min((J) + D, last), xr[SC]);                           \
   }
   // Start-up: chunk 0's outlier offsets, the decode table's image, the first
   // records' fixed parts and the first X tile go out together; the records'
@@ -649,8 +733,11 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
     RZ_OFFSETS();
     r_tab_load<WAVES * 64>(tab, threadIdx.x);
 #pragma unroll
-    for (int k = 0; k < D; ++k) RZ_ISSUE_FIXED(min(k, last), R[k]);
-    RZ_LOADX(0, xn);
+    for (int k = 0; k < D; ++k) {
+      RZ_ISSUE_FIXED(min(k, last), R[k]);
+      if constexpr (XD > 0) RZ_LOADXS(min(k, last), xr[k]);
+    }
+    if constexpr (XD == 0) RZ_LOADX(0, xn);
 #pragma unroll
     for (int k = 0; k < D; ++k) RZ_ISSUE_EXPS(min(k, last), R[k], MT[k]);
     r_tab_store_exp<WAVES * 64>(T, tab, threadIdx.x, ex.lo, ex.hi);
@@ -663,8 +750,11 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
     if (c0 > 0) {
       RZ_OFFSETS();
 #pragma unroll
-      for (int k = 0; k < D; ++k) RZ_ISSUE(min(k, last), R[k], MT[k]);
-      RZ_LOADX(0, xn);
+      for (int k = 0; k < D; ++k) {
+        RZ_ISSUE(min(k, last), R[k], MT[k]);
+        if constexpr (XD > 0) RZ_LOADXS(min(k, last), xr[k]);
+      }
+      if constexpr (XD == 0) RZ_LOADX(0, xn);
     }
     RZ_STAGE(0, R[0], MT[0]);
     for (int j = 0; j < n; j += D) {
@@ -678,6 +768,7 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
 #undef RZ_ISSUE_EXPS
 #undef RZ_ISSUE_FIXED
 #undef RZ_ISSUE
+#undef RZ_LOADXS
 #undef RZ_LOADX
 #undef RZ_OFFSETS
 
@@ -974,19 +1065,40 @@ static int r_grid(int64_t nrec, int waves_per_block) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, 256 * 64));
 }
 
-template <int F, int NB, int kWaves>
-static hipError_t launch_rgemm(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
-                               const int32_t* eoff, int start_exp, const uint16_t* X,
-                               uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split,
-                               SplitFix fx) {
+template <int F, int NB, int kWaves, int XD>
+static hipError_t launch_rgemm_x(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
+                                 const int32_t* eoff, int start_exp, const uint16_t* X,
+                                 uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split,
+                                 SplitFix fx) {
   // records in flight per wave: 4 with one band per wave (more bytes in
   // flight at the same occupancy: 1-2.5 us faster on the 14336- to
   // 28672-row shapes), 3 with two (VGPRs)
   constexpr int kDepth = F == 1 ? 4 : 3;
   dim3 grid((M / 16 + F - 1) / F, split_k, (N + NB * 16 - 1) / (NB * 16));
-  hipLaunchKernelGGL((rgemm_kernel<F, NB, kWaves, kDepth>), grid, dim3(kWaves * 64), 0, st, fixed, exps,
-                     eoff, start_exp, X, Y, M, N, K, kb_per_split, fx);
+  hipLaunchKernelGGL((rgemm_kernel<F, NB, kWaves, kDepth, XD>), grid, dim3(kWaves * 64), 0, st,
+                     fixed, exps, eoff, start_exp, X, Y, M, N, K, kb_per_split, fx);
   return hipGetLastError();
+}
+
+// Narrow kernels: X staged through LDS for N <= 8 (one, two or four dwords
+// per lane per tile: 2-9% faster than B fragments from memory on the
+// Llama-3 / 3.1 shapes), B fragments straight from memory above.
+template <int F, int NB, int kWaves>
+static hipError_t launch_rgemm(hipStream_t st, const uint8_t* fixed, const uint8_t* exps,
+                               const int32_t* eoff, int start_exp, const uint16_t* X,
+                               uint16_t* Y, int M, int N, int K, int split_k, int kb_per_split,
+                               SplitFix fx) {
+  if (NB == 1 && N <= 2)
+    return launch_rgemm_x<F, NB, kWaves, 1>(st, fixed, exps, eoff, start_exp, X, Y, M, N, K,
+                                            split_k, kb_per_split, fx);
+  if (NB == 1 && N <= 4)
+    return launch_rgemm_x<F, NB, kWaves, 2>(st, fixed, exps, eoff, start_exp, X, Y, M, N, K,
+                                            split_k, kb_per_split, fx);
+  if (NB == 1 && N <= 8)
+    return launch_rgemm_x<F, NB, kWaves, 4>(st, fixed, exps, eoff, start_exp, X, Y, M, N, K,
+                                            split_k, kb_per_split, fx);
+  return launch_rgemm_x<F, NB, kWaves, 0>(st, fixed, exps, eoff, start_exp, X, Y, M, N, K,
+                                          split_k, kb_per_split, fx);
 }
 
 constexpr int kWideDepth = 2;  // records in flight per wave (ring of RD steps)
