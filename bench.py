@@ -181,6 +181,9 @@ def bench_c3(torch, zs, stream, gen, dev):
         comp.append(layer)
     comp_bytes = sum(c.compressed_bytes for L in comp for c in L)
     dense_bytes = C3_LAYERS * sum(2 * M * K for _, M, K in C3_SHAPES)
+    # encoder kernels alone on layer 0 (no host size synchronisation)
+    k_t = sum(compress_kernel_seconds(torch, zs, w) for w in dense[:len(C3_SHAPES)])
+    k_bytes = sum(2 * M * K for _, M, K in C3_SHAPES)
     rows = []
     for N in C3_NS:
         progress(f"config 3: N={N}")
@@ -225,6 +228,7 @@ def bench_c3(torch, zs, stream, gen, dev):
             "weights": "N(0,0.02) bf16", "compression_ratio": round(dense_bytes / comp_bytes, 4),
             "compressed_GB": round(comp_bytes / 1e9, 3), "dense_GB": round(dense_bytes / 1e9, 3),
             "gpu_compress_GBps": round(enc_bytes / enc_t / 1e9, 2),
+            "gpu_compress_kernels_GBps": round(k_bytes / k_t / 1e9, 2),
             "dense_timing": "8 distinct resident layers, scaled x10", "per_N": rows}
 
 
@@ -343,9 +347,11 @@ def bench_kv(torch, zs, dev, gen):
                         "bit_exact": bool(torch.equal(out.view(torch.int16), mat.view(torch.int16)))})
             del c
         tr, r = host_clock(lambda: zs.compress_retiled(mat))
+        tk = compress_kernel_seconds(torch, zs, mat)
         tdr = clock(lambda: zs.decompress_retiled(r, out))
         row.update({"ratio_retiled": round(nbytes / r.compressed_bytes, 4),
                     "compress_retiled_GBps": round(nbytes / tr / 1e9, 2),
+                    "compress_retiled_kernels_GBps": round(nbytes / tk / 1e9, 2),
                     "decompress_retiled_GBps": round(nbytes / tdr / 1e9, 2),
                     "bit_exact_retiled": bool(torch.equal(out.view(torch.int16),
                                                           mat.view(torch.int16)))})
@@ -353,7 +359,8 @@ def bench_kv(torch, zs, dev, gen):
         del mat, r, out
         torch.cuda.empty_cache()
     return {"layout": "by_kv_head",
-            "compress_timing": "host clock around one call incl. its size sync",
+            "compress_timing": "host clock around one call incl. its size sync; *_kernels_GBps: "
+                               "HIP events around the encoder's kernels alone",
             "decompress_timing": "HIP events, 5 calls", "cases": rows}
 
 
@@ -394,6 +401,46 @@ def traffic_from_profile(kernel):
                 return {"bytes_per_launch": int(line.rsplit(":", 1)[1].strip()),
                         "source": os.path.relpath(path, ROOT)}
     return None
+
+
+def compress_kernel_seconds(torch, zs, x, window="kv", reps=3):
+    """Device time of the re-tiled GPU encoder's kernels on the bf16 matrix x
+    (window histogram + selection, fixed parts + counts + offset scan,
+    exponent-byte compaction), HIP events on the current stream, with every
+    buffer allocated beforehand so that no host size synchronisation sits
+    between the phases (compress_retiled needs one to size the stream)."""
+    L = zs.lib()
+    rows, cols = x.shape
+    nrec = rows // 16 * (cols // 64)
+    dev = x.device
+    i32 = dict(dtype=torch.int32, device=dev)
+    top, counts = torch.empty(7, **i32), torch.empty(256, dtype=torch.int64, device=dev)
+    cnt, eoff = torch.empty(nrec, **i32), torch.empty(nrec + 1, **i32)
+    total = torch.empty(1, dtype=torch.int64, device=dev)
+    fixed = torch.empty(nrec * 1408, dtype=torch.uint8, device=dev)
+    tmp = torch.empty(nrec * zs._lib.ZS_RETILED_EXP_SLOT_BYTES, dtype=torch.uint8, device=dev)
+    nexp = zs.compress_retiled(x, window=window).num_outliers
+    exps = torch.empty(nexp + 64, dtype=torch.uint8, device=dev)
+    analyze = (L.zs_analyze_top_exponents_u64_gpu if window == "kv"
+               else L.zs_analyze_exponents_weights_gpu)
+
+    def run():
+        st = torch.cuda.current_stream().cuda_stream
+        assert analyze(st, x.data_ptr(), x.numel(), counts.data_ptr(), top.data_ptr()) == 0
+        assert L.zs_compress_retiled_fixed_gpu(st, x.data_ptr(), rows, cols, top.data_ptr(),
+                                               fixed.data_ptr(), cnt.data_ptr(), eoff.data_ptr(),
+                                               total.data_ptr(), tmp.data_ptr()) == 0
+        assert L.zs_compress_retiled_exps_gpu(st, x.data_ptr(), rows, cols, top.data_ptr(),
+                                              eoff.data_ptr(), tmp.data_ptr(), exps.data_ptr()) == 0
+    run()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        run()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / 1e3 / reps
 
 
 def clone_retiled(r):
@@ -557,8 +604,9 @@ def main():
             for N in NS for M in {m for _, m, _ in SHAPES}}
 
     # GPU encoder throughput on one layer (config 2 weights), GB/s of original bytes.
-    enc_t, enc_c_t, enc_bytes = 0.0, 0.0, 0
+    enc_t, enc_c_t, enc_k_t, enc_bytes = 0.0, 0.0, 0.0, 0
     for name, M, K, w, c, r in layers[0]:
+        enc_k_t += compress_kernel_seconds(torch, zs, w)
         zs.compress_retiled(w)
         zs.compress_zipserv(w)
         torch.cuda.synchronize()
@@ -743,6 +791,7 @@ def main():
         "dense_TBps_effective": None if result_dense is None else round(result_dense, 4),
         "speedup_vs_dense": None if result_dense is None else round(value / result_dense, 4),
         "gpu_compress_GBps": round(enc_bytes / enc_t / 1e9, 2),
+        "gpu_compress_kernels_GBps": round(enc_bytes / enc_k_t / 1e9, 2),
         "gpu_compress_canonical_GBps": round(enc_bytes / enc_c_t / 1e9, 2),
         "roofline": {
             "bound": "hbm",

@@ -45,6 +45,8 @@ extern "C" {
 #define ZS_E_NOMEM (-4)       /* host allocation failed                    */
 
 #define ZS_STREAM_SLACK_BYTES 64
+/* Bytes of d_tmp per 16 x 64 record for zs_compress_retiled_fixed_gpu. */
+#define ZS_RETILED_EXP_SLOT_BYTES 256
 
 /* KV layouts of a compressed cache (flash.h:19-20). */
 #define ZS_LAYOUT_HEAD_MAJOR 0 /* rows = ((b * Hkv + h) * rows_per_head + t) */
@@ -194,6 +196,20 @@ int zs_compress_retiled_count_gpu(void* stream, const uint16_t* d_input, int M, 
 int zs_compress_retiled_emit_gpu(void* stream, const uint16_t* d_input, int M, int K,
                                  const int32_t* d_top_exponents, const int32_t* d_eoff,
                                  uint8_t* d_fixed, uint8_t* d_exps);
+/* The same bytes with the input read once after the window histogram (two
+ * input passes in all instead of three): zs_compress_retiled_fixed_gpu
+ * writes the fixed parts, the per-record outlier counts and their offsets
+ * (*d_total as above) and parks up to ZS_RETILED_EXP_SLOT_BYTES outlier bytes
+ * per record in d_tmp (num_records * ZS_RETILED_EXP_SLOT_BYTES bytes); once d_exps is allocated (*d_total +
+ * ZS_STREAM_SLACK_BYTES), zs_compress_retiled_exps_gpu moves them into the
+ * exponent stream (records with more outliers re-read their input tile). */
+int zs_compress_retiled_fixed_gpu(void* stream, const uint16_t* d_input, int M, int K,
+                                  const int32_t* d_top_exponents, uint8_t* d_fixed,
+                                  int32_t* d_counts, int32_t* d_eoff, int64_t* d_total,
+                                  uint8_t* d_tmp);
+int zs_compress_retiled_exps_gpu(void* stream, const uint16_t* d_input, int M, int K,
+                                 const int32_t* d_top_exponents, const int32_t* d_eoff,
+                                 const uint8_t* d_tmp, uint8_t* d_exps);
 /* Canonical TCA-TBE streams -> re-tiled, same two phases (window start_exp). */
 int zs_retile_triple_bitmap_count_gpu(void* stream, const uint8_t* SignMantissa,
                                       const uint16_t* CompressedFull, const uint64_t* Bitmap1,

@@ -101,11 +101,15 @@ def _data_with_counts(counts, rng):
     return (e << 7) | rng.integers(0, 128, e.size, dtype=np.uint16)
 
 
+@pytest.mark.parametrize("rule", ["kv", "weights"])
 @pytest.mark.parametrize("case", ["evict_first_min_slot", "ties_at_seventh", "few_present",
-                                  "all_equal", "top_edge", "noncontiguous"])
-def test_gpu_select_window_special_cases(torch_cuda, case):
+                                  "all_equal", "top_edge", "noncontiguous", "one_exponent",
+                                  "zeros_only", "bottom_edge"])
+def test_gpu_select_window_special_cases(torch_cuda, case, rule):
     # window selection of zipserv_decode_attention_ext.cu:65-134 (streaming
-    # top-7 evicting the first minimum slot) against the oracle restatement
+    # top-7 evicting the first minimum slot; "kv") and of
+    # kernel_benchmark/utils.h:189-272 (seven largest-count passes; "weights")
+    # against the oracle restatements
     torch = torch_cuda
     rng = np.random.default_rng(31)
     c = np.zeros(256, np.int64)
@@ -120,18 +124,31 @@ def test_gpu_select_window_special_cases(torch_cuda, case):
         c[:] = 3
     elif case == "top_edge":
         c[250:256] = [10, 20, 30, 40, 50, 60]
+    elif case == "one_exponent":
+        c[127] = 4096                        # the rules differ: 121..127 vs 1..7
+    elif case == "zeros_only":
+        c[0] = 4096
+    elif case == "bottom_edge":
+        c[0:5] = [60, 50, 40, 30, 20]
     else:
         c[[10, 11, 12, 40, 41, 90, 200]] = [7, 8, 9, 30, 31, 5, 6]
     a = _data_with_counts(c, rng)
     t = to_torch_bf16(a)
-    counts = torch.empty(256, dtype=torch.int32, device="cuda")
     top = torch.empty(7, dtype=torch.int32, device="cuda")
-    rc = zs.lib().zs_analyze_top_exponents_gpu(int(torch.cuda.current_stream().cuda_stream),
-                                              t.data_ptr(), a.size, counts.data_ptr(),
-                                              top.data_ptr(), None)
+    st = int(torch.cuda.current_stream().cuda_stream)
+    if rule == "kv":
+        counts = torch.empty(256, dtype=torch.int32, device="cuda")
+        rc = zs.lib().zs_analyze_top_exponents_gpu(st, t.data_ptr(), a.size, counts.data_ptr(),
+                                                  top.data_ptr(), None)
+        want = zo.select_gpu(c)
+    else:
+        counts = torch.empty(256, dtype=torch.int64, device="cuda")
+        rc = zs.lib().zs_analyze_exponents_weights_gpu(st, t.data_ptr(), a.size,
+                                                      counts.data_ptr(), top.data_ptr())
+        want = zo.select_cpu(c)
     assert rc == 0
     np.testing.assert_array_equal(counts.cpu().numpy(), c)
-    assert top.cpu().tolist() == zo.select_gpu(c)
+    assert top.cpu().tolist() == want
 
 
 def rel_err(y, ref):

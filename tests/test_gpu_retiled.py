@@ -331,3 +331,51 @@ def test_retiled_mm_fused_rejects_bad_args(torch_cuda):
     assert L.zs_retiled_mm_fused(*args()) == 0
     torch.cuda.synchronize()
     assert int(cnt.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("kind", ["weights", "kv", "random_bits", "zeros"])
+def test_two_pass_encoder_equals_three_pass(torch_cuda, kind):
+    # zs_compress_retiled_fixed_gpu / _exps_gpu (input read once after the
+    # histogram; outlier bytes parked in 256-byte slots, records with more
+    # re-read their tile) against zs_compress_retiled_count_gpu / _emit_gpu
+    torch = torch_cuda
+    L = zs.lib()
+    rng = np.random.default_rng(91)
+    if kind == "weights":
+        W = weights_bf16(rng, (512, 1024), outlier_frac=0.01)
+    elif kind == "kv":
+        W, _ = pad_by_kv_head(kv_bf16(rng, 2, 200, 8, 128))
+    elif kind == "random_bits":
+        W = rng.integers(0, 65536, size=(128, 256), dtype=np.uint16)  # > 256 outliers per record
+    else:
+        W = np.zeros((64, 192), np.uint16)
+    x = to_torch_bf16(W)
+    M, K = W.shape
+    nrec = M // 16 * (K // 64)
+    st = int(torch.cuda.current_stream().cuda_stream)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    # zeros: the weights-path window (121..127) makes every element an outlier
+    top = torch.tensor(zo.analyze_cpu(W) if kind == "zeros" else zo.analyze_gpu(W), **i32)
+    cnt3, eoff3, cnt2, eoff2 = (torch.empty(n, **i32) for n in (nrec, nrec + 1, nrec, nrec + 1))
+    tot3, tot2 = (torch.empty(1, dtype=torch.int64, device="cuda") for _ in range(2))
+    fixed3 = torch.empty(nrec * 1408, dtype=torch.uint8, device="cuda")
+    fixed2 = torch.empty_like(fixed3)
+    tmp = torch.empty(nrec * 256, dtype=torch.uint8, device="cuda")
+    assert L.zs_compress_retiled_count_gpu(st, x.data_ptr(), M, K, top.data_ptr(), cnt3.data_ptr(),
+                                           eoff3.data_ptr(), tot3.data_ptr()) == 0
+    assert L.zs_compress_retiled_fixed_gpu(st, x.data_ptr(), M, K, top.data_ptr(),
+                                           fixed2.data_ptr(), cnt2.data_ptr(), eoff2.data_ptr(),
+                                           tot2.data_ptr(), tmp.data_ptr()) == 0
+    total = int(tot3.item())
+    assert int(tot2.item()) == total
+    exps3 = torch.zeros(total + 64, dtype=torch.uint8, device="cuda")
+    exps2 = torch.zeros_like(exps3)
+    assert L.zs_compress_retiled_emit_gpu(st, x.data_ptr(), M, K, top.data_ptr(), eoff3.data_ptr(),
+                                          fixed3.data_ptr(), exps3.data_ptr()) == 0
+    assert L.zs_compress_retiled_exps_gpu(st, x.data_ptr(), M, K, top.data_ptr(), eoff2.data_ptr(),
+                                          tmp.data_ptr(), exps2.data_ptr()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(cnt2, cnt3) and torch.equal(eoff2, eoff3)
+    assert torch.equal(fixed2, fixed3) and torch.equal(exps2, exps3)
+    if kind in ("random_bits", "zeros"):
+        assert int(cnt2.max()) > 256  # the re-read path ran

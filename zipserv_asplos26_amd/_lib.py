@@ -19,6 +19,7 @@ ZS_E_UNSUPPORTED = -2
 ZS_E_OVERFLOW = -3
 ZS_E_NOMEM = -4
 ZS_STREAM_SLACK_BYTES = 64
+ZS_RETILED_EXP_SLOT_BYTES = 256
 ZS_LAYOUT_HEAD_MAJOR = 0
 ZS_LAYOUT_TOKEN_MAJOR = 1
 
@@ -59,6 +60,9 @@ SIGNATURES = {
     "zs_retiled_fixed_bytes": (C.c_int64, [C.c_int, C.c_int]),
     "zs_compress_retiled_count_gpu": (C.c_int, [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p]),
     "zs_compress_retiled_emit_gpu": (C.c_int, [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p]),
+    "zs_compress_retiled_fixed_gpu": (C.c_int, [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p, _p,
+                                                _p]),
+    "zs_compress_retiled_exps_gpu": (C.c_int, [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p]),
     "zs_retile_triple_bitmap_count_gpu": (
         C.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, C.c_int, C.c_int, _p, _p, _p]),
     "zs_retile_triple_bitmap_emit_gpu": (

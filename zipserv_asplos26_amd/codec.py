@@ -501,19 +501,22 @@ def compress_retiled(input, logical_rows=None, logical_cols=None, layout="by_kv_
     top, counts = torch.empty(7, **i32), torch.empty(256, dtype=torch.int64, device=dev)
     cnt, eoff = torch.empty(nrec, **i32), torch.empty(nrec + 1, **i32)
     total = torch.empty(1, dtype=torch.int64, device=dev)
+    fixed = torch.empty(nrec * 1408, dtype=torch.uint8, device=dev)
+    tmp = torch.empty(nrec * _lib.ZS_RETILED_EXP_SLOT_BYTES, dtype=torch.uint8, device=dev)
     st = _stream()
     # 64-bit bins: the re-tiled layout takes matrices past 2^31 elements.
     _device_window(input, window, top, counts)
-    check("zs_compress_retiled_count_gpu",
-          L.zs_compress_retiled_count_gpu(st, _dptr(input), rows, cols, _dptr(top), _dptr(cnt),
-                                          _dptr(eoff), _dptr(total)))
+    check("zs_compress_retiled_fixed_gpu",
+          L.zs_compress_retiled_fixed_gpu(st, _dptr(input), rows, cols, _dptr(top), _dptr(fixed),
+                                          _dptr(cnt), _dptr(eoff), _dptr(total), _dptr(tmp)))
     tot, top0 = int(total.item()), int(top[0].item())  # synchronises (sizes the stream)
     if tot > 2**31 - 1:
         raise OverflowError("outlier count exceeds the int32 offsets")
-    fixed, exps, _ = _retiled_alloc(rows, cols, tot, dev)
-    check("zs_compress_retiled_emit_gpu",
-          L.zs_compress_retiled_emit_gpu(st, _dptr(input), rows, cols, _dptr(top), _dptr(eoff),
-                                         _dptr(fixed), _dptr(exps)))
+    exps = torch.zeros(tot + _lib.ZS_STREAM_SLACK_BYTES, dtype=torch.uint8, device=dev)
+    check("zs_compress_retiled_exps_gpu",
+          L.zs_compress_retiled_exps_gpu(st, _dptr(input), rows, cols, _dptr(top), _dptr(eoff),
+                                         _dptr(tmp), _dptr(exps)))
+    del tmp  # stream-ordered: the allocator reuses it only after the compaction
     return ZipservRetiled(fixed, exps, eoff, rows, cols,
                           rows if logical_rows is None else logical_rows,
                           cols if logical_cols is None else logical_cols,

@@ -1,6 +1,6 @@
 // zs_encode.hip -- gfx950 TCA-TBE encoder (the KV-cache compressor path).
 //
-//   analyze:  hist_kernel (LDS 256-bin histogram, grid-stride 16-byte loads)
+//   analyze:  hist_kernel (per-lane LDS 256-bin histograms, grid-stride 16-byte loads)
 //             -> select_kernel (window choice with the semantics of
 //             kernel_benchmark/zipserv_decode_attention_ext.cu:65-134).
 //   encode:   classify_kernel (bitmaps, small/median tile counts, per-GT
@@ -26,42 +26,64 @@ __global__ void fill_i32_kernel(int32_t* p, int n, int32_t v) {
   if (i < n) p[i] = v;
 }
 
-// 256-bin exponent histogram.  Weights concentrate in a few exponents, so a
-// single LDS copy of the bins serialises on conflicting atomics; 16 copies
-// (lane % 16) cut the worst case from 64-way to 4-way.  A workgroup's own
-// bins stay below 2^31 (the launch gives each at most 2^30 elements); the
-// global bins are int32 (the reference's) or 64-bit (any numel).
+// 256-bin exponent histogram.  Weights concentrate in a few exponents, so
+// shared bins serialise on conflicting LDS atomics; each lane of a wave owns
+// a copy of the bins (a copy per lane id, shared by the workgroup's waves),
+// and copies sit kHistPitch = 257 dwords apart so that 64 lanes adding to
+// one bin hit 64 different banks.  A workgroup's own bins stay below 2^31
+// (the launch gives each at most 2^30 elements); the global bins are int32
+// (the reference's) or 64-bit (any numel).
+constexpr int kHistThreads = 512, kHistCopies = 64, kHistPitch = 257;
+
+__device__ __forceinline__ void hist_add8(uint32_t* hc, uint4 x) {
+  const uint32_t d[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    atomicAdd(&hc[(d[j] >> 7) & 0xFF], 1u);
+    atomicAdd(&hc[(d[j] >> 23) & 0xFF], 1u);
+  }
+}
+
+__device__ __forceinline__ uint4 nt_load16(const uint4* p) {
+  const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(x.x, x.y, x.z, x.w);
+}
+
 template <typename C>
-__global__ __launch_bounds__(256) void hist_kernel(const uint16_t* in, int64_t n, C* counts) {
-  __shared__ int32_t h[16][256];
-  for (int i = threadIdx.x; i < 16 * 256; i += blockDim.x) (&h[0][0])[i] = 0;
+__global__ __launch_bounds__(kHistThreads) void hist_kernel(const uint16_t* in, int64_t n,
+                                                            C* counts) {
+  __shared__ uint32_t h[kHistCopies * kHistPitch];
+  for (int i = threadIdx.x; i < kHistCopies * kHistPitch; i += kHistThreads) h[i] = 0;
   __syncthreads();
-  int32_t* hc = h[threadIdx.x & 15];
-  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
+  uint32_t* hc = h + lane_id() * kHistPitch;
+  const int64_t tid = (int64_t)blockIdx.x * kHistThreads + threadIdx.x;
+  const int64_t nthreads = (int64_t)gridDim.x * kHistThreads;
   const bool aligned = (reinterpret_cast<uintptr_t>(in) & 15) == 0;
   const int64_t nvec = aligned ? n / 8 : 0;
   const uint4* v = reinterpret_cast<const uint4*>(in);
-  for (int64_t i = tid; i < nvec; i += nthreads) {
-    const uint4 x = v[i];
-    const uint32_t d[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      atomicAdd(&hc[(d[j] >> 7) & 0xFF], 1);
-      atomicAdd(&hc[(d[j] >> 23) & 0xFF], 1);
-    }
+  int64_t i = tid;
+  for (; i + 3 * nthreads < nvec; i += 4 * nthreads) {  // four 16-byte loads in flight
+    // streamed once: non-temporal loads keep the caches for other data
+    const uint4 x0 = nt_load16(v + i), x1 = nt_load16(v + i + nthreads),
+                x2 = nt_load16(v + i + 2 * nthreads), x3 = nt_load16(v + i + 3 * nthreads);
+    hist_add8(hc, x0);
+    hist_add8(hc, x1);
+    hist_add8(hc, x2);
+    hist_add8(hc, x3);
   }
-  for (int64_t i = nvec * 8 + tid; i < n; i += nthreads) atomicAdd(&hc[(in[i] >> 7) & 0xFF], 1);
+  for (; i < nvec; i += nthreads) hist_add8(hc, v[i]);
+  for (int64_t e = nvec * 8 + tid; e < n; e += nthreads) atomicAdd(&hc[(in[e] >> 7) & 0xFF], 1u);
   __syncthreads();
-  int32_t c = 0;
-#pragma unroll
-  for (int k = 0; k < 16; ++k) c += h[k][threadIdx.x];
-  if (c) {
-    if constexpr (sizeof(C) == 8)
-      atomicAdd(reinterpret_cast<unsigned long long*>(&counts[threadIdx.x]),
-                (unsigned long long)c);
-    else
-      atomicAdd(&counts[threadIdx.x], c);
+  if (threadIdx.x < 256) {
+    uint32_t c = 0;
+    for (int k = 0; k < kHistCopies; ++k) c += h[k * kHistPitch + threadIdx.x];
+    if (c) {
+      if constexpr (sizeof(C) == 8)
+        atomicAdd(reinterpret_cast<unsigned long long*>(&counts[threadIdx.x]),
+                  (unsigned long long)c);
+      else
+        atomicAdd(&counts[threadIdx.x], (C)c);
+    }
   }
 }
 
@@ -72,42 +94,78 @@ __device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
 }
 
 // Shared tail of both window rules (kernel_benchmark/utils.h:228-270,
-// zipserv_decode_attention_ext.cu:103-133): n found candidates (exponents),
-// filled up to 7 with 127 - i, sorted; the first candidate whose 7-exponent
-// window has only positive counts wins, else the start of the longest run of
-// consecutive candidates (clamped to [0, 248] by the GPU rule only).
-__device__ __forceinline__ void window_from_candidates(const int64_t* counts, int* cand, int n,
+// zipserv_decode_attention_ext.cu:103-133): the 7 candidates (exponents;
+// missing ones already filled with 127 - i), sorted; the first candidate
+// whose 7-exponent window has only positive counts wins, else the start of
+// the longest run of consecutive candidates (clamped to [0, 248] by the GPU
+// rule only).  Every array index is a compile-time constant, so the
+// candidates stay in registers (a dynamic index would put them in scratch
+// memory, one memory round trip per access).
+__device__ __forceinline__ void window_from_candidates(const int64_t* counts, int (&cand)[7],
                                                        bool clamp, int32_t* top) {
-  for (; n < 7; ++n) cand[n] = 127 - n;
-  for (int i = 1; i < 7; ++i) {
-    const int key = cand[i];
-    int j = i - 1;
-    while (j >= 0 && cand[j] > key) {
-      cand[j + 1] = cand[j];
-      --j;
+#pragma unroll
+  for (int i = 0; i < 6; ++i)  // bubble sort; ties are equal values, so any sort agrees
+#pragma unroll
+    for (int j = 0; j < 6 - i; ++j) {
+      const int lo = min(cand[j], cand[j + 1]), hi = max(cand[j], cand[j + 1]);
+      cand[j] = lo;
+      cand[j + 1] = hi;
     }
-    cand[j + 1] = key;
-  }
+  int win = -1;
+#pragma unroll
   for (int c = 0; c < 7; ++c) {
     const int st = cand[c];
-    if (st < 0 || st + 6 > 255) continue;
-    bool all = true;
-    for (int i = 0; i < 7 && all; ++i) all = counts[st + i] > 0;
-    if (all) {
-      for (int i = 0; i < 7; ++i) top[i] = st + i;
-      return;
+    if (win < 0 && st >= 0 && st + 6 <= 255) {
+      bool all = true;
+      for (int i = 0; i < 7; ++i) all = all && counts[st + i] > 0;
+      if (all) win = st;
     }
   }
-  int best = cand[0], best_len = 1, run = 1;
-  for (int i = 1; i < 7; ++i) {
-    run = (cand[i] == cand[i - 1] + 1) ? run + 1 : 1;
-    if (run > best_len) {
-      best_len = run;
-      best = cand[i] - run + 1;
+  if (win < 0) {
+    int best = cand[0], best_len = 1, run = 1;
+#pragma unroll
+    for (int i = 1; i < 7; ++i) {
+      run = (cand[i] == cand[i - 1] + 1) ? run + 1 : 1;
+      if (run > best_len) {
+        best_len = run;
+        best = cand[i] - run + 1;
+      }
     }
+    win = clamp ? (best < 0 ? 0 : (best > 248 ? 248 : best)) : best;
   }
-  if (clamp) best = best < 0 ? 0 : (best > 248 ? 248 : best);
-  for (int i = 0; i < 7; ++i) top[i] = best + i;
+#pragma unroll
+  for (int i = 0; i < 7; ++i) top[i] = win + i;
+}
+
+// Seven wave-wide maxima of key = (count << 8 | 255 - exponent) over the
+// exponents not taken yet (lane i holds exponents i, i + 64, i + 128,
+// i + 192; zero counts have key 0 and are never taken): cand[t] is the
+// exponent of pass t, or 127 - t once no positive count is left.  Returns the
+// number of exponents taken; *c7 is the count of the last one taken.
+__device__ __forceinline__ int top7_passes(int64_t (&key)[4], int l, int (&cand)[7],
+                                           int64_t* c7) {
+  int taken = 0;
+#pragma unroll
+  for (int t = 0; t < 7; ++t) {
+    int64_t best = key[0];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) best = key[k] > best ? key[k] : best;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const int64_t o = __shfl_xor(best, off);
+      best = o > best ? o : best;
+    }
+    const int e = 255 - (int)(best & 0xFF);
+    cand[t] = best == 0 ? 127 - t : e;
+    if (best != 0) {
+      ++taken;
+      *c7 = best >> 8;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (best != 0 && 64 * k + l == e) key[k] = 0;
+  }
+  return taken;
 }
 
 // Window selection of zipserv_decode_attention_ext.cu:65-134: seven slots
@@ -129,6 +187,26 @@ __global__ __launch_bounds__(64) void select_kernel(const C* counts_g, int32_t* 
 #pragma unroll
   for (int k = 0; k < 4; ++k) counts[64 * k + l] = cv[k];
   __syncthreads();
+  // When exactly seven exponents have a count >= the seventh largest count
+  // c7 > 0, those seven are the final slots whatever the order: one of them
+  // is rejected or evicted only while seven others with counts >= its own
+  // sit in the slots, which would make eight.  Only then is the streaming
+  // walk below skipped.
+  {
+    int64_t key[4], c7 = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) key[k] = cv[k] > 0 ? (cv[k] << 8) | (255 - (64 * k + l)) : 0;
+    int cand[7];
+    if (top7_passes(key, l, cand, &c7) == 7) {
+      int ge = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ge += __builtin_popcountll(__builtin_amdgcn_ballot_w64(cv[k] >= c7));
+      if (ge == 7) {
+        if (l == 0) window_from_candidates(counts, cand, true, top);
+        return;
+      }
+    }
+  }
   int te[7];
   int64_t tc[7];
 #pragma unroll
@@ -138,7 +216,9 @@ __global__ __launch_bounds__(64) void select_kernel(const C* counts_g, int32_t* 
   }
   // Only an exponent whose count beats the current minimum slot changes the
   // slots, and the minimum never decreases: walk just those (a ballot of
-  // count > min, refreshed after every change), in exponent order.
+  // count > min, refreshed after every change), in exponent order.  The
+  // first minimum slot is replaced; its count is the running minimum tmin,
+  // so the slot is found by comparing against tmin (no dynamic index).
   int64_t tmin = -1;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
@@ -147,16 +227,14 @@ __global__ __launch_bounds__(64) void select_kernel(const C* counts_g, int32_t* 
       const int j = __builtin_ctzll(mask);
       mask &= mask - 1;
       const int64_t c = readlane64(cv[k], j);
-      int mi = 0;
-#pragma unroll
-      for (int i = 1; i < 7; ++i)
-        if (tc[i] < tc[mi]) mi = i;
-      if (c > tc[mi]) {
+      if (c > tmin) {
+        bool done = false;
 #pragma unroll
         for (int i = 0; i < 7; ++i)
-          if (i == mi) {
+          if (!done && tc[i] == tmin) {
             tc[i] = c;
             te[i] = 64 * k + j;
+            done = true;
           }
         tmin = tc[0];
 #pragma unroll
@@ -166,11 +244,14 @@ __global__ __launch_bounds__(64) void select_kernel(const C* counts_g, int32_t* 
     }
   }
   if (l != 0) return;
-  int cand[7], n = 0;
-  for (int i = 0; i < 7; ++i)
-    if (te[i] >= 0) cand[n++] = te[i];
-  window_from_candidates(counts, cand, n, true, top);
+  // Slots fill in index order, so untaken slots (-1) form a suffix: slot i
+  // untaken is candidate i missing, filled with 127 - i.
+  int cand[7];
+#pragma unroll
+  for (int i = 0; i < 7; ++i) cand[i] = te[i] >= 0 ? te[i] : 127 - i;
+  window_from_candidates(counts, cand, true, top);
 }
+
 
 // Window selection of kernel_benchmark/utils.h:189-272 (the host analyzer of
 // the weights path) on the device: seven passes each take the strictly
@@ -193,26 +274,13 @@ __global__ __launch_bounds__(64) void select_weights_kernel(const C* counts_g, i
     key[k] = c > 0 ? (c << 8) | (255 - (64 * k + l)) : 0;
   }
   __syncthreads();
-  int cand[7], n = 0;
-  for (int t = 0; t < 7; ++t) {
-    int64_t best = key[0];
-#pragma unroll
-    for (int k = 1; k < 4; ++k) best = key[k] > best ? key[k] : best;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const int64_t o = __shfl_xor(best, off);
-      best = o > best ? o : best;
-    }
-    if (best == 0) break;  // wave-uniform: no positive count left
-    const int e = 255 - (int)(best & 0xFF);
-    cand[n++] = e;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (64 * k + l == e) key[k] = 0;
-  }
+  int cand[7];
+  int64_t c7;
+  top7_passes(key, l, cand, &c7);
   if (l != 0) return;
-  window_from_candidates(counts, cand, n, false, top);
+  window_from_candidates(counts, cand, false, top);
 }
+
 
 // Exponent -> code LUT in LDS (code 0 = outlier), as s_exp_lut of
 // csrc/L_API.cu:1149-1156.
@@ -543,14 +611,16 @@ static int hip_status(hipError_t e) { return e == hipSuccess ? ZS_OK : (int)e; }
 template <typename C>
 static int analyze(hipStream_t st, const uint16_t* d_input, int64_t numel, C* d_counts,
                    int32_t* d_top, bool weights_rule = false) {
-  // Enough workgroups to fill the chip, and at most 2^30 elements each.
+  // Two 512-thread workgroups per CU (their bins fill 2 x 64 KB of LDS),
+  // and at most 2^30 elements each.
   const int64_t blocks = std::max<int64_t>(
-      std::min<int64_t>((numel + 2047) / 2048, (int64_t)device_cu_count() * 4),
+      std::min<int64_t>((numel + 8 * kHistThreads - 1) / (8 * kHistThreads),
+                        (int64_t)device_cu_count() * 2),
       (numel + (1LL << 30) - 1) >> 30);
   if (blocks > INT32_MAX) return ZS_E_OVERFLOW;
   hipLaunchKernelGGL(fill_i32_kernel, dim3(sizeof(C) / 4), dim3(256), 0, st,
                      reinterpret_cast<int32_t*>(d_counts), (int)(256 * sizeof(C) / 4), 0);
-  hipLaunchKernelGGL(hist_kernel<C>, dim3((unsigned)blocks), dim3(256), 0, st, d_input, numel,
+  hipLaunchKernelGGL(hist_kernel<C>, dim3((unsigned)blocks), dim3(kHistThreads), 0, st, d_input, numel,
                      d_counts);
   if (weights_rule)
     hipLaunchKernelGGL(select_weights_kernel<C>, dim3(1), dim3(64), 0, st, d_counts, d_top);

@@ -183,11 +183,34 @@ static void launch_rscan(hipStream_t st, const int32_t* counts, int64_t n, int32
   hipLaunchKernelGGL(rscan_write_kernel, dim3((unsigned)tiles), dim3(256), 0, st, counts, n, eoff);
 }
 
+// The outlier exponent bytes of one record, in (half, lane, element) order,
+// from exps[0] on.
+__device__ __forceinline__ void emit_exps(uint8_t* exps, const u32x4 v[2], const uint32_t b[2][3]) {
+  uint32_t n[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) n[h] = 8 - __builtin_popcount(b[h][0] | b[h][1] | b[h][2]);
+  int rank0, rank1;
+  r_scan(n[0], n[1], rank0, rank1);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint32_t fm = ~(b[h][0] | b[h][1] | b[h][2]) & 0xFFu;
+    int o = h ? rank1 : rank0;
+    while (fm) {
+      const int i = __builtin_ctz(fm);
+      fm &= fm - 1;
+      const uint32_t x = (v[h][i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+      exps[o++] = (uint8_t)((x >> 7) & 0xFFu);
+    }
+  }
+}
+
 // Writes one record from the lane's 16 bf16 values and their code bit-planes
-// (Bp bit i = bit p-1 of the code of element i).
-__device__ __forceinline__ void emit_record(uint8_t* fixed, uint8_t* exps, int64_t rec,
-                                            int64_t ebase, const u32x4 v[2],
-                                            const uint32_t b[2][3]) {
+// (Bp bit i = bit p-1 of the code of element i): the fixed part, and the
+// outlier bytes from exps[ebase] on unless the record has more than `limit`
+// of them.  Returns the record's outlier count.
+__device__ __forceinline__ int emit_record(uint8_t* fixed, uint8_t* exps, int64_t rec,
+                                           int64_t ebase, const u32x4 v[2],
+                                           const uint32_t b[2][3], int limit = 1 << 30) {
   const int l = lane_id();
   u32x4 sm;
 #pragma unroll
@@ -220,17 +243,22 @@ __device__ __forceinline__ void emit_record(uint8_t* fixed, uint8_t* exps, int64
   *reinterpret_cast<uint16_t*>(f + kRecP16 + 2 * l) = (uint16_t)(c[1] >> 8);
   int rank0, rank1;
   r_scan(n[0], n[1], rank0, rank1);
+  // total = the last lane's inclusive half-1 rank
+  const int total = __builtin_amdgcn_readlane(rank1 + (int)n[1], 63);
+  if (total <= limit) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    uint32_t fm = ~(b[h][0] | b[h][1] | b[h][2]) & 0xFFu;
-    int64_t o = ebase + (h ? rank1 : rank0);
-    while (fm) {
-      const int i = __builtin_ctz(fm);
-      fm &= fm - 1;
-      const uint32_t x = (v[h][i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-      exps[o++] = (uint8_t)((x >> 7) & 0xFFu);
+    for (int h = 0; h < 2; ++h) {
+      uint32_t fm = ~(b[h][0] | b[h][1] | b[h][2]) & 0xFFu;
+      int64_t o = ebase + (h ? rank1 : rank0);
+      while (fm) {
+        const int i = __builtin_ctz(fm);
+        fm &= fm - 1;
+        const uint32_t x = (v[h][i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+        exps[o++] = (uint8_t)((x >> 7) & 0xFFu);
+      }
     }
   }
+  return total;
 }
 
 __global__ __launch_bounds__(256) void remit_kernel(const uint16_t* a, int M, int K,
@@ -249,6 +277,109 @@ __global__ __launch_bounds__(256) void remit_kernel(const uint16_t* a, int M, in
       classify8(v[h], st, b[h][0], b[h][1], b[h][2]);
     }
     emit_record(fixed, exps, rec, eoff[rec], v, b);
+  }
+}
+
+// Two-pass encoder (the input is read once after the window histogram):
+// rfixed_kernel writes every record's fixed part -- which does not depend
+// on where the outlier bytes go -- its outlier count, and up to kExpSlot of
+// its outlier bytes into a per-record slot of a temporary buffer; after the
+// scan of the counts, rcompact_kernel moves each record's slot to its place
+// in the exponent stream (a record with more outliers than the slot re-reads
+// its 16 x 64 input tile instead).  Same bytes as rcount + remit.
+constexpr int kExpSlot = ZS_RETILED_EXP_SLOT_BYTES;
+
+__global__ __launch_bounds__(256) void rfixed_kernel(const uint16_t* a, int M, int K,
+                                                     const int32_t* top, uint8_t* fixed,
+                                                     int32_t* counts, uint8_t* tmp) {
+  const uint32_t st = (uint32_t)(top[0] - 1) & 0xFFu;
+  const int64_t nrec = (int64_t)(M >> 4) * (K >> 6);
+  const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t rec = wid; rec < nrec; rec += nw) {
+    u32x4 v[2];
+    uint32_t b[2][3];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v[h] = *reinterpret_cast<const u32x4*>(rec_src(a, K, rec, h));
+      classify8(v[h], st, b[h][0], b[h][1], b[h][2]);
+    }
+    const int n = emit_record(fixed, tmp + rec * kExpSlot, rec, 0, v, b, kExpSlot);
+    if (lane_id() == 0) counts[rec] = n;
+  }
+}
+
+// Each wave takes kCompactRecs consecutive records: lane j < kCompactRecs
+// loads record r0 + j's offsets, the wave loads the slots of all of them at
+// once, then writes them one after another, lane l writing destination dword
+// d0 + l of the record's byte range [e0, e0 + n) (d0 = e0 / 4): whole dwords
+// with one aligned store (assembled from slot dwords l - 1 and l), the partial
+// first and last dwords -- shared with the neighbouring records -- byte by
+// byte.  Only the slot dwords that hold outlier bytes are read.  A record
+// with more outlier bytes than its slot holds is emitted from a re-read of
+// its input tile.  With n <= kExpSlot - 4 the lanes that write stay below
+// (n + 3 + 3) / 4 <= kExpSlot / 4, so slot dword l (and l - 1) is in range.
+// Few records per wave keep each wave's chain of dependent memory operations
+// short; the grid, not the wave, supplies the parallelism.
+constexpr int kExpFast = kExpSlot - 4;
+constexpr int kCompactRecs = 8;
+
+__global__ __launch_bounds__(256) void rcompact_kernel(const uint16_t* a, int M, int K,
+                                                       const int32_t* top, const int32_t* eoff,
+                                                       const uint8_t* __restrict__ tmp,
+                                                       uint8_t* __restrict__ exps) {
+  const uint32_t st = (uint32_t)(top[0] - 1) & 0xFFu;
+  const int64_t nrec = (int64_t)(M >> 4) * (K >> 6);
+  const uint32_t* tmp32 = reinterpret_cast<const uint32_t*>(tmp);
+  const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  const int l = lane_id();
+  for (int64_t r0 = wid * kCompactRecs; r0 < nrec; r0 += nw * kCompactRecs) {
+    const int cnt = (int)min<int64_t>(kCompactRecs, nrec - r0);
+    const int64_t rl = r0 + min(l, cnt - 1);
+    const int e0l = eoff[rl], nl = eoff[rl + 1] - e0l;
+    uint32_t cur[kCompactRecs], prev[kCompactRecs];
+#pragma unroll
+    for (int q = 0; q < kCompactRecs; ++q)
+      cur[q] = q < cnt && l < kExpSlot / 4 && 4 * l < __builtin_amdgcn_readlane(nl, q) + 4
+                   ? tmp32[(r0 + q) * (kExpSlot / 4) + l]
+                   : 0u;
+#pragma unroll
+    for (int q = 0; q < kCompactRecs; ++q) prev[q] = __shfl_up(cur[q], 1);
+    uint32_t slow = 0;  // records re-read from the input
+#pragma unroll
+    for (int q = 0; q < kCompactRecs; ++q) {
+      const int n = __builtin_amdgcn_readlane(nl, q);
+      const int e0 = __builtin_amdgcn_readlane(e0l, q);
+      if (q >= cnt || n == 0) continue;
+      if (n > kExpFast) {
+        slow |= 1u << q;
+        continue;
+      }
+      const int al = e0 & 3;
+      const int64_t p0 = (int64_t)(e0 & ~3) + 4 * l;  // stream byte of this dword
+      // slot bytes 4l - al .. 4l - al + 3
+      const uint32_t v = al == 0 ? cur[q] : __builtin_amdgcn_alignbyte(cur[q], prev[q], 4 - al);
+      if (p0 >= e0 && p0 + 4 <= e0 + n) {
+        *reinterpret_cast<uint32_t*>(exps + p0) = v;
+      } else {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          if (p0 + b >= e0 && p0 + b < e0 + n) exps[p0 + b] = (uint8_t)(v >> (8 * b));
+      }
+    }
+    while (slow) {
+      const int q = __builtin_ctz(slow);
+      slow &= slow - 1;
+      u32x4 x[2];
+      uint32_t bp[2][3];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        x[h] = *reinterpret_cast<const u32x4*>(rec_src(a, K, r0 + q, h));
+        classify8(x[h], st, bp[h][0], bp[h][1], bp[h][2]);
+      }
+      emit_exps(exps + __builtin_amdgcn_readlane(e0l, q), x, bp);
+    }
   }
 }
 
@@ -1379,6 +1510,37 @@ extern "C" int zs_compress_retiled_emit_gpu(void* stream, const uint16_t* d_inpu
   const int64_t nrec = (int64_t)(M / 16) * (K / 64);
   hipLaunchKernelGGL(remit_kernel, dim3(r_grid(nrec, 4)), dim3(256), 0, (hipStream_t)stream,
                      d_input, M, K, d_top_exponents, d_eoff, d_fixed, d_exps);
+  return status_of(hipGetLastError());
+}
+
+extern "C" int zs_compress_retiled_fixed_gpu(void* stream, const uint16_t* d_input, int M, int K,
+                                             const int32_t* d_top_exponents, uint8_t* d_fixed,
+                                             int32_t* d_counts, int32_t* d_eoff, int64_t* d_total,
+                                             uint8_t* d_tmp) {
+  if (!shape_ok(M, K) || !d_input || !d_top_exponents || !d_fixed || !d_counts || !d_eoff ||
+      !d_total || !d_tmp)
+    return ZS_E_INVAL;
+  if ((reinterpret_cast<uintptr_t>(d_input) & 15) || (reinterpret_cast<uintptr_t>(d_fixed) & 15))
+    return ZS_E_INVAL;
+  const int64_t nrec = (int64_t)(M / 16) * (K / 64);
+  if (nrec + 1 > INT32_MAX) return ZS_E_OVERFLOW;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(rfixed_kernel, dim3(r_grid(nrec, 4)), dim3(256), 0, st, d_input, M, K,
+                     d_top_exponents, d_fixed, d_counts, d_tmp);
+  launch_rscan(st, d_counts, nrec, d_eoff, d_total);
+  return status_of(hipGetLastError());
+}
+
+extern "C" int zs_compress_retiled_exps_gpu(void* stream, const uint16_t* d_input, int M, int K,
+                                            const int32_t* d_top_exponents, const int32_t* d_eoff,
+                                            const uint8_t* d_tmp, uint8_t* d_exps) {
+  if (!shape_ok(M, K) || !d_input || !d_top_exponents || !d_eoff || !d_tmp || !d_exps)
+    return ZS_E_INVAL;
+  if (reinterpret_cast<uintptr_t>(d_input) & 15) return ZS_E_INVAL;
+  const int64_t nrec = (int64_t)(M / 16) * (K / 64);
+  hipLaunchKernelGGL(rcompact_kernel, dim3(r_grid((nrec + kCompactRecs - 1) / kCompactRecs, 4)), dim3(256), 0,
+                     (hipStream_t)stream,
+                     d_input, M, K, d_top_exponents, d_eoff, d_tmp, d_exps);
   return status_of(hipGetLastError());
 }
 
