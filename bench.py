@@ -405,31 +405,33 @@ def traffic_from_profile(kernel):
 
 def compress_kernel_seconds(torch, zs, x, window="kv", reps=3):
     """Device time of the re-tiled GPU encoder's kernels on the bf16 matrix x
-    (window histogram + selection, fixed parts + counts + offset scan,
-    exponent-byte compaction), HIP events on the current stream, with every
-    buffer allocated beforehand so that no host size synchronisation sits
-    between the phases (compress_retiled needs one to size the stream)."""
+    (window guess from a sample, fixed parts + counts + full histogram in one
+    input pass, window check -- a second pass only when the guess was wrong --
+    offset scan, exponent-byte compaction), HIP events on the current stream,
+    with every buffer allocated beforehand so that no host size
+    synchronisation sits between the phases (compress_retiled needs one to
+    size the stream)."""
     L = zs.lib()
     rows, cols = x.shape
     nrec = rows // 16 * (cols // 64)
     dev = x.device
     i32 = dict(dtype=torch.int32, device=dev)
-    top, counts = torch.empty(7, **i32), torch.empty(256, dtype=torch.int64, device=dev)
+    top, hist = torch.empty(7, **i32), torch.empty(256, dtype=torch.int64, device=dev)
     cnt, eoff = torch.empty(nrec, **i32), torch.empty(nrec + 1, **i32)
     total = torch.empty(1, dtype=torch.int64, device=dev)
     fixed = torch.empty(nrec * 1408, dtype=torch.uint8, device=dev)
     tmp = torch.empty(nrec * zs._lib.ZS_RETILED_EXP_SLOT_BYTES, dtype=torch.uint8, device=dev)
+    work = torch.empty(zs._lib.ZS_RETILED_AUTO_WORK_BYTES, dtype=torch.uint8, device=dev)
     nexp = zs.compress_retiled(x, window=window).num_outliers
     exps = torch.empty(nexp + 64, dtype=torch.uint8, device=dev)
-    analyze = (L.zs_analyze_top_exponents_u64_gpu if window == "kv"
-               else L.zs_analyze_exponents_weights_gpu)
+    rule = zs._lib.ZS_WINDOW_KV if window == "kv" else zs._lib.ZS_WINDOW_WEIGHTS
 
     def run():
         st = torch.cuda.current_stream().cuda_stream
-        assert analyze(st, x.data_ptr(), x.numel(), counts.data_ptr(), top.data_ptr()) == 0
-        assert L.zs_compress_retiled_fixed_gpu(st, x.data_ptr(), rows, cols, top.data_ptr(),
-                                               fixed.data_ptr(), cnt.data_ptr(), eoff.data_ptr(),
-                                               total.data_ptr(), tmp.data_ptr()) == 0
+        assert L.zs_compress_retiled_auto_gpu(st, x.data_ptr(), rows, cols, rule, hist.data_ptr(),
+                                              top.data_ptr(), work.data_ptr(), fixed.data_ptr(),
+                                              cnt.data_ptr(), eoff.data_ptr(), total.data_ptr(),
+                                              tmp.data_ptr()) == 0
         assert L.zs_compress_retiled_exps_gpu(st, x.data_ptr(), rows, cols, top.data_ptr(),
                                               eoff.data_ptr(), tmp.data_ptr(), exps.data_ptr()) == 0
     run()

@@ -47,6 +47,13 @@ extern "C" {
 #define ZS_STREAM_SLACK_BYTES 64
 /* Bytes of d_tmp per 16 x 64 record for zs_compress_retiled_fixed_gpu. */
 #define ZS_RETILED_EXP_SLOT_BYTES 256
+/* Window rules of zs_compress_retiled_auto_gpu: the KV-cache compressor's
+ * (zipserv_decode_attention_ext.cu:65-134) and the weight path's
+ * (kernel_benchmark/utils.h:189-272). */
+#define ZS_WINDOW_KV 0
+#define ZS_WINDOW_WEIGHTS 1
+/* Scratch bytes (d_work) of zs_compress_retiled_auto_gpu. */
+#define ZS_RETILED_AUTO_WORK_BYTES 40960
 
 /* KV layouts of a compressed cache (flash.h:19-20). */
 #define ZS_LAYOUT_HEAD_MAJOR 0 /* rows = ((b * Hkv + h) * rows_per_head + t) */
@@ -207,6 +214,21 @@ int zs_compress_retiled_fixed_gpu(void* stream, const uint16_t* d_input, int M, 
                                   const int32_t* d_top_exponents, uint8_t* d_fixed,
                                   int32_t* d_counts, int32_t* d_eoff, int64_t* d_total,
                                   uint8_t* d_tmp);
+/* zs_analyze_* + zs_compress_retiled_fixed_gpu in one input pass (when the
+ * guess holds): the window (rule ZS_WINDOW_KV or ZS_WINDOW_WEIGHTS) is
+ * guessed from every 32nd 4096-byte chunk of the input, the fixed parts,
+ * counts and slots are written under the guess while the full exponent
+ * histogram is counted (d_hist, 256 x uint64, out), the rule picks the window
+ * from the full histogram (d_top, out), and only if it differs from the guess
+ * are the fixed parts, counts and slots written again under it.  Outputs are
+ * those of zs_analyze_* (u64 bins) followed by zs_compress_retiled_fixed_gpu
+ * with d_top.  d_work: ZS_RETILED_AUTO_WORK_BYTES of device scratch (8-byte
+ * aligned).  No counterpart in the reference, whose compressor reads its
+ * input once for the histogram and once more per encoding pass. */
+int zs_compress_retiled_auto_gpu(void* stream, const uint16_t* d_input, int M, int K, int rule,
+                                 uint64_t* d_hist, int32_t* d_top, uint8_t* d_work,
+                                 uint8_t* d_fixed, int32_t* d_counts, int32_t* d_eoff,
+                                 int64_t* d_total, uint8_t* d_tmp);
 int zs_compress_retiled_exps_gpu(void* stream, const uint16_t* d_input, int M, int K,
                                  const int32_t* d_top_exponents, const int32_t* d_eoff,
                                  const uint8_t* d_tmp, uint8_t* d_exps);

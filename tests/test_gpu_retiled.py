@@ -379,3 +379,89 @@ def test_two_pass_encoder_equals_three_pass(torch_cuda, kind):
     assert torch.equal(fixed2, fixed3) and torch.equal(exps2, exps3)
     if kind in ("random_bits", "zeros"):
         assert int(cnt2.max()) > 256  # the re-read path ran
+
+
+_DIFFERS = 16 * 256 * 8 + 2048 + 32  # the flag's byte offset in the auto encoder's scratch
+
+
+def _guess_miss_matrix(rng, M, K):
+    """Sampled chunks (every 32nd run of 2048 elements) hold exponents near 100,
+    the rest near 120, so the sample's window is not the full histogram's."""
+    W = np.empty(M * K, np.uint16)
+    chunks = W.reshape(-1, 2048)
+    for c in range(chunks.shape[0]):
+        base = 100 if c % 32 == 0 else 120
+        e = rng.integers(base - 3, base + 4, 2048).astype(np.uint16)
+        chunks[c] = (e << 7) | rng.integers(0, 128, 2048, dtype=np.uint16)
+    return W.reshape(M, K)
+
+
+@pytest.mark.parametrize("rule", ["kv", "weights"])
+@pytest.mark.parametrize("kind", ["weights", "kv", "random_bits", "zeros", "guess_miss"])
+def test_one_pass_encoder_equals_analyze_then_fixed(torch_cuda, kind, rule):
+    # zs_compress_retiled_auto_gpu (window guessed from a sample, histogram
+    # counted during the encoding pass, second pass only on a wrong guess)
+    # against zs_analyze_* followed by zs_compress_retiled_fixed_gpu / _exps_gpu
+    torch = torch_cuda
+    L = zs.lib()
+    rng = np.random.default_rng(92)
+    if kind == "weights":
+        W = weights_bf16(rng, (1024, 2048), outlier_frac=0.01)
+    elif kind == "kv":
+        W, _ = pad_by_kv_head(kv_bf16(rng, 2, 300, 8, 128))
+    elif kind == "random_bits":
+        W = rng.integers(0, 65536, size=(128, 256), dtype=np.uint16)
+    elif kind == "zeros":
+        W = np.zeros((64, 192), np.uint16)
+    else:
+        W = _guess_miss_matrix(rng, 512, 4096)
+    x = to_torch_bf16(W)
+    M, K = W.shape
+    nrec = M // 16 * (K // 64)
+    st = int(torch.cuda.current_stream().cuda_stream)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    want_top = zo.analyze_gpu(W) if rule == "kv" else zo.analyze_cpu(W)
+    u8 = dict(dtype=torch.uint8, device="cuda")
+    outs = []
+    for path in ("auto", "two_step"):
+        hist, top = torch.empty(256, dtype=torch.int64, device="cuda"), torch.empty(7, **i32)
+        cnt, eoff = torch.empty(nrec, **i32), torch.empty(nrec + 1, **i32)
+        tot = torch.empty(1, dtype=torch.int64, device="cuda")
+        fixed, tmp = torch.empty(nrec * 1408, **u8), torch.empty(nrec * 256, **u8)
+        work = torch.empty(zs._lib.ZS_RETILED_AUTO_WORK_BYTES, **u8)
+        if path == "auto":
+            r = zs._lib.ZS_WINDOW_KV if rule == "kv" else zs._lib.ZS_WINDOW_WEIGHTS
+            assert L.zs_compress_retiled_auto_gpu(st, x.data_ptr(), M, K, r, hist.data_ptr(),
+                                                  top.data_ptr(), work.data_ptr(),
+                                                  fixed.data_ptr(), cnt.data_ptr(),
+                                                  eoff.data_ptr(), tot.data_ptr(),
+                                                  tmp.data_ptr()) == 0
+        else:
+            fn = (L.zs_analyze_top_exponents_u64_gpu if rule == "kv"
+                  else L.zs_analyze_exponents_weights_gpu)
+            assert fn(st, x.data_ptr(), W.size, hist.data_ptr(), top.data_ptr()) == 0
+            assert L.zs_compress_retiled_fixed_gpu(st, x.data_ptr(), M, K, top.data_ptr(),
+                                                   fixed.data_ptr(), cnt.data_ptr(),
+                                                   eoff.data_ptr(), tot.data_ptr(),
+                                                   tmp.data_ptr()) == 0
+        total = int(tot.item())
+        exps = torch.zeros(total + 64, **u8)
+        assert L.zs_compress_retiled_exps_gpu(st, x.data_ptr(), M, K, top.data_ptr(),
+                                              eoff.data_ptr(), tmp.data_ptr(),
+                                              exps.data_ptr()) == 0
+        torch.cuda.synchronize()
+        differs = int(work[_DIFFERS:_DIFFERS + 4].view(torch.int32).item()) if path == "auto" else None
+        outs.append((hist, top, cnt, eoff, total, fixed, exps, differs))
+    (h1, t1, c1, e1, n1, f1, x1, differs), (h2, t2, c2, e2, n2, f2, x2, _) = outs
+    np.testing.assert_array_equal(h1.cpu().numpy(), zo.histogram(W))
+    assert torch.equal(h1, h2)
+    assert t1.cpu().tolist() == want_top == t2.cpu().tolist()
+    assert n1 == n2 and torch.equal(c1, c2) and torch.equal(e1, e2)
+    assert torch.equal(f1, f2) and torch.equal(x1, x2)
+    if kind == "guess_miss":
+        assert differs == 1  # the second pass ran
+    elif kind in ("weights", "kv"):
+        assert differs == 0
+    r = zo.compress_retiled(W, (want_top[0] - 1) & 0xFF)
+    np.testing.assert_array_equal(f1.cpu().numpy(), r.fixed)
+    np.testing.assert_array_equal(x1[:n1].cpu().numpy(), r.exps[:n1])

@@ -20,6 +20,9 @@ ZS_E_OVERFLOW = -3
 ZS_E_NOMEM = -4
 ZS_STREAM_SLACK_BYTES = 64
 ZS_RETILED_EXP_SLOT_BYTES = 256
+ZS_WINDOW_KV = 0
+ZS_WINDOW_WEIGHTS = 1
+ZS_RETILED_AUTO_WORK_BYTES = 40960
 ZS_LAYOUT_HEAD_MAJOR = 0
 ZS_LAYOUT_TOKEN_MAJOR = 1
 
@@ -62,6 +65,8 @@ SIGNATURES = {
     "zs_compress_retiled_emit_gpu": (C.c_int, [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p]),
     "zs_compress_retiled_fixed_gpu": (C.c_int, [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p, _p,
                                                 _p]),
+    "zs_compress_retiled_auto_gpu": (C.c_int, [_p, _p, C.c_int, C.c_int, C.c_int, _p, _p, _p, _p, _p,
+                                               _p, _p, _p]),
     "zs_compress_retiled_exps_gpu": (C.c_int, [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p]),
     "zs_retile_triple_bitmap_count_gpu": (
         C.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, C.c_int, C.c_int, _p, _p, _p]),

@@ -486,7 +486,9 @@ def compress_retiled(input, logical_rows=None, logical_cols=None, layout="by_kv_
     """bf16 [rows, cols] on the GPU -> re-tiled layout.  The window is chosen on
     the GPU, by default with the rule of zipserv_decode_attention_ext.cu:35-135
     ("kv"); "weights" applies kernel_benchmark/utils.h:189-272 instead (see
-    _device_window)."""
+    _device_window).  Under a rule the encoder reads the input once when the
+    window guessed from a sample of it is the rule's (zs_compress_retiled_auto_gpu),
+    twice otherwise; an explicit window is one more input pass."""
     torch = _torch()
     _check_cuda(input, "input", torch.bfloat16)
     if input.dim() != 2:
@@ -504,11 +506,22 @@ def compress_retiled(input, logical_rows=None, logical_cols=None, layout="by_kv_
     fixed = torch.empty(nrec * 1408, dtype=torch.uint8, device=dev)
     tmp = torch.empty(nrec * _lib.ZS_RETILED_EXP_SLOT_BYTES, dtype=torch.uint8, device=dev)
     st = _stream()
-    # 64-bit bins: the re-tiled layout takes matrices past 2^31 elements.
-    _device_window(input, window, top, counts)
-    check("zs_compress_retiled_fixed_gpu",
-          L.zs_compress_retiled_fixed_gpu(st, _dptr(input), rows, cols, _dptr(top), _dptr(fixed),
-                                          _dptr(cnt), _dptr(eoff), _dptr(total), _dptr(tmp)))
+    if isinstance(window, str):
+        if window not in WINDOW_RULES:
+            raise ValueError(f"window must be one of {WINDOW_RULES} or 7 exponents")
+        rule = _lib.ZS_WINDOW_KV if window == "kv" else _lib.ZS_WINDOW_WEIGHTS
+        work = torch.empty(_lib.ZS_RETILED_AUTO_WORK_BYTES, dtype=torch.uint8, device=dev)
+        # 64-bit bins: the re-tiled layout takes matrices past 2^31 elements.
+        check("zs_compress_retiled_auto_gpu",
+              L.zs_compress_retiled_auto_gpu(st, _dptr(input), rows, cols, rule, _dptr(counts),
+                                             _dptr(top), _dptr(work), _dptr(fixed), _dptr(cnt),
+                                             _dptr(eoff), _dptr(total), _dptr(tmp)))
+    else:
+        _device_window(input, window, top, counts)
+        check("zs_compress_retiled_fixed_gpu",
+              L.zs_compress_retiled_fixed_gpu(st, _dptr(input), rows, cols, _dptr(top),
+                                              _dptr(fixed), _dptr(cnt), _dptr(eoff),
+                                              _dptr(total), _dptr(tmp)))
     tot, top0 = int(total.item()), int(top[0].item())  # synchronises (sizes the stream)
     if tot > 2**31 - 1:
         raise OverflowError("outlier count exceeds the int32 offsets")

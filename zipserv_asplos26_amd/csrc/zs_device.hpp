@@ -24,6 +24,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
+// Histogram slices of the one-pass re-tiled encoder (zs_retiled.hip writes
+// them, zs_encode.hip's window check sums them).
+constexpr int kVerifySlices = 16;
+
 // LDS lookup tables used by the row decoder.  Indexed by one bitmap byte
 // (8 positions of a small-tile row); each entry is four dwords = eight 16-bit
 // lanes, lane j for position j.

@@ -87,6 +87,40 @@ __global__ __launch_bounds__(kHistThreads) void hist_kernel(const uint16_t* in, 
   }
 }
 
+// Histogram of every kSampleStride-th 4096-byte chunk of the input (the
+// window guess of the one-pass re-tiled encoder); bins as hist_kernel's.
+constexpr int kSampleStride = 32;
+
+__global__ __launch_bounds__(kHistThreads) void sample_hist_kernel(const uint16_t* in,
+                                                                   int64_t nchunks,
+                                                                   uint64_t* counts) {
+  __shared__ uint32_t h[kHistCopies * kHistPitch];
+  for (int i = threadIdx.x; i < kHistCopies * kHistPitch; i += kHistThreads) h[i] = 0;
+  __syncthreads();
+  uint32_t* hc = h + lane_id() * kHistPitch;
+  const uint4* v = reinterpret_cast<const uint4*>(in);
+  const int64_t nvec = (nchunks + kSampleStride - 1) / kSampleStride * 256;
+  const int64_t nthreads = (int64_t)gridDim.x * kHistThreads;
+  auto at = [&](int64_t i) { return v + (i >> 8) * (256 * kSampleStride) + (i & 255); };
+  int64_t i = (int64_t)blockIdx.x * kHistThreads + threadIdx.x;
+  for (; i + 3 * nthreads < nvec; i += 4 * nthreads) {  // four 16-byte loads in flight
+    const uint4 x0 = nt_load16(at(i)), x1 = nt_load16(at(i + nthreads)),
+                x2 = nt_load16(at(i + 2 * nthreads)), x3 = nt_load16(at(i + 3 * nthreads));
+    hist_add8(hc, x0);
+    hist_add8(hc, x1);
+    hist_add8(hc, x2);
+    hist_add8(hc, x3);
+  }
+  for (; i < nvec; i += nthreads) hist_add8(hc, nt_load16(at(i)));
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    uint32_t c = 0;
+    for (int k = 0; k < kHistCopies; ++k) c += h[k * kHistPitch + threadIdx.x];
+    if (c) atomicAdd(reinterpret_cast<unsigned long long*>(&counts[threadIdx.x]),
+                     (unsigned long long)c);
+  }
+}
+
 __device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), lane);
@@ -102,7 +136,8 @@ __device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
 // candidates stay in registers (a dynamic index would put them in scratch
 // memory, one memory round trip per access).
 __device__ __forceinline__ void window_from_candidates(const int64_t* counts, int (&cand)[7],
-                                                       bool clamp, int32_t* top) {
+                                                       bool clamp, int32_t* top,
+                                                       const int32_t* guess, int32_t* differs) {
 #pragma unroll
   for (int i = 0; i < 6; ++i)  // bubble sort; ties are equal values, so any sort agrees
 #pragma unroll
@@ -135,6 +170,7 @@ __device__ __forceinline__ void window_from_candidates(const int64_t* counts, in
   }
 #pragma unroll
   for (int i = 0; i < 7; ++i) top[i] = win + i;
+  if (guess) *differs = guess[0] != win;  // windows are 7 consecutive exponents
 }
 
 // Seven wave-wide maxima of key = (count << 8 | 255 - exponent) over the
@@ -168,13 +204,26 @@ __device__ __forceinline__ int top7_passes(int64_t (&key)[4], int l, int (&cand)
   return taken;
 }
 
+// Count of exponent e: the sum of nslices histograms 256 bins apart; written
+// back to sum_out (when given) as the one histogram.
+template <int NS, typename C>
+__device__ __forceinline__ int64_t load_count(const C* counts_g, int e, uint64_t* sum_out) {
+  int64_t c = 0;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) c += (int64_t)counts_g[256 * s + e];
+  if (sum_out) sum_out[e] = (uint64_t)c;
+  return c;
+}
+
 // Window selection of zipserv_decode_attention_ext.cu:65-134: seven slots
 // start at count -1 (so zero counts can be taken); each exponent 0..255
 // replaces the first minimum slot on strictly greater count; candidates are
 // sorted, the first one starting 7 present exponents wins, else the start of
 // the longest consecutive run, clamped to [0, 248].
-template <typename C>
-__global__ __launch_bounds__(64) void select_kernel(const C* counts_g, int32_t* top) {
+template <typename C, int NS = 1>
+__global__ __launch_bounds__(64) void select_kernel(const C* counts_g,
+                                                   uint64_t* sum_out, int32_t* top,
+                                                   const int32_t* guess, int32_t* differs) {
   // One wave.  Lane i holds the counts of exponents i, i+64, i+128, i+192;
   // the streaming top-7 below runs on wave-uniform values (scalar unit),
   // reading each count with v_readlane instead of a dependent memory load.
@@ -182,7 +231,7 @@ __global__ __launch_bounds__(64) void select_kernel(const C* counts_g, int32_t* 
   const int l = threadIdx.x;
   int64_t cv[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) cv[k] = (int64_t)counts_g[64 * k + l];
+  for (int k = 0; k < 4; ++k) cv[k] = load_count<NS>(counts_g, 64 * k + l, sum_out);
   __shared__ int64_t counts[256];
 #pragma unroll
   for (int k = 0; k < 4; ++k) counts[64 * k + l] = cv[k];
@@ -202,7 +251,7 @@ __global__ __launch_bounds__(64) void select_kernel(const C* counts_g, int32_t* 
 #pragma unroll
       for (int k = 0; k < 4; ++k) ge += __builtin_popcountll(__builtin_amdgcn_ballot_w64(cv[k] >= c7));
       if (ge == 7) {
-        if (l == 0) window_from_candidates(counts, cand, true, top);
+        if (l == 0) window_from_candidates(counts, cand, true, top, guess, differs);
         return;
       }
     }
@@ -249,7 +298,7 @@ __global__ __launch_bounds__(64) void select_kernel(const C* counts_g, int32_t* 
   int cand[7];
 #pragma unroll
   for (int i = 0; i < 7; ++i) cand[i] = te[i] >= 0 ? te[i] : 127 - i;
-  window_from_candidates(counts, cand, true, top);
+  window_from_candidates(counts, cand, true, top, guess, differs);
 }
 
 
@@ -260,15 +309,18 @@ __global__ __launch_bounds__(64) void select_kernel(const C* counts_g, int32_t* 
 // the tail is select_kernel's without the [0, 248] clamp.  One wave; lane i
 // holds exponents i, i + 64, i + 128, i + 192; a pass is one wave-wide
 // maximum of (count << 8 | 255 - exponent) over the exponents not taken.
-template <typename C>
-__global__ __launch_bounds__(64) void select_weights_kernel(const C* counts_g, int32_t* top) {
+template <typename C, int NS = 1>
+__global__ __launch_bounds__(64) void select_weights_kernel(const C* counts_g,
+                                                           uint64_t* sum_out, int32_t* top,
+                                                           const int32_t* guess,
+                                                           int32_t* differs) {
   if (blockIdx.x != 0) return;
   const int l = threadIdx.x;
   __shared__ int64_t counts[256];
   int64_t key[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const int64_t c = (int64_t)counts_g[64 * k + l];
+    const int64_t c = load_count<NS>(counts_g, 64 * k + l, sum_out);
     counts[64 * k + l] = c;
     // counts stay below 2^55 (numel < 2^63 / 256 is far past any tensor)
     key[k] = c > 0 ? (c << 8) | (255 - (64 * k + l)) : 0;
@@ -278,7 +330,7 @@ __global__ __launch_bounds__(64) void select_weights_kernel(const C* counts_g, i
   int64_t c7;
   top7_passes(key, l, cand, &c7);
   if (l != 0) return;
-  window_from_candidates(counts, cand, false, top);
+  window_from_candidates(counts, cand, false, top, guess, differs);
 }
 
 
@@ -623,11 +675,52 @@ static int analyze(hipStream_t st, const uint16_t* d_input, int64_t numel, C* d_
   hipLaunchKernelGGL(hist_kernel<C>, dim3((unsigned)blocks), dim3(kHistThreads), 0, st, d_input, numel,
                      d_counts);
   if (weights_rule)
-    hipLaunchKernelGGL(select_weights_kernel<C>, dim3(1), dim3(64), 0, st, d_counts, d_top);
+    hipLaunchKernelGGL(select_weights_kernel<C>, dim3(1), dim3(64), 0, st, d_counts, nullptr, d_top,
+                       nullptr, nullptr);
   else
-    hipLaunchKernelGGL(select_kernel<C>, dim3(1), dim3(64), 0, st, d_counts, d_top);
+    hipLaunchKernelGGL(select_kernel<C>, dim3(1), dim3(64), 0, st, d_counts, nullptr, d_top,
+                       nullptr, nullptr);
   return hip_status(hipGetLastError());
 }
+
+namespace zs {
+
+// Window guess from a sample of the input (chunks of 2048 elements; numel a
+// multiple of 2048, input 16-byte aligned; counts zeroed by the caller).
+hipError_t launch_window_sample(hipStream_t st, const uint16_t* in, int64_t numel,
+                                bool weights_rule, uint64_t* counts, int32_t* guess) {
+  const int64_t nchunks = numel / 2048;
+  const int64_t nvec = (nchunks + kSampleStride - 1) / kSampleStride * 256;
+  // Few workgroups: each ends with up to 256 atomics on the same 256 bins.
+  const int blocks = (int)std::max<int64_t>(
+      1, std::min<int64_t>((nvec + 4 * kHistThreads - 1) / (4 * kHistThreads),
+                           device_cu_count() / 2));
+  hipLaunchKernelGGL(sample_hist_kernel, dim3(blocks), dim3(kHistThreads), 0, st, in, nchunks,
+                     counts);
+  if (weights_rule)
+    hipLaunchKernelGGL(select_weights_kernel<uint64_t>, dim3(1), dim3(64), 0, st, counts,
+                       nullptr, guess, nullptr, nullptr);
+  else
+    hipLaunchKernelGGL(select_kernel<uint64_t>, dim3(1), dim3(64), 0, st, counts, nullptr,
+                       guess, nullptr, nullptr);
+  return hipGetLastError();
+}
+
+// The window of the full histogram (the sum of kVerifySlices histograms 256
+// bins apart, also written to hist), and whether it differs from the guess.
+hipError_t launch_window_verify(hipStream_t st, bool weights_rule, const uint64_t* slices,
+                                uint64_t* hist, int32_t* top, const int32_t* guess,
+                                int32_t* differs) {
+  if (weights_rule)
+    hipLaunchKernelGGL((select_weights_kernel<uint64_t, kVerifySlices>), dim3(1), dim3(64), 0, st,
+                       slices, hist, top, guess, differs);
+  else
+    hipLaunchKernelGGL((select_kernel<uint64_t, kVerifySlices>), dim3(1), dim3(64), 0, st, slices,
+                       hist, top, guess, differs);
+  return hipGetLastError();
+}
+
+}  // namespace zs
 
 extern "C" int zs_analyze_top_exponents_gpu(void* stream, const uint16_t* d_input, int64_t numel,
                                             int32_t* d_counts, int32_t* d_top,

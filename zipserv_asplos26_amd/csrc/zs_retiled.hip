@@ -289,13 +289,30 @@ __global__ __launch_bounds__(256) void remit_kernel(const uint16_t* a, int M, in
 // its 16 x 64 input tile instead).  Same bytes as rcount + remit.
 constexpr int kExpSlot = ZS_RETILED_EXP_SLOT_BYTES;
 
+// kHist: also the exponent histogram of the input, added to hist (64-bit
+// bins): in-window elements counted per code from the bit-planes, outliers
+// from their exponent bytes.  Workgroup b adds its bins to slice b % kHistSlices
+// of hist (kHistSlices histograms 256 bins apart), which spreads the
+// same-address atomics of the workgroups over more addresses.  redo: a flag;
+// when it is zero the launch does nothing (the one-pass encoder's first pass
+// already used the right window).
+constexpr int kHistSlices = kVerifySlices;
+template <bool kHist>
 __global__ __launch_bounds__(256) void rfixed_kernel(const uint16_t* a, int M, int K,
                                                      const int32_t* top, uint8_t* fixed,
-                                                     int32_t* counts, uint8_t* tmp) {
+                                                     int32_t* counts, uint8_t* tmp,
+                                                     uint64_t* hist, const int32_t* redo) {
+  if (!kHist && redo && *redo == 0) return;
+  __shared__ uint32_t lh[kHist ? 256 : 1];
+  if constexpr (kHist) {
+    lh[threadIdx.x] = 0;
+    __syncthreads();
+  }
   const uint32_t st = (uint32_t)(top[0] - 1) & 0xFFu;
   const int64_t nrec = (int64_t)(M >> 4) * (K >> 6);
   const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  uint32_t cc[7] = {0, 0, 0, 0, 0, 0, 0};  // this lane's elements with code 1..7
   for (int64_t rec = wid; rec < nrec; rec += nw) {
     u32x4 v[2];
     uint32_t b[2][3];
@@ -304,8 +321,40 @@ __global__ __launch_bounds__(256) void rfixed_kernel(const uint16_t* a, int M, i
       v[h] = *reinterpret_cast<const u32x4*>(rec_src(a, K, rec, h));
       classify8(v[h], st, b[h][0], b[h][1], b[h][2]);
     }
+    if constexpr (kHist) {
+      const uint32_t p1 = b[0][0] | (b[1][0] << 8), p2 = b[0][1] | (b[1][1] << 8),
+                     p3 = b[0][2] | (b[1][2] << 8);
+#pragma unroll
+      for (int c = 1; c <= 7; ++c)
+        cc[c - 1] += __builtin_popcount((c & 1 ? p1 : ~p1) & (c & 2 ? p2 : ~p2) &
+                                        (c & 4 ? p3 : ~p3) & 0xFFFFu);
+    }
     const int n = emit_record(fixed, tmp + rec * kExpSlot, rec, 0, v, b, kExpSlot);
+    if constexpr (kHist) {
+      // outlier exponents into the workgroup's LDS bins
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint32_t fm = ~(b[h][0] | b[h][1] | b[h][2]) & 0xFFu;
+        while (fm) {
+          const int i = __builtin_ctz(fm);
+          fm &= fm - 1;
+          atomicAdd(&lh[(v[h][i >> 1] >> (16 * (i & 1) + 7)) & 0xFFu], 1u);
+        }
+      }
+    }
     if (lane_id() == 0) counts[rec] = n;
+  }
+  if constexpr (kHist) {
+#pragma unroll
+    for (int c = 0; c < 7; ++c) {
+      const int tot = wave_sum((int)cc[c]);
+      if (lane_id() == 0 && tot) atomicAdd(&lh[(st + 1 + c) & 0xFFu], (uint32_t)tot);
+    }
+    __syncthreads();
+    if (lh[threadIdx.x])
+      atomicAdd(reinterpret_cast<unsigned long long*>(
+                    &hist[256 * (blockIdx.x % kHistSlices) + threadIdx.x]),
+                (unsigned long long)lh[threadIdx.x]);
   }
 }
 
@@ -427,6 +476,13 @@ __global__ __launch_bounds__(256) void remit_canon_kernel(Streams s, int start_e
 // ---------------------------------------------------------------------------
 constexpr int kDecWaves = 8, kDecDepth = 3;
 int device_cu_count();  // zs_gemm.hip
+// zs_encode.hip: the window guessed from a sample of the input, and the
+// window of a full histogram with a flag saying whether it differs.
+hipError_t launch_window_sample(hipStream_t st, const uint16_t* in, int64_t numel,
+                                bool weights_rule, uint64_t* counts, int32_t* guess);
+hipError_t launch_window_verify(hipStream_t st, bool weights_rule, const uint64_t* slices,
+                                uint64_t* hist, int32_t* top, const int32_t* guess,
+                                int32_t* differs);
 
 __global__ __launch_bounds__(kDecWaves * 64) void rdecompress_kernel(const uint8_t* fixed,
                                                                      const uint8_t* exps,
@@ -1525,8 +1581,53 @@ extern "C" int zs_compress_retiled_fixed_gpu(void* stream, const uint16_t* d_inp
   const int64_t nrec = (int64_t)(M / 16) * (K / 64);
   if (nrec + 1 > INT32_MAX) return ZS_E_OVERFLOW;
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(rfixed_kernel, dim3(r_grid(nrec, 4)), dim3(256), 0, st, d_input, M, K,
-                     d_top_exponents, d_fixed, d_counts, d_tmp);
+  hipLaunchKernelGGL(rfixed_kernel<false>, dim3(r_grid(nrec, 4)), dim3(256), 0, st, d_input, M,
+                     K, d_top_exponents, d_fixed, d_counts, d_tmp, nullptr, nullptr);
+  launch_rscan(st, d_counts, nrec, d_eoff, d_total);
+  return status_of(hipGetLastError());
+}
+
+__global__ void zero_u64_kernel(uint64_t* a, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) a[i] = 0;
+}
+
+// d_work: kHistSlices histogram slices, the sample histogram, the guessed
+// window and the flag that says whether the full histogram's window differs.
+constexpr int kWorkSample = kHistSlices * 256 * 8, kWorkGuess = kWorkSample + 2048,
+              kWorkDiffers = kWorkGuess + 32;
+static_assert(kWorkDiffers + 4 <= ZS_RETILED_AUTO_WORK_BYTES, "auto encoder scratch");
+
+extern "C" int zs_compress_retiled_auto_gpu(void* stream, const uint16_t* d_input, int M, int K,
+                                            int rule, uint64_t* d_hist, int32_t* d_top,
+                                            uint8_t* d_work, uint8_t* d_fixed, int32_t* d_counts,
+                                            int32_t* d_eoff, int64_t* d_total, uint8_t* d_tmp) {
+  if (!shape_ok(M, K) || !d_input || !d_hist || !d_top || !d_work || !d_fixed || !d_counts ||
+      !d_eoff || !d_total || !d_tmp || (rule != ZS_WINDOW_KV && rule != ZS_WINDOW_WEIGHTS))
+    return ZS_E_INVAL;
+  if ((reinterpret_cast<uintptr_t>(d_input) & 15) || (reinterpret_cast<uintptr_t>(d_fixed) & 15) ||
+      (reinterpret_cast<uintptr_t>(d_hist) & 7) || (reinterpret_cast<uintptr_t>(d_work) & 7))
+    return ZS_E_INVAL;
+  const int64_t nrec = (int64_t)(M / 16) * (K / 64);
+  if (nrec + 1 > INT32_MAX) return ZS_E_OVERFLOW;
+  hipStream_t st = (hipStream_t)stream;
+  const bool weights = rule == ZS_WINDOW_WEIGHTS;
+  uint64_t* slices = reinterpret_cast<uint64_t*>(d_work);
+  uint64_t* sample = reinterpret_cast<uint64_t*>(d_work + kWorkSample);
+  int32_t* guess = reinterpret_cast<int32_t*>(d_work + kWorkGuess);
+  int32_t* differs = reinterpret_cast<int32_t*>(d_work + kWorkDiffers);
+  hipLaunchKernelGGL(zero_u64_kernel, dim3(1), dim3(1024), 0, st, slices,
+                     (kHistSlices + 1) * 256);
+  hipError_t e = launch_window_sample(st, d_input, (int64_t)M * K, weights, sample, guess);
+  if (e != hipSuccess) return status_of(e);
+  const int hist_grid = r_grid(nrec, 4);
+  hipLaunchKernelGGL(rfixed_kernel<true>, dim3(hist_grid), dim3(256), 0, st, d_input, M, K, guess,
+                     d_fixed, d_counts, d_tmp, slices, nullptr);
+  e = launch_window_verify(st, weights, slices, d_hist, d_top, guess, differs);
+  if (e != hipSuccess) return status_of(e);
+  // Usually a no-op: a small grid keeps the launch cheap.
+  hipLaunchKernelGGL(rfixed_kernel<false>, dim3(std::min(r_grid(nrec, 4), device_cu_count() * 4)),
+                     dim3(256), 0, st, d_input, M, K, d_top, d_fixed, d_counts, d_tmp, nullptr,
+                     differs);
   launch_rscan(st, d_counts, nrec, d_eoff, d_total);
   return status_of(hipGetLastError());
 }
