@@ -366,10 +366,11 @@ def bench_kv(torch, zs, dev, gen):
 
 def kernel_name(N, M, split_k):
     """Kernel that zs_retiled_mm launches for batch N (mirrors its dispatch):
-    N <= 16 -> rgemm_kernel<F, 1, W, D> (F bands per wave: 2 when N > 8 and
-    M/16 >= 384, else 1; one 16-column block; W = 4 waves when N > 1 and
+    N <= 16 -> rgemm_kernel<F, 1, W, D, XD> (F bands per wave: 2 when N > 8
+    and M/16 >= 384, else 1; one 16-column block; W = 4 waves when N > 1 and
     M/16 >= 640, else 8; records D = 4 tiles ahead with one band per wave, 3
-    with two); N > 16 ->
+    with two; X staged through LDS in XD-row loads: 1 for N <= 2, 2 for
+    N <= 4, 4 for N <= 8, none (0) above); N > 16 ->
     rgemm_wide_kernel<NB, 4, PH, 2> with NB = 2, 4 or 8
     column blocks, 4 row bands, 4 K phases when M/64 * split_k < 384 (2
     otherwise), records 2 steps ahead; N > 32 on grids of >= 160 128-row
@@ -378,7 +379,8 @@ def kernel_name(N, M, split_k):
     if nb <= 1:
         waves = 4 if (N > 1 and M // 16 >= 640) else 8
         f = 2 if (N > 8 and M // 16 >= 384) else 1
-        return f"zs::rgemm_kernel<{f}, 1, {waves}, {4 if f == 1 else 3}>"
+        xd = 1 if N <= 2 else (2 if N <= 4 else (4 if N <= 8 else 0))
+        return f"zs::rgemm_kernel<{f}, 1, {waves}, {4 if f == 1 else 3}, {xd}>"
     nb = 2 if nb <= 2 else (4 if nb <= 4 else 8)
     if nb == 8 and M % 128 == 0 and (M // 128) * split_k * ((N + 127) // 128) >= 160:
         return "zs::rgemm_wide2_kernel<8, 8, 2>"
