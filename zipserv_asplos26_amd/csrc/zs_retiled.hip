@@ -1015,15 +1015,24 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
 // registers, X tiles two steps ahead into registers and one step ahead into
 // a double-buffered LDS tile; one barrier per step.
 // ---------------------------------------------------------------------------
-// LDS pitch of an X tile row: 128 B + 32 B of padding (fewer bank conflicts
-// on the B-fragment reads than + 16 B: 2-6% faster at N = 64 / 128), or
-// + 16 B where the larger tile would cost a workgroup per CU.
-constexpr int kXRowWide = 160, kXRowNarrowPad = 144;
+// X tiles in LDS are stored as MFMA B fragments, unpadded: for column block
+// nb and K half h (k 32h .. 32h + 31 of the tile) a 1 KB block of 64
+// 16-byte slots; lane l's B operand of v_mfma_f32_16x16x32_bf16 (batch row
+// 16*nb + r, k 32h + 8*q .. +7 with r = l%16, q = l/16) sits in slot
+// 16*q + (r ^ (8*h + 2*q)).  A B-fragment read pass (16 lanes: one q, r =
+// 0..15) then covers 16 slots distinct mod 16, and so does a write pass of
+// the X loads (16 threads: two rows r, r ^ 1 times the eight 16-byte
+// columns 4*h + q of a row), so neither conflicts on the LDS banks; the
+// loads keep whole 128-byte rows per 8 threads.
+constexpr int kXFragBlock = 1024;
+__device__ __forceinline__ int xfrag_slot(int nb, int h, int q, int r) {
+  return 64 * (2 * nb + h) + 16 * q + (r ^ (8 * h + 2 * q));
+}
 
 template <int NB, int BANDS, int PH>
 struct RWideSmem {
-  static constexpr int kXRow = kXRowWide;
-  static constexpr int kX = PH * 2 * 16 * NB * kXRow;   // [phase][buffer] tiles
+  static constexpr int kXTile = 2 * NB * kXFragBlock;
+  static constexpr int kX = PH * 2 * kXTile;   // [phase][buffer] tiles
   static constexpr int kStages = BANDS * PH * 2 * kExpStage;
   static constexpr int kMain = (int)sizeof(RTables) + kStages + kX;
   static constexpr int kRed = (PH - 1) * BANDS * NB * 64 * 16;
@@ -1038,7 +1047,7 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
                                                               int M, int N, int K,
                                                               int kb_per_split, SplitFix fx) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[RWideSmem<NB, BANDS, PH>::kBytes];
-  constexpr int kXRow = RWideSmem<NB, BANDS, PH>::kXRow;
+  constexpr int kXTile = RWideSmem<NB, BANDS, PH>::kXTile;
   RTables& T = *reinterpret_cast<RTables*>(smem);
   const RExp ex = r_exp(start_exp);
 
@@ -1049,9 +1058,9 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   uint8_t* stage0 = smem + sizeof(RTables) + w * 2 * kExpStage;
   uint8_t* stage1 = stage0 + kExpStage;
   uint8_t* xbase =
-      smem + sizeof(RTables) + RWideSmem<NB, BANDS, PH>::kStages + p * 2 * 16 * NB * kXRow;
+      smem + sizeof(RTables) + RWideSmem<NB, BANDS, PH>::kStages + p * 2 * kXTile;
   uint8_t* xb0 = xbase;
-  uint8_t* xb1 = xbase + 16 * NB * kXRow;
+  uint8_t* xb1 = xbase + kXTile;
   const int band = blockIdx.x * BANDS + q;
   const int split = blockIdx.y;
   const int n0 = blockIdx.z * NB * 16;
@@ -1084,12 +1093,14 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
     const int c = t + 64 * BANDS * i;
     const int row = min(c >> 3, 16 * NB - 1), cc = c & 7;
     xsrc[i] = 2u * ((uint32_t)min(n0 + row, N - 1) * (uint32_t)K + 8u * (uint32_t)cc);
-    xdst[i] = c < 128 * NB ? row * kXRow + 16 * cc : -1;
+    xdst[i] = c < 128 * NB ? 16 * xfrag_slot(row >> 4, cc >> 2, cc & 3, row & 15) : -1;
   }
   f32x4 acc[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int brd = (l & 15) * kXRow + 16 * (l >> 4);  // B fragment byte offset (nb = 0, h = 0)
+  // B fragment byte offsets of this lane in the block of nb = 0, h = 0 / 1
+  const int brd = 16 * xfrag_slot(0, 0, l >> 4, l & 15);
+  const int brd1 = 16 * xfrag_slot(0, 1, l >> 4, l & 15);
 
   // Outlier offsets of this wave's tiles, 64 at a time (lane i: tile c0 + i).
   int oe0 = 0, oe1 = 0, ochunk = -1;
@@ -1122,7 +1133,7 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
         *reinterpret_cast<u32x4*>(xb + xdst[i]) = XR[i];
   };
 
-  static_assert(RD == 2 || RD == 4, "record ring of 2 or 4 steps");
+  static_assert(RD == 2, "record ring of 2 steps");
   RStage R[RD];
   RMeta MT[RD];
   u32x4 XA[kXC], XB[kXC];
@@ -1154,24 +1165,55 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   xload(2, XA);
   __syncthreads();  // decode tables and X tile 0 visible
 
+  // NB = 8: the step's sixteen B fragments are read from LDS before the
+  // decode, so their latency hides behind it instead of stalling each MFMA
+  // pair, and the first K half of every column block goes to the MFMA unit
+  // before the second, so consecutive MFMAs never depend on each other
+  // (N = 128: 3-11% faster; at NB = 4 the extra registers cost more than
+  // the latency they hide: 1-7% slower, so it keeps one read pair per
+  // column block next to its MFMAs).
+  constexpr bool kEarlyB = NB >= 8;
+  auto b_read = [&](const uint8_t* xcur, bf16x8 (&b0)[NB], bf16x8 (&b1)[NB]) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const uint8_t* bp = xcur + nb * kXFragBlock * 2;
+      b0[nb] = *reinterpret_cast<const bf16x8*>(bp + brd);
+      b1[nb] = *reinterpret_cast<const bf16x8*>(bp + brd1);
+    }
+  };
+  auto mfma_step = [&](const uint8_t* xcur, const bf16x8 (&b0)[NB], const bf16x8 (&b1)[NB],
+                       const u32x4& a0, const u32x4& a1) {
+    if constexpr (kEarlyB) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0), b0[nb], acc[nb], 0, 0, 0);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1), b1[nb], acc[nb], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint8_t* bp = xcur + nb * kXFragBlock * 2;
+        const bf16x8 x0 = *reinterpret_cast<const bf16x8*>(bp + brd);
+        const bf16x8 x1 = *reinterpret_cast<const bf16x8*>(bp + brd1);
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0), x0, acc[nb], 0, 0, 0);
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1), x1, acc[nb], 0, 0, 0);
+      }
+    }
+  };
+
 #define RW_STEP(S, CUR, NXT, XCUR, RC, MC, RN, MN, XRN, XRC)                           \
   {                                                                                  \
     const RStage cs_ = RC;                                                           \
     const RMeta cm_ = MC;                                                            \
+    bf16x8 b0_[NB], b1_[NB];                                                         \
+    if constexpr (kEarlyB) b_read(XCUR, b0_, b1_);                                   \
     r_stage_all(NXT, RN);                                                            \
     issue((S) + RD, RC, MC);                                                         \
     if ((S) < cnt) {                                                                 \
       u32x4 a0_, a1_;                                                                \
-      r_decode_staged<true>(T, ex, cs_, cm_, CUR, exps, a0_, a1_);                         \
-      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                         \
-        const uint8_t* bp_ = XCUR + brd + nb_ * 16 * kXRow;                          \
-        const bf16x8 b0_ = *reinterpret_cast<const bf16x8*>(bp_);                    \
-        const bf16x8 b1_ = *reinterpret_cast<const bf16x8*>(bp_ + 64);               \
-        acc[nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0_), b0_,      \
-                                                           acc[nb_], 0, 0, 0);       \
-        acc[nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1_), b1_,      \
-                                                           acc[nb_], 0, 0, 0);       \
-      }                                                                              \
+      r_decode_staged<true>(T, ex, cs_, cm_, CUR, exps, a0_, a1_);                   \
+      mfma_step(XCUR, b0_, b1_, a0_, a1_);                                           \
     }                                                                                \
     xwrite((XCUR) == xb0 ? xb1 : xb0, XRN);                                          \
     xload((S) + 3, XRC);                                                             \
@@ -1179,15 +1221,10 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   }
   // Step s reads X buffer s%2; X registers: XB holds step s+1, XA step s+2
   // at the start of an even step (roles swap on odd steps).
-  // Record ring: step s consumes R[s % RD] and refills it with step s + RD.
-  for (int s = 0; s < steps; s += RD) {
+  // Record ring: step s consumes R[s % 2] and refills it with step s + 2.
+  for (int s = 0; s < steps; s += 2) {
     RW_STEP(s, stage0, stage1, xb0, R[0], MT[0], R[1], MT[1], XB, XB);
-    if (s + 1 < steps)
-      RW_STEP(s + 1, stage1, stage0, xb1, R[1], MT[1], R[2 % RD], MT[2 % RD], XA, XA);
-    if constexpr (RD == 4) {
-      if (s + 2 < steps) RW_STEP(s + 2, stage0, stage1, xb0, R[2], MT[2], R[3], MT[3], XB, XB);
-      if (s + 3 < steps) RW_STEP(s + 3, stage1, stage0, xb1, R[3], MT[3], R[0], MT[0], XA, XA);
-    }
+    if (s + 1 < steps) RW_STEP(s + 1, stage1, stage0, xb1, R[1], MT[1], R[0], MT[0], XA, XA);
   }
 #undef RW_STEP
 
@@ -1299,10 +1336,10 @@ constexpr int kWideDepth = 2;  // records in flight per wave (ring of RD steps)
 // ---------------------------------------------------------------------------
 template <int NB, int BANDS, int PH>
 struct RWide2Smem {
-  static constexpr int kXRow = NB == 4 ? kXRowNarrowPad : kXRowWide;  // 4: two workgroups per CU
+  static constexpr int kXTile = 2 * NB * kXFragBlock;
   static constexpr int kWP = BANDS / 2;                  // waves per phase
   static constexpr int kStageBytes = kWP * PH * 2 * 2 * kExpStage;  // [wave][buf][band]
-  static constexpr int kX = PH * 2 * 16 * NB * kXRow;    // [phase][buffer] tiles
+  static constexpr int kX = PH * 2 * kXTile;             // [phase][buffer] tiles
   static constexpr int kMain = kStageBytes + kX + (int)sizeof(RTables);
   static constexpr int kRed = (PH - 1) * kWP * 2 * NB * 64 * 16;
   static constexpr int kBytes = kMain > kRed ? kMain : kRed;
@@ -1313,7 +1350,7 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
     const uint8_t* fixed, const uint8_t* exps, const int32_t* eoff, int start_exp,
     const uint16_t* X, uint16_t* Y, int M, int N, int K, int kb_per_split, SplitFix fx) {
   using S = RWide2Smem<NB, BANDS, PH>;
-  constexpr int kXRow = S::kXRow;
+  constexpr int kXTile = S::kXTile;
   constexpr int WP = S::kWP;
   __shared__ __attribute__((aligned(16))) uint8_t smem[S::kBytes];
   RTables& T = *reinterpret_cast<RTables*>(smem + S::kStageBytes + S::kX);
@@ -1326,9 +1363,9 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
   // stage (buffer b, band f) of this wave
   uint8_t* stg = smem + w * 4 * kExpStage;
   auto stage_of = [&](int b, int f) { return stg + (2 * b + f) * kExpStage; };
-  uint8_t* xbase = smem + S::kStageBytes + p * 2 * 16 * NB * kXRow;
+  uint8_t* xbase = smem + S::kStageBytes + p * 2 * kXTile;
   uint8_t* xb0 = xbase;
-  uint8_t* xb1 = xbase + 16 * NB * kXRow;
+  uint8_t* xb1 = xbase + kXTile;
   const int band0 = blockIdx.x * BANDS + 2 * q;
   const int split = blockIdx.y;
   const int n0 = blockIdx.z * NB * 16;
@@ -1354,14 +1391,19 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
     const int c = t + 64 * WP * i;
     const int row = min(c >> 3, 16 * NB - 1), cc = c & 7;
     xsrc[i] = 2u * ((uint32_t)min(n0 + row, N - 1) * (uint32_t)K + 8u * (uint32_t)cc);
-    xdst[i] = c < 128 * NB ? row * kXRow + 16 * cc : -1;
+    xdst[i] = c < 128 * NB ? 16 * xfrag_slot(row >> 4, cc >> 2, cc & 3, row & 15) : -1;
   }
   f32x4 acc[2][NB];
 #pragma unroll
   for (int f = 0; f < 2; ++f)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[f][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int brd = (l & 15) * kXRow + 16 * (l >> 4);
+  const int brd = 16 * xfrag_slot(0, 0, l >> 4, l & 15);
+  const int brd1 = 16 * xfrag_slot(0, 1, l >> 4, l & 15);
+  // NB = 8: all B fragments of a step read before the decodes (see
+  // rgemm_wide_kernel); NB = 4 keeps them next to their MFMAs, where the
+  // extra registers would cost a wave per SIMD (measured 12-16% slower).
+  constexpr bool kEarlyB2 = NB >= 8;
 
   int oe0[2] = {0, 0}, oe1[2] = {0, 0}, ochunk = -1;
   auto issue = [&](int j, RStage (&R)[2], RMeta (&Mt)[2]) {
@@ -1437,6 +1479,14 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
   {                                                                                     \
     RStage cs_[2] = {RC[0], RC[1]};                                                     \
     RMeta cm_[2] = {MC[0], MC[1]};                                                      \
+    bf16x8 eb0_[NB], eb1_[NB];                                                          \
+    if constexpr (kEarlyB2) {                                                           \
+      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                            \
+        const uint8_t* bp_ = XCUR + nb_ * kXFragBlock * 2;                              \
+        eb0_[nb_] = *reinterpret_cast<const bf16x8*>(bp_ + brd);                        \
+        eb1_[nb_] = *reinterpret_cast<const bf16x8*>(bp_ + brd1);                       \
+      }                                                                                 \
+    }                                                                                   \
     _Pragma("unroll") for (int f_ = 0; f_ < 2; ++f_)                                    \
       r_stage_all(stage_of((BC) ^ 1, f_), RN[f_]);                                      \
     issue((S_) + 2, RC, MC);                                                            \
@@ -1445,15 +1495,26 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
       _Pragma("unroll") for (int f_ = 0; f_ < 2; ++f_)                                  \
         r_decode_staged<true>(T, ex, cs_[f_], cm_[f_], stage_of(BC, f_), exps, a0_[f_], \
                               a1_[f_]);                                                 \
-      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                            \
-        const uint8_t* bp_ = XCUR + brd + nb_ * 16 * kXRow;                             \
-        const bf16x8 b0_ = *reinterpret_cast<const bf16x8*>(bp_);                       \
-        const bf16x8 b1_ = *reinterpret_cast<const bf16x8*>(bp_ + 64);                  \
-        _Pragma("unroll") for (int f_ = 0; f_ < 2; ++f_) {                              \
-          acc[f_][nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                       \
-              as_bf16x8(a0_[f_]), b0_, acc[f_][nb_], 0, 0, 0);                          \
-          acc[f_][nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                       \
-              as_bf16x8(a1_[f_]), b1_, acc[f_][nb_], 0, 0, 0);                          \
+      if constexpr (kEarlyB2) {                                                         \
+        _Pragma("unroll") for (int f_ = 0; f_ < 2; ++f_)                                \
+          _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_)                          \
+            acc[f_][nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                     \
+                as_bf16x8(a0_[f_]), eb0_[nb_], acc[f_][nb_], 0, 0, 0);                  \
+        _Pragma("unroll") for (int f_ = 0; f_ < 2; ++f_)                                \
+          _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_)                          \
+            acc[f_][nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                     \
+                as_bf16x8(a1_[f_]), eb1_[nb_], acc[f_][nb_], 0, 0, 0);                  \
+      } else {                                                                          \
+        _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                          \
+          const uint8_t* bp_ = XCUR + nb_ * kXFragBlock * 2;                            \
+          const bf16x8 b0_ = *reinterpret_cast<const bf16x8*>(bp_ + brd);               \
+          const bf16x8 b1_ = *reinterpret_cast<const bf16x8*>(bp_ + brd1);              \
+          _Pragma("unroll") for (int f_ = 0; f_ < 2; ++f_) {                            \
+            acc[f_][nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                     \
+                as_bf16x8(a0_[f_]), b0_, acc[f_][nb_], 0, 0, 0);                        \
+            acc[f_][nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                     \
+                as_bf16x8(a1_[f_]), b1_, acc[f_][nb_], 0, 0, 0);                        \
+          }                                                                             \
         }                                                                               \
       }                                                                                 \
     }                                                                                   \
