@@ -53,7 +53,7 @@ extern "C" {
 #define ZS_WINDOW_KV 0
 #define ZS_WINDOW_WEIGHTS 1
 /* Scratch bytes (d_work) of zs_compress_retiled_auto_gpu. */
-#define ZS_RETILED_AUTO_WORK_BYTES 40960
+#define ZS_RETILED_AUTO_WORK_BYTES 65600
 
 /* KV layouts of a compressed cache (flash.h:19-20). */
 #define ZS_LAYOUT_HEAD_MAJOR 0 /* rows = ((b * Hkv + h) * rows_per_head + t) */
@@ -216,7 +216,8 @@ int zs_compress_retiled_fixed_gpu(void* stream, const uint16_t* d_input, int M, 
                                   uint8_t* d_tmp);
 /* zs_analyze_* + zs_compress_retiled_fixed_gpu in one input pass (when the
  * guess holds): the window (rule ZS_WINDOW_KV or ZS_WINDOW_WEIGHTS) is
- * guessed from every 32nd 4096-byte chunk of the input, the fixed parts,
+ * guessed from a sample of the input (every 32nd 4096-byte chunk, or sparser
+ * so that at most 512 chunks are read), the fixed parts,
  * counts and slots are written under the guess while the full exponent
  * histogram is counted (d_hist, 256 x uint64, out), the rule picks the window
  * from the full histogram (d_top, out), and only if it differs from the guess

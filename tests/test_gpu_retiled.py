@@ -381,7 +381,7 @@ def test_two_pass_encoder_equals_three_pass(torch_cuda, kind):
         assert int(cnt2.max()) > 256  # the re-read path ran
 
 
-_DIFFERS = 16 * 256 * 8 + 2048 + 32  # the flag's byte offset in the auto encoder's scratch
+_DIFFERS = 2 * 16 * 256 * 8 + 32  # the flag's byte offset in the auto encoder's scratch
 
 
 def _guess_miss_matrix(rng, M, K):

@@ -22,7 +22,7 @@ ZS_STREAM_SLACK_BYTES = 64
 ZS_RETILED_EXP_SLOT_BYTES = 256
 ZS_WINDOW_KV = 0
 ZS_WINDOW_WEIGHTS = 1
-ZS_RETILED_AUTO_WORK_BYTES = 40960
+ZS_RETILED_AUTO_WORK_BYTES = 65600
 ZS_LAYOUT_HEAD_MAJOR = 0
 ZS_LAYOUT_TOKEN_MAJOR = 1
 

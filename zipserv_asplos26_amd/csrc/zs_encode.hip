@@ -87,37 +87,49 @@ __global__ __launch_bounds__(kHistThreads) void hist_kernel(const uint16_t* in, 
   }
 }
 
-// Histogram of every kSampleStride-th 4096-byte chunk of the input (the
-// window guess of the one-pass re-tiled encoder); bins as hist_kernel's.
-constexpr int kSampleStride = 32;
+// Histogram of a sample of the input -- every stride-th 4096-byte chunk,
+// stride >= 32 and at most kSampleChunks chunks -- for the window guess of
+// the one-pass re-tiled encoder.  kSampleGroups workgroups each write their
+// own 256 bins (slice blockIdx.x of `slices`, no atomics, so nothing needs
+// zeroing first) and clear `zero` (the fused encoding pass's kVerifySlices
+// histogram slices, added to with atomics later).
+constexpr int kSampleStrideMin = 32, kSampleChunks = 128, kSampleGroups = 4;
+
+__device__ __forceinline__ int64_t sample_stride(int64_t nchunks) {
+  const int64_t s = (nchunks + kSampleChunks - 1) / kSampleChunks;
+  return s > kSampleStrideMin ? s : kSampleStrideMin;
+}
 
 __global__ __launch_bounds__(kHistThreads) void sample_hist_kernel(const uint16_t* in,
                                                                    int64_t nchunks,
-                                                                   uint64_t* counts) {
+                                                                   uint64_t* slices,
+                                                                   uint64_t* zero) {
   __shared__ uint32_t h[kHistCopies * kHistPitch];
   for (int i = threadIdx.x; i < kHistCopies * kHistPitch; i += kHistThreads) h[i] = 0;
+  for (int i = blockIdx.x * kHistThreads + threadIdx.x; i < kVerifySlices * 256;
+       i += kSampleGroups * kHistThreads)
+    zero[i] = 0;
   __syncthreads();
   uint32_t* hc = h + lane_id() * kHistPitch;
   const uint4* v = reinterpret_cast<const uint4*>(in);
-  const int64_t nvec = (nchunks + kSampleStride - 1) / kSampleStride * 256;
+  const int64_t stride = sample_stride(nchunks);
+  const int64_t nvec = (nchunks + stride - 1) / stride * 256;
   const int64_t nthreads = (int64_t)gridDim.x * kHistThreads;
-  auto at = [&](int64_t i) { return v + (i >> 8) * (256 * kSampleStride) + (i & 255); };
+  auto at = [&](int64_t i) { return v + (i >> 8) * (256 * stride) + (i & 255); };
   int64_t i = (int64_t)blockIdx.x * kHistThreads + threadIdx.x;
-  for (; i + 3 * nthreads < nvec; i += 4 * nthreads) {  // four 16-byte loads in flight
-    const uint4 x0 = nt_load16(at(i)), x1 = nt_load16(at(i + nthreads)),
-                x2 = nt_load16(at(i + 2 * nthreads)), x3 = nt_load16(at(i + 3 * nthreads));
-    hist_add8(hc, x0);
-    hist_add8(hc, x1);
-    hist_add8(hc, x2);
-    hist_add8(hc, x3);
+  for (; i + 7 * nthreads < nvec; i += 8 * nthreads) {  // eight 16-byte loads in flight
+    uint4 x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = nt_load16(at(i + j * nthreads));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) hist_add8(hc, x[j]);
   }
   for (; i < nvec; i += nthreads) hist_add8(hc, nt_load16(at(i)));
   __syncthreads();
   if (threadIdx.x < 256) {
     uint32_t c = 0;
     for (int k = 0; k < kHistCopies; ++k) c += h[k * kHistPitch + threadIdx.x];
-    if (c) atomicAdd(reinterpret_cast<unsigned long long*>(&counts[threadIdx.x]),
-                     (unsigned long long)c);
+    slices[256 * blockIdx.x + threadIdx.x] = c;
   }
 }
 
@@ -221,21 +233,22 @@ __device__ __forceinline__ int64_t load_count(const C* counts_g, int e, uint64_t
 // sorted, the first one starting 7 present exponents wins, else the start of
 // the longest consecutive run, clamped to [0, 248].
 template <typename C, int NS = 1>
-__global__ __launch_bounds__(64) void select_kernel(const C* counts_g,
-                                                   uint64_t* sum_out, int32_t* top,
-                                                   const int32_t* guess, int32_t* differs) {
-  // One wave.  Lane i holds the counts of exponents i, i+64, i+128, i+192;
-  // the streaming top-7 below runs on wave-uniform values (scalar unit),
-  // reading each count with v_readlane instead of a dependent memory load.
+__global__ __launch_bounds__(256) void select_kernel(const C* counts_g,
+                                                    uint64_t* sum_out, int32_t* top,
+                                                    const int32_t* guess, int32_t* differs) {
+  // Thread t sums bin t over the NS slices; then one wave: lane i holds the
+  // counts of exponents i, i+64, i+128, i+192, and the streaming top-7
+  // below runs on wave-uniform values (scalar unit), reading each count
+  // with v_readlane instead of a dependent memory load.
   if (blockIdx.x != 0) return;
+  __shared__ int64_t counts[256];
+  counts[threadIdx.x] = load_count<NS>(counts_g, threadIdx.x, sum_out);
+  __syncthreads();
+  if (threadIdx.x >= 64) return;
   const int l = threadIdx.x;
   int64_t cv[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) cv[k] = load_count<NS>(counts_g, 64 * k + l, sum_out);
-  __shared__ int64_t counts[256];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) counts[64 * k + l] = cv[k];
-  __syncthreads();
+  for (int k = 0; k < 4; ++k) cv[k] = counts[64 * k + l];
   // When exactly seven exponents have a count >= the seventh largest count
   // c7 > 0, those seven are the final slots whatever the order: one of them
   // is rejected or evicted only while seven others with counts >= its own
@@ -310,22 +323,23 @@ __global__ __launch_bounds__(64) void select_kernel(const C* counts_g,
 // holds exponents i, i + 64, i + 128, i + 192; a pass is one wave-wide
 // maximum of (count << 8 | 255 - exponent) over the exponents not taken.
 template <typename C, int NS = 1>
-__global__ __launch_bounds__(64) void select_weights_kernel(const C* counts_g,
-                                                           uint64_t* sum_out, int32_t* top,
-                                                           const int32_t* guess,
-                                                           int32_t* differs) {
+__global__ __launch_bounds__(256) void select_weights_kernel(const C* counts_g,
+                                                            uint64_t* sum_out, int32_t* top,
+                                                            const int32_t* guess,
+                                                            int32_t* differs) {
   if (blockIdx.x != 0) return;
-  const int l = threadIdx.x;
   __shared__ int64_t counts[256];
+  counts[threadIdx.x] = load_count<NS>(counts_g, threadIdx.x, sum_out);
+  __syncthreads();
+  if (threadIdx.x >= 64) return;
+  const int l = threadIdx.x;
   int64_t key[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const int64_t c = load_count<NS>(counts_g, 64 * k + l, sum_out);
-    counts[64 * k + l] = c;
+    const int64_t c = counts[64 * k + l];
     // counts stay below 2^55 (numel < 2^63 / 256 is far past any tensor)
     key[k] = c > 0 ? (c << 8) | (255 - (64 * k + l)) : 0;
   }
-  __syncthreads();
   int cand[7];
   int64_t c7;
   top7_passes(key, l, cand, &c7);
@@ -675,10 +689,10 @@ static int analyze(hipStream_t st, const uint16_t* d_input, int64_t numel, C* d_
   hipLaunchKernelGGL(hist_kernel<C>, dim3((unsigned)blocks), dim3(kHistThreads), 0, st, d_input, numel,
                      d_counts);
   if (weights_rule)
-    hipLaunchKernelGGL(select_weights_kernel<C>, dim3(1), dim3(64), 0, st, d_counts, nullptr, d_top,
+    hipLaunchKernelGGL(select_weights_kernel<C>, dim3(1), dim3(256), 0, st, d_counts, nullptr, d_top,
                        nullptr, nullptr);
   else
-    hipLaunchKernelGGL(select_kernel<C>, dim3(1), dim3(64), 0, st, d_counts, nullptr, d_top,
+    hipLaunchKernelGGL(select_kernel<C>, dim3(1), dim3(256), 0, st, d_counts, nullptr, d_top,
                        nullptr, nullptr);
   return hip_status(hipGetLastError());
 }
@@ -686,23 +700,20 @@ static int analyze(hipStream_t st, const uint16_t* d_input, int64_t numel, C* d_
 namespace zs {
 
 // Window guess from a sample of the input (chunks of 2048 elements; numel a
-// multiple of 2048, input 16-byte aligned; counts zeroed by the caller).
+// multiple of 2048, input 16-byte aligned) into `guess`; the per-workgroup
+// sample bins go to `sample` (kSampleGroups x 256), and `zero`
+// (kVerifySlices x 256 entries) is cleared on the way.
 hipError_t launch_window_sample(hipStream_t st, const uint16_t* in, int64_t numel,
-                                bool weights_rule, uint64_t* counts, int32_t* guess) {
-  const int64_t nchunks = numel / 2048;
-  const int64_t nvec = (nchunks + kSampleStride - 1) / kSampleStride * 256;
-  // Few workgroups: each ends with up to 256 atomics on the same 256 bins.
-  const int blocks = (int)std::max<int64_t>(
-      1, std::min<int64_t>((nvec + 4 * kHistThreads - 1) / (4 * kHistThreads),
-                           device_cu_count() / 2));
-  hipLaunchKernelGGL(sample_hist_kernel, dim3(blocks), dim3(kHistThreads), 0, st, in, nchunks,
-                     counts);
+                                bool weights_rule, uint64_t* sample, uint64_t* zero,
+                                int32_t* guess) {
+  hipLaunchKernelGGL(sample_hist_kernel, dim3(kSampleGroups), dim3(kHistThreads), 0, st, in,
+                     numel / 2048, sample, zero);
   if (weights_rule)
-    hipLaunchKernelGGL(select_weights_kernel<uint64_t>, dim3(1), dim3(64), 0, st, counts,
-                       nullptr, guess, nullptr, nullptr);
+    hipLaunchKernelGGL((select_weights_kernel<uint64_t, kSampleGroups>), dim3(1), dim3(256), 0, st,
+                       sample, nullptr, guess, nullptr, nullptr);
   else
-    hipLaunchKernelGGL(select_kernel<uint64_t>, dim3(1), dim3(64), 0, st, counts, nullptr,
-                       guess, nullptr, nullptr);
+    hipLaunchKernelGGL((select_kernel<uint64_t, kSampleGroups>), dim3(1), dim3(256), 0, st, sample,
+                       nullptr, guess, nullptr, nullptr);
   return hipGetLastError();
 }
 
@@ -712,10 +723,10 @@ hipError_t launch_window_verify(hipStream_t st, bool weights_rule, const uint64_
                                 uint64_t* hist, int32_t* top, const int32_t* guess,
                                 int32_t* differs) {
   if (weights_rule)
-    hipLaunchKernelGGL((select_weights_kernel<uint64_t, kVerifySlices>), dim3(1), dim3(64), 0, st,
+    hipLaunchKernelGGL((select_weights_kernel<uint64_t, kVerifySlices>), dim3(1), dim3(256), 0, st,
                        slices, hist, top, guess, differs);
   else
-    hipLaunchKernelGGL((select_kernel<uint64_t, kVerifySlices>), dim3(1), dim3(64), 0, st, slices,
+    hipLaunchKernelGGL((select_kernel<uint64_t, kVerifySlices>), dim3(1), dim3(256), 0, st, slices,
                        hist, top, guess, differs);
   return hipGetLastError();
 }
@@ -728,7 +739,7 @@ extern "C" int zs_analyze_top_exponents_gpu(void* stream, const uint16_t* d_inpu
   if (!d_input || numel <= 0 || !d_counts || !d_top) return ZS_E_INVAL;
   if (numel > INT32_MAX) return ZS_E_OVERFLOW;  // int32 bins of the reference
   hipStream_t st = (hipStream_t)stream;
-  if (d_done) hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, st, d_done, 1, 0);
+  if (d_done) hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(256), 0, st, d_done, 1, 0);
   return analyze(st, d_input, numel, d_counts, d_top);
 }
 

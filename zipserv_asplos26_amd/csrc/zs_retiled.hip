@@ -479,7 +479,8 @@ int device_cu_count();  // zs_gemm.hip
 // zs_encode.hip: the window guessed from a sample of the input, and the
 // window of a full histogram with a flag saying whether it differs.
 hipError_t launch_window_sample(hipStream_t st, const uint16_t* in, int64_t numel,
-                                bool weights_rule, uint64_t* counts, int32_t* guess);
+                                bool weights_rule, uint64_t* sample, uint64_t* zero,
+                                int32_t* guess);
 hipError_t launch_window_verify(hipStream_t st, bool weights_rule, const uint64_t* slices,
                                 uint64_t* hist, int32_t* top, const int32_t* guess,
                                 int32_t* differs);
@@ -1648,13 +1649,10 @@ extern "C" int zs_compress_retiled_fixed_gpu(void* stream, const uint16_t* d_inp
   return status_of(hipGetLastError());
 }
 
-__global__ void zero_u64_kernel(uint64_t* a, int n) {
-  for (int i = threadIdx.x; i < n; i += blockDim.x) a[i] = 0;
-}
-
-// d_work: kHistSlices histogram slices, the sample histogram, the guessed
-// window and the flag that says whether the full histogram's window differs.
-constexpr int kWorkSample = kHistSlices * 256 * 8, kWorkGuess = kWorkSample + 2048,
+// d_work: kHistSlices histogram slices of the encoding pass, as many of the
+// sample, the guessed window and the flag that says whether the full
+// histogram's window differs.
+constexpr int kWorkSample = kHistSlices * 256 * 8, kWorkGuess = 2 * kWorkSample,
               kWorkDiffers = kWorkGuess + 32;
 static_assert(kWorkDiffers + 4 <= ZS_RETILED_AUTO_WORK_BYTES, "auto encoder scratch");
 
@@ -1676,9 +1674,7 @@ extern "C" int zs_compress_retiled_auto_gpu(void* stream, const uint16_t* d_inpu
   uint64_t* sample = reinterpret_cast<uint64_t*>(d_work + kWorkSample);
   int32_t* guess = reinterpret_cast<int32_t*>(d_work + kWorkGuess);
   int32_t* differs = reinterpret_cast<int32_t*>(d_work + kWorkDiffers);
-  hipLaunchKernelGGL(zero_u64_kernel, dim3(1), dim3(1024), 0, st, slices,
-                     (kHistSlices + 1) * 256);
-  hipError_t e = launch_window_sample(st, d_input, (int64_t)M * K, weights, sample, guess);
+  hipError_t e = launch_window_sample(st, d_input, (int64_t)M * K, weights, sample, slices, guess);
   if (e != hipSuccess) return status_of(e);
   const int hist_grid = r_grid(nrec, 4);
   hipLaunchKernelGGL(rfixed_kernel<true>, dim3(hist_grid), dim3(256), 0, st, d_input, M, K, guess,
@@ -1686,7 +1682,7 @@ extern "C" int zs_compress_retiled_auto_gpu(void* stream, const uint16_t* d_inpu
   e = launch_window_verify(st, weights, slices, d_hist, d_top, guess, differs);
   if (e != hipSuccess) return status_of(e);
   // Usually a no-op: a small grid keeps the launch cheap.
-  hipLaunchKernelGGL(rfixed_kernel<false>, dim3(std::min(r_grid(nrec, 4), device_cu_count() * 4)),
+  hipLaunchKernelGGL(rfixed_kernel<false>, dim3(std::min(r_grid(nrec, 4), device_cu_count() * 2)),
                      dim3(256), 0, st, d_input, M, K, d_top, d_fixed, d_counts, d_tmp, nullptr,
                      differs);
   launch_rscan(st, d_counts, nrec, d_eoff, d_total);
