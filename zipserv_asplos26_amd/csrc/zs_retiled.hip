@@ -280,6 +280,88 @@ __global__ __launch_bounds__(256) void remit_kernel(const uint16_t* a, int M, in
   }
 }
 
+// Record encoding a dword (two bf16) at a time.  Codes: with e the exponent
+// byte of an element in a 16-bit lane, code = (min((e - st - 1) mod 256, 7)
+// + 1) mod 8 -- 1..7 in the window, 0 outside -- from packed 16-bit
+// subtract / min / add.  C(h, l) (code of element i at bits 3i) joins the
+// lane pairs; z(h) has bit 3i set for each outlier.  The sign / mantissa
+// byte of an element, (mantissa << 1) | sign of its pair partner, is byte 0
+// (low element) or byte 2 (high element) of the dword rotated left by one
+// bit, so one rotate per dword and one byte permute per four elements build
+// the record's first 16 bytes.  Same bytes as classify8 + emit_record.
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+
+struct RecCodes {
+  uint32_t c24[2];  // C(h, l)
+  uint32_t z[2];    // bit 3i: element i of half h is an outlier
+};
+
+__device__ __forceinline__ RecCodes rec_codes(const u32x4 v[2], uint32_t st) {
+  const unsigned short s1 = (unsigned short)(st + 1);
+  const us2 sub = {s1, s1}, seven = {7, 7}, one = {1, 1};
+  RecCodes r;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint32_t c = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t e = (v[h][j] >> 7) & 0x00FF00FFu;
+      const uint32_t dm = __builtin_bit_cast(uint32_t, __builtin_bit_cast(us2, e) - sub) &
+                          0x00FF00FFu;
+      const uint32_t c2 =
+          __builtin_bit_cast(uint32_t,
+                             __builtin_elementwise_min(__builtin_bit_cast(us2, dm), seven) + one) &
+          0x00070007u;
+      c |= ((c2 & 7u) | (c2 >> 13)) << (6 * j);  // codes of elements 2j, 2j + 1
+    }
+    r.c24[h] = c;
+    r.z[h] = ~(c | (c >> 1) | (c >> 2)) & 0x249249u;
+  }
+  return r;
+}
+
+// Element of bit 3i of z (i = 3i / 3 for 3i <= 21).
+__device__ __forceinline__ int rec_elem(int bit3) { return (bit3 * 11) >> 5; }
+
+// emit_record from rec_codes: the fixed part, and the outlier bytes from
+// exps[ebase] on unless the record has more than `limit` of them.  Returns
+// the record's outlier count.
+__device__ __forceinline__ int emit_record_c(uint8_t* fixed, uint8_t* exps, int64_t rec,
+                                             int64_t ebase, const u32x4 v[2], const RecCodes& rc,
+                                             int limit) {
+  const int l = lane_id();
+  u32x4 sm;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint32_t t[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t[j] = __builtin_amdgcn_alignbit(v[h][j], v[h][j], 31);
+    sm[2 * h] = __builtin_amdgcn_perm(t[1], t[0], 0x06040200u);
+    sm[2 * h + 1] = __builtin_amdgcn_perm(t[3], t[2], 0x06040200u);
+  }
+  uint8_t* f = fixed + rec * kRecBytes;
+  *reinterpret_cast<u32x4*>(f + 16 * l) = sm;
+  *reinterpret_cast<uint32_t*>(f + kRecP32 + 4 * l) = rc.c24[0] | (rc.c24[1] << 24);
+  *reinterpret_cast<uint16_t*>(f + kRecP16 + 2 * l) = (uint16_t)(rc.c24[1] >> 8);
+  const uint32_t n0 = __builtin_popcount(rc.z[0]), n1 = __builtin_popcount(rc.z[1]);
+  int rank0, rank1;
+  r_scan(n0, n1, rank0, rank1);
+  const int total = __builtin_amdgcn_readlane(rank1 + (int)n1, 63);
+  if (total <= limit) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t z = rc.z[h];
+      int64_t o = ebase + (h ? rank1 : rank0);
+      while (z) {
+        const int i = rec_elem(__builtin_ctz(z));
+        z &= z - 1;
+        exps[o++] = (uint8_t)((v[h][i >> 1] >> (16 * (i & 1) + 7)) & 0xFFu);
+      }
+    }
+  }
+  return total;
+}
+
 // Two-pass encoder (the input is read once after the window histogram):
 // rfixed_kernel writes every record's fixed part -- which does not depend
 // on where the outlier bytes go -- its outlier count, and up to kExpSlot of
@@ -315,29 +397,30 @@ __global__ __launch_bounds__(256) void rfixed_kernel(const uint16_t* a, int M, i
   uint32_t cc[7] = {0, 0, 0, 0, 0, 0, 0};  // this lane's elements with code 1..7
   for (int64_t rec = wid; rec < nrec; rec += nw) {
     u32x4 v[2];
-    uint32_t b[2][3];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      v[h] = *reinterpret_cast<const u32x4*>(rec_src(a, K, rec, h));
-      classify8(v[h], st, b[h][0], b[h][1], b[h][2]);
-    }
+    for (int h = 0; h < 2; ++h) v[h] = *reinterpret_cast<const u32x4*>(rec_src(a, K, rec, h));
+    const RecCodes rc = rec_codes(v, st);
     if constexpr (kHist) {
-      const uint32_t p1 = b[0][0] | (b[1][0] << 8), p2 = b[0][1] | (b[1][1] << 8),
-                     p3 = b[0][2] | (b[1][2] << 8);
+      // code bit p of element i of half h at bit 3i + h of P[p]; a code's
+      // elements are one 3-input bit function of the three planes
+      uint32_t P[3];
+#pragma unroll
+      for (int q = 0; q < 3; ++q)
+        P[q] = ((rc.c24[0] >> q) & 0x249249u) | (((rc.c24[1] >> q) & 0x249249u) << 1);
 #pragma unroll
       for (int c = 1; c <= 7; ++c)
-        cc[c - 1] += __builtin_popcount((c & 1 ? p1 : ~p1) & (c & 2 ? p2 : ~p2) &
-                                        (c & 4 ? p3 : ~p3) & 0xFFFFu);
+        cc[c - 1] += __builtin_popcount((c & 1 ? P[0] : ~P[0]) & (c & 2 ? P[1] : ~P[1]) &
+                                        (c & 4 ? P[2] : ~P[2]) & 0x6DB6DBu);
     }
-    const int n = emit_record(fixed, tmp + rec * kExpSlot, rec, 0, v, b, kExpSlot);
+    const int n = emit_record_c(fixed, tmp + rec * kExpSlot, rec, 0, v, rc, kExpSlot);
     if constexpr (kHist) {
       // outlier exponents into the workgroup's LDS bins
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        uint32_t fm = ~(b[h][0] | b[h][1] | b[h][2]) & 0xFFu;
-        while (fm) {
-          const int i = __builtin_ctz(fm);
-          fm &= fm - 1;
+        uint32_t z = rc.z[h];
+        while (z) {
+          const int i = rec_elem(__builtin_ctz(z));
+          z &= z - 1;
           atomicAdd(&lh[(v[h][i >> 1] >> (16 * (i & 1) + 7)) & 0xFFu], 1u);
         }
       }
