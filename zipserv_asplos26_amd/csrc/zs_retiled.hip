@@ -456,10 +456,19 @@ __global__ __launch_bounds__(256) void rfixed_kernel(const uint16_t* a, int M, i
 constexpr int kExpFast = kExpSlot - 4;
 constexpr int kCompactRecs = 8;
 
+// A group whose records all fit their slots is assembled in a wave-private
+// LDS buffer first (the shared edge dwords of neighbouring records merged
+// there, byte writes staying in LDS) and stored as whole dwords, with byte
+// stores only at the two ends of the group's range; a group with a record
+// past its slot writes each record straight to global memory as below.
+constexpr int kCompactBuf = kCompactRecs * kExpFast + 16;  // group range + alignment
+
 __global__ __launch_bounds__(256) void rcompact_kernel(const uint16_t* a, int M, int K,
                                                        const int32_t* top, const int32_t* eoff,
                                                        const uint8_t* __restrict__ tmp,
                                                        uint8_t* __restrict__ exps) {
+  __shared__ __attribute__((aligned(16))) uint8_t cbuf[4 * kCompactBuf];
+  uint8_t* buf = cbuf + (threadIdx.x >> 6) * kCompactBuf;
   const uint32_t st = (uint32_t)(top[0] - 1) & 0xFFu;
   const int64_t nrec = (int64_t)(M >> 4) * (K >> 6);
   const uint32_t* tmp32 = reinterpret_cast<const uint32_t*>(tmp);
@@ -478,6 +487,38 @@ __global__ __launch_bounds__(256) void rcompact_kernel(const uint16_t* a, int M,
                    : 0u;
 #pragma unroll
     for (int q = 0; q < kCompactRecs; ++q) prev[q] = __shfl_up(cur[q], 1);
+    if (__builtin_amdgcn_ballot_w64(l < cnt && nl > kExpFast) == 0) {
+      const int E0 = __builtin_amdgcn_readlane(e0l, 0);
+      const int E1 = __builtin_amdgcn_readlane(e0l + nl, cnt - 1);
+      const int base = E0 & ~3;  // buf byte 0 = stream byte base
+#pragma unroll
+      for (int q = 0; q < kCompactRecs; ++q) {
+        const int n = __builtin_amdgcn_readlane(nl, q);
+        const int e0 = __builtin_amdgcn_readlane(e0l, q);
+        if (q >= cnt || n == 0) continue;
+        const int al = e0 & 3;
+        const int p0 = (e0 & ~3) + 4 * l;  // stream byte of this dword
+        const uint32_t v = al == 0 ? cur[q] : __builtin_amdgcn_alignbyte(cur[q], prev[q], 4 - al);
+        if (p0 >= e0 && p0 + 4 <= e0 + n) {
+          *reinterpret_cast<uint32_t*>(buf + (p0 - base)) = v;
+        } else {
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            if (p0 + b >= e0 && p0 + b < e0 + n) buf[p0 - base + b] = (uint8_t)(v >> (8 * b));
+        }
+      }
+      for (int d = base + 4 * l; d < E1; d += 256) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(buf + (d - base));
+        if (d >= E0 && d + 4 <= E1) {
+          *reinterpret_cast<uint32_t*>(exps + d) = w;
+        } else {
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            if (d + b >= E0 && d + b < E1) exps[d + b] = (uint8_t)(w >> (8 * b));
+        }
+      }
+      continue;
+    }
     uint32_t slow = 0;  // records re-read from the input
 #pragma unroll
     for (int q = 0; q < kCompactRecs; ++q) {
