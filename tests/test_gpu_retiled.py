@@ -465,3 +465,25 @@ def test_one_pass_encoder_equals_analyze_then_fixed(torch_cuda, kind, rule):
     r = zo.compress_retiled(W, (want_top[0] - 1) & 0xFF)
     np.testing.assert_array_equal(f1.cpu().numpy(), r.fixed)
     np.testing.assert_array_equal(x1[:n1].cpu().numpy(), r.exps[:n1])
+
+
+@pytest.mark.parametrize("first", [0, 1, 100, 248, 249])
+def test_explicit_window_encoder_bytes(torch_cuda, first):
+    # the GPU encoder under an explicit window, including the windows that
+    # wrap the code arithmetic (first exponent 0: start_exp 255) or end at 255,
+    # byte for byte against the oracle's re-tiled encoder
+    torch = torch_cuda
+    rng = np.random.default_rng(700 + first)
+    W = rng.integers(0, 65536, size=(128, 512), dtype=np.uint16)
+    # make the window's exponents frequent so that both codes and outliers occur
+    e = rng.integers(first, first + 7, size=W.shape).astype(np.uint16) & 0xFF
+    keep = rng.random(W.shape) < 0.6
+    W = np.where(keep, (W & 0x807F) | (e << 7), W).astype(np.uint16)
+    r = zs.compress_retiled(to_torch_bf16(W), window=list(range(first, first + 7)))
+    o = zo.compress_retiled(W, (first - 1) & 0xFF)
+    torch.cuda.synchronize()
+    assert r.start_exp == (first - 1) & 0xFF
+    np.testing.assert_array_equal(r.fixed.cpu().numpy(), o.fixed)
+    np.testing.assert_array_equal(r.eoff.cpu().numpy(), o.eoff)
+    np.testing.assert_array_equal(r.exps[: r.num_outliers].cpu().numpy(), o.exps)
+    np.testing.assert_array_equal(from_torch_bf16(zs.decompress_retiled(r)), W)
