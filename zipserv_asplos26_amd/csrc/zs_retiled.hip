@@ -1136,9 +1136,10 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
 // columns; wave w decodes band w%BANDS of K tiles kb0 + PH*s + w/BANDS (PH
 // interleaved phases).  Each X tile (16*NB x 64) is loaded once per
 // workgroup into LDS and read by the BANDS band waves of its phase, so X
-// crosses L2 1/BANDS as often as with 16-row workgroups.  Records are fetched two steps ahead into
-// registers, X tiles two steps ahead into registers and one step ahead into
-// a double-buffered LDS tile; one barrier per step.
+// crosses L2 1/BANDS as often as with 16-row workgroups.  Records are fetched
+// RD steps ahead into registers and decoded one step before their MFMAs, X
+// tiles two steps ahead into registers and one step ahead into a
+// double-buffered LDS tile; one barrier per step.
 // ---------------------------------------------------------------------------
 // X tiles in LDS are stored as MFMA B fragments, unpadded: for column block
 // nb and K half h (k 32h .. 32h + 31 of the tile) a 1 KB block of 64
@@ -1227,24 +1228,22 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   const int brd = 16 * xfrag_slot(0, 0, l >> 4, l & 15);
   const int brd1 = 16 * xfrag_slot(0, 1, l >> 4, l & 15);
 
-  // Outlier offsets of this wave's tiles, 64 at a time (lane i: tile c0 + i).
-  int oe0 = 0, oe1 = 0, ochunk = -1;
-  auto offs = [&](int j, int& e0, int& e1) {
-    const int c = j & ~63;
-    if (c != ochunk) {
-      ochunk = c;
-      const int64_t ri = rowrec + tile_of(c + l);
-      oe0 = eoff[ri];
-      oe1 = eoff[ri + 1];
-    }
-    e0 = __builtin_amdgcn_readlane(oe0, j - c);
-    e1 = __builtin_amdgcn_readlane(oe1, j - c);
+  // Outlier offsets of a tile through the scalar cache (the address is
+  // uniform per wave), fetched one step before the record's loads go out.
+  // (Vector loads of 64 tiles' offsets, reloaded inside the step loop, made
+  // the compiler wait for every outstanding vector load before each step's
+  // record loads.)
+  using ci32 = const __attribute__((address_space(4))) int32_t;
+  ci32* eoffs = (ci32*)(eoff + rowrec);
+  int pe0, pe1;
+  auto offs = [&](int j) {
+    const int ti = tile_of(j);
+    pe0 = eoffs[ti];
+    pe1 = eoffs[ti + 1];
   };
   auto issue = [&](int j, RStage& R, RMeta& Mt) {
-    int e0, e1;
-    offs(j, e0, e1);
     r_issue_fixed_r(frs, (uint32_t)tile_of(j) * kRecBytes, R);
-    r_issue_exps(exps, e0, e1, R, Mt);
+    r_issue_exps(exps, pe0, pe1, R, Mt);
   };
   auto xload = [&](int j, u32x4 (&XR)[kXC]) {
     const uint32_t xs = (uint32_t)tile_of(j) * 128u;
@@ -1258,7 +1257,7 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
         *reinterpret_cast<u32x4*>(xb + xdst[i]) = XR[i];
   };
 
-  static_assert(RD == 2, "record ring of 2 steps");
+  static_assert(RD % 2 == 0, "record ring of an even number of steps");
   RStage R[RD];
   RMeta MT[RD];
   u32x4 XA[kXC], XB[kXC];
@@ -1268,11 +1267,12 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   // bytes follow as soon as the offsets land, then the table is written.
   {
     RTabRegs<BANDS * PH * 64> tab;
-    {
-      const int64_t ri = rowrec + tile_of(l);
-      oe0 = eoff[ri];
-      oe1 = eoff[ri + 1];
-      ochunk = 0;
+    int se0[RD + 1], se1[RD + 1];
+#pragma unroll
+    for (int k = 0; k <= RD; ++k) {
+      const int ti = tile_of(k);
+      se0[k] = eoffs[ti];
+      se1[k] = eoffs[ti + 1];
     }
     r_tab_load<BANDS * PH * 64>(tab, threadIdx.x);
 #pragma unroll
@@ -1280,9 +1280,9 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
     xload(0, XA);
     xload(1, XB);
 #pragma unroll
-    for (int k = 0; k < RD; ++k)
-      r_issue_exps(exps, __builtin_amdgcn_readlane(oe0, k), __builtin_amdgcn_readlane(oe1, k),
-                   R[k], MT[k]);
+    for (int k = 0; k < RD; ++k) r_issue_exps(exps, se0[k], se1[k], R[k], MT[k]);
+    pe0 = se0[RD];
+    pe1 = se1[RD];
     r_tab_store_exp<BANDS * PH * 64>(T, tab, threadIdx.x, ex.lo, ex.hi);
   }
   r_stage_all(stage0, R[0]);
@@ -1327,30 +1327,77 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
     }
   };
 
+  // Software pipeline: step s runs the MFMAs of record s (decoded in step
+  // s - 1) and decodes record s + 1, so one wave's decode VALU work overlaps
+  // its own matrix-core work (N = 128: 3-9% faster than decoding and
+  // multiplying the same record in one step).
+  u32x4 ac0, ac1;
+  if (0 < cnt) r_decode_staged<true>(T, ex, R[0], MT[0], stage0, exps, ac0, ac1);
 #define RW_STEP(S, CUR, NXT, XCUR, RC, MC, RN, MN, XRN, XRC)                           \
   {                                                                                  \
-    const RStage cs_ = RC;                                                           \
-    const RMeta cm_ = MC;                                                            \
+    const RStage cn_ = RN;                                                           \
+    const RMeta mn_ = MN;                                                            \
     bf16x8 b0_[NB], b1_[NB];                                                         \
     if constexpr (kEarlyB) b_read(XCUR, b0_, b1_);                                   \
-    r_stage_all(NXT, RN);                                                            \
+    r_stage_all(NXT, cn_);                                                           \
     issue((S) + RD, RC, MC);                                                         \
-    if ((S) < cnt) {                                                                 \
-      u32x4 a0_, a1_;                                                                \
-      r_decode_staged<true>(T, ex, cs_, cm_, CUR, exps, a0_, a1_);                   \
-      mfma_step(XCUR, b0_, b1_, a0_, a1_);                                           \
+    offs((S) + RD + 1);                                                              \
+    if ((S) < cnt) mfma_step(XCUR, b0_, b1_, ac0, ac1);                              \
+    if ((S) + 1 < cnt) r_decode_staged<true>(T, ex, cn_, mn_, NXT, exps, ac0, ac1);  \
+    xwrite((XCUR) == xb0 ? xb1 : xb0, XRN);                                          \
+    xload((S) + 3, XRC);                                                             \
+    __syncthreads();                                                                 \
+  }
+  // Steps s <= steps - 3 have record s and s + 1 in every phase (cnt >=
+  // steps - 1): no step condition, and the decode and MFMAs of a step share
+  // one basic block (records with unstaged outlier bytes take a branch).
+#define RW_MAIN(S, CUR, NXT, XCUR, RC, MC, RN, MN, XRN, XRC)                           \
+  {                                                                                  \
+    const RStage cn_ = RN;                                                           \
+    const RMeta mn_ = MN;                                                            \
+    bf16x8 b0_[NB], b1_[NB];                                                         \
+    if constexpr (kEarlyB) b_read(XCUR, b0_, b1_);                                   \
+    r_stage_all(NXT, cn_);                                                           \
+    issue((S) + RD, RC, MC);                                                         \
+    offs((S) + RD + 1);                                                              \
+    u32x4 n0_, n1_;                                                                  \
+    if (r_staged(mn_)) {                                                             \
+      r_decode<true>(T, ex, cn_.r, NXT, mn_.rel, n0_, n1_);                          \
+      mfma_step(XCUR, b0_, b1_, ac0, ac1);                                           \
+    } else {                                                                         \
+      r_decode<true>(T, ex, cn_.r, exps + mn_.e0, 0, n0_, n1_);                      \
+      mfma_step(XCUR, b0_, b1_, ac0, ac1);                                           \
     }                                                                                \
+    ac0 = n0_;                                                                       \
+    ac1 = n1_;                                                                       \
     xwrite((XCUR) == xb0 ? xb1 : xb0, XRN);                                          \
     xload((S) + 3, XRC);                                                             \
     __syncthreads();                                                                 \
   }
   // Step s reads X buffer s%2; X registers: XB holds step s+1, XA step s+2
   // at the start of an even step (roles swap on odd steps).
-  // Record ring: step s consumes R[s % 2] and refills it with step s + 2.
-  for (int s = 0; s < steps; s += 2) {
-    RW_STEP(s, stage0, stage1, xb0, R[0], MT[0], R[1], MT[1], XB, XB);
-    if (s + 1 < steps) RW_STEP(s + 1, stage1, stage0, xb1, R[1], MT[1], R[0], MT[0], XA, XA);
+  // Record ring: record s + 1 sits in R[(s + 1) % RD] during step s; the
+  // slot of record s (decoded in step s - 1) is refilled with record s + RD.
+  int s = 0;
+  for (; s + RD <= steps - 2; s += RD) {
+#pragma unroll
+    for (int k = 0; k < RD; k += 2) {
+      RW_MAIN(s + k, stage0, stage1, xb0, R[k], MT[k], R[k + 1], MT[k + 1], XB, XB);
+      RW_MAIN(s + k + 1, stage1, stage0, xb1, R[k + 1], MT[k + 1], R[(k + 2) % RD],
+              MT[(k + 2) % RD], XA, XA);
+    }
   }
+  for (; s < steps; s += RD) {
+#pragma unroll
+    for (int k = 0; k < RD; k += 2) {
+      if (s + k < steps)
+        RW_STEP(s + k, stage0, stage1, xb0, R[k], MT[k], R[k + 1], MT[k + 1], XB, XB);
+      if (s + k + 1 < steps)
+        RW_STEP(s + k + 1, stage1, stage0, xb1, R[k + 1], MT[k + 1], R[(k + 2) % RD],
+                MT[(k + 2) % RD], XA, XA);
+    }
+  }
+#undef RW_MAIN
 #undef RW_STEP
 
   // Phases 1..PH-1 hand their sums to phase 0 through LDS (added in phase
