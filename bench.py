@@ -374,8 +374,15 @@ def kernel_name(N, M, split_k):
     rgemm_wide_kernel<NB, 4, PH, 2> with NB = 2, 4 or 8
     column blocks, 4 row bands, 4 K phases when M/64 * split_k < 384 (2
     otherwise), records 2 steps ahead; N > 32 on grids of >= 160 128-row
-    workgroups -> rgemm_wide2_kernel<NB, 8, 2> (two bands per wave)."""
+    workgroups -> rgemm_wide2_kernel<NB, 8, 2> (two bands per wave);
+    4 <= N <= 16 on grids of M/64 * split_k >= 7/8 of the CU count ->
+    rgemm_wide_kernel<1, 4, PH, 2>."""
+    import torch
     nb = (N + 15) // 16
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if nb <= 1 and N >= 4 and (M // 64) * split_k * 8 >= cus * 7:
+        ph = 4 if (M // 64) * split_k < 384 else 2
+        return f"zs::rgemm_wide_kernel<1, 4, {ph}, 2>"
     if nb <= 1:
         waves = 4 if (N > 1 and M // 16 >= 640) else 8
         f = 2 if (N > 8 and M // 16 >= 384) else 1

@@ -141,11 +141,15 @@ def test_retiled_zipgemm_two_bands_per_wave(torch_cuda, N, M):
 @pytest.mark.parametrize("N,split_k,M", [(20, 1, 24576), (64, 1, 24576), (128, 1, 24576),
                                          (40, 2, 24576), (100, 1, 24576), (200, 1, 24576),
                                          (128, 2, 20480), (128, 1, 24640), (64, 1, 20480),
-                                         (50, 2, 20480)])
+                                         (50, 2, 20480), (4, 1, 24576), (5, 1, 24576),
+                                         (8, 1, 16384), (13, 2, 8192), (16, 1, 24640),
+                                         (3, 1, 24576)])
 def test_retiled_zipgemm_large_grid(torch_cuda, N, split_k, M):
     # M / 64 * split_k >= 384 selects the two-phase 64-row kernel; N > 32 with
     # M % 128 == 0 and >= 160 128-row workgroups the two-bands-per-wave one
-    # (M = 24640 is not a multiple of 128: the 64-row kernel)
+    # (M = 24640 is not a multiple of 128: the 64-row kernel); 4 <= N <= 16
+    # on >= 224 64-row workgroups the 64-row kernel over one column block
+    # (four phases below 384 workgroups); N = 3 stays on the 16-row kernel
     torch = torch_cuda
     rng = np.random.default_rng(N * 3 + split_k + M)
     K = 128
