@@ -252,12 +252,14 @@ def test_retiled_rejects_bad_args(torch_cuda):
     assert L.zs_retiled_mm(*args(sk=0)) == zs._lib.ZS_E_INVAL
 
 
-# (M, K, N, split_k) -> the kernel zs_retiled_mm picks: narrow F = 1, narrow
-# F = 2, narrow 4-wave F = 1 and F = 2, an empty last split, wide 4-phase,
-# wide 2-phase, two-band wide (4 and 8 column blocks), wide 8 column blocks.
+# (M, K, N, split_k) -> the kernel zs_retiled_mm picks: narrow F = 1, 64-row
+# one-column-block 2-phase, 4-phase, 2-phase (N <= 16 on >= 224 workgroups),
+# an empty last split, wide 4-phase, wide 2-phase, two-band wide (4 and 8
+# column blocks), wide 8 column blocks, narrow F = 2, narrow 4-wave F = 1.
 FUSED_CASES = [(1024, 1024, 1, 2), (6144, 512, 16, 4), (10240, 512, 8, 2), (10240, 256, 12, 3),
                (256, 320, 8, 4), (512, 2048, 32, 3),
-               (12288, 256, 32, 2), (10240, 256, 64, 2), (10240, 256, 128, 2), (512, 1024, 100, 3)]
+               (12288, 256, 32, 2), (10240, 256, 64, 2), (10240, 256, 128, 2), (512, 1024, 100, 3),
+               (6144, 512, 16, 2), (10240, 512, 3, 2)]
 
 
 @pytest.mark.parametrize("M,K,N,split_k", FUSED_CASES)
