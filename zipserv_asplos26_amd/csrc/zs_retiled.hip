@@ -1131,7 +1131,8 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
 }
 
 // ---------------------------------------------------------------------------
-// ZipGEMM over the re-tiled layout for wider batches (N > 16).  Workgroup =
+// ZipGEMM over the re-tiled layout for wider batches (N > 16, and 4 <= N <= 16
+// on grids of at least 7/8 of a workgroup per CU).  Workgroup =
 // BANDS*PH waves on one 16*BANDS-row tile x one split-K slice x 16*NB
 // columns; wave w decodes band w%BANDS of K tiles kb0 + PH*s + w/BANDS (PH
 // interleaved phases).  Each X tile (16*NB x 64) is loaded once per
