@@ -164,6 +164,24 @@ def test_retiled_zipgemm_large_grid(torch_cuda, N, split_k, M):
     assert np.abs(y - ref).max() / np.abs(ref).max() <= 1e-2
 
 
+@pytest.mark.parametrize("M,K,N,split_k", [(14336, 320, 9, 4), (14336, 448, 16, 1),
+                                           (14336, 1600, 5, 1), (14336, 1600, 12, 2)])
+def test_retiled_zipgemm_64row_narrow_batches(torch_cuda, M, K, N, split_k):
+    # 4 <= N <= 16 on >= 224 64-row workgroups: the 64-row kernel over one
+    # column block -- K tiles not a multiple of the phases (phases with one
+    # tile fewer), an empty last split, a steady loop of several steps.
+    torch = torch_cuda
+    rng = np.random.default_rng(M + K + N + split_k)
+    W = weights_bf16(rng, (M, K), outlier_frac=0.01)
+    X = zo.f32_to_bf16(rng.standard_normal((N, K), dtype=np.float32))
+    r = zs.compress_retiled(to_torch_bf16(W))
+    Y = zs.zipgemm(r, to_torch_bf16(X), split_k=split_k)
+    torch.cuda.synchronize()
+    y = zo.bf16_to_f32(from_torch_bf16(Y))
+    ref = zo.gemm_f32(W, X) if split_k == 1 else zo.bf16_to_f32(zo.gemm_splitk_bf16(W, X, split_k))
+    assert np.abs(y - ref).max() / np.abs(ref).max() <= 1e-2
+
+
 @pytest.mark.parametrize("N,M,K", [(1, 256, 1024), (16, 256, 1024), (32, 256, 2048),
                                    (64, 256, 1024), (128, 256, 2048), (8, 14336, 512)])
 def test_retiled_mixed_direct_and_staged_records(torch_cuda, N, M, K):
