@@ -500,9 +500,12 @@ def compress_retiled(input, logical_rows=None, logical_cols=None, layout="by_kv_
     dev = input.device
     i32 = dict(dtype=torch.int32, device=dev)
     nrec = rows // 16 * (cols // 64)
-    top, counts = torch.empty(7, **i32), torch.empty(256, dtype=torch.int64, device=dev)
+    # the outlier total and the window share one buffer, so that a single
+    # synchronising copy brings both to the host
+    meta = torch.empty(5, dtype=torch.int64, device=dev)
+    total, top = meta[:1], meta[1:].view(torch.int32)[:7]
+    counts = torch.empty(256, dtype=torch.int64, device=dev)
     cnt, eoff = torch.empty(nrec, **i32), torch.empty(nrec + 1, **i32)
-    total = torch.empty(1, dtype=torch.int64, device=dev)
     fixed = torch.empty(nrec * 1408, dtype=torch.uint8, device=dev)
     tmp = torch.empty(nrec * _lib.ZS_RETILED_EXP_SLOT_BYTES, dtype=torch.uint8, device=dev)
     st = _stream()
@@ -522,7 +525,8 @@ def compress_retiled(input, logical_rows=None, logical_cols=None, layout="by_kv_
               L.zs_compress_retiled_fixed_gpu(st, _dptr(input), rows, cols, _dptr(top),
                                               _dptr(fixed), _dptr(cnt), _dptr(eoff),
                                               _dptr(total), _dptr(tmp)))
-    tot, top0 = int(total.item()), int(top[0].item())  # synchronises (sizes the stream)
+    host = meta.cpu()  # synchronises (sizes the stream)
+    tot, top0 = int(host[0]), int(host[1:].view(torch.int32)[0])
     if tot > 2**31 - 1:
         raise OverflowError("outlier count exceeds the int32 offsets")
     exps = torch.zeros(tot + _lib.ZS_STREAM_SLACK_BYTES, dtype=torch.uint8, device=dev)
