@@ -214,6 +214,45 @@ def test_zipgemm_unit_vectors_exact(torch_cuda):
         np.testing.assert_array_equal(Y[i], W[:, k])
 
 
+# 64-row workgroups (X tiles staged in LDS) run every split-K launch and a
+# single slice at N > 16 on grids of >= 160 row blocks (>= 96 for N > 112):
+# M = 10240 / 6144 select them with one slice, M = 12352 with two slices
+# selects two K phases per workgroup instead of four; N = 200 spans two
+# column blocks of 128.
+@pytest.mark.parametrize("M,K,N,split_k", [(10240, 256, 17, 1), (10240, 256, 40, 1),
+                                           (10240, 320, 100, 1), (10240, 256, 128, 1),
+                                           (10240, 256, 200, 1), (6144, 512, 128, 1),
+                                           (12352, 512, 1, 2), (12352, 512, 8, 2),
+                                           (12352, 256, 40, 2), (12352, 384, 128, 3)])
+def test_zipgemm_64row_workgroups(torch_cuda, M, K, N, split_k):
+    rng = np.random.default_rng(M + K + N + split_k)
+    W = weights_bf16(rng, (M, K), outlier_frac=0.01)
+    X = normal_bf16(rng, (N, K))
+    c = upload(zo.compress(W))
+    Y = zs.zipgemm(c, to_torch_bf16(X), split_k=split_k)
+    y = zo.bf16_to_f32(from_torch_bf16(Y))
+    ref = zo.gemm_f32(W, X)
+    assert rel_err(y, ref) <= 1e-2
+    if split_k > 1:
+        assert rel_err(y, zo.bf16_to_f32(zo.gemm_splitk_bf16(W, X, split_k))) <= 1e-2
+
+
+@pytest.mark.parametrize("M,split_k", [(10240, 1), (128, 2), (12352, 3)])
+def test_zipgemm_64row_unit_vectors_exact(torch_cuda, M, split_k):
+    """One nonzero per batch row: every output is one weight, exactly, which
+    pins the K phase of each tile and the B-fragment slot of each batch row."""
+    rng = np.random.default_rng(M + split_k)
+    K = 256
+    W = weights_bf16(rng, (M, K), outlier_frac=0.05)
+    ks = [0, 7, 8, 31, 32, 63, 64, 65, 100, 127, 128, 191, 192, 200, 255] * 3
+    X = np.zeros((len(ks), K), np.uint16)
+    for i, k in enumerate(ks):
+        X[i, k] = 0x3F80
+    Y = from_torch_bf16(zs.zipgemm(upload(zo.compress(W)), to_torch_bf16(X), split_k=split_k))
+    for i, k in enumerate(ks):
+        np.testing.assert_array_equal(Y[i], W[:, k])
+
+
 def test_zipgemm_rejects_bad_args(torch_cuda):
     rng = np.random.default_rng(0)
     W = weights_bf16(rng, (64, 128))

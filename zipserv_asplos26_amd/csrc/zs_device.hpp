@@ -330,4 +330,18 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
+// X tiles staged in LDS by the 64-row ZipGEMM kernels are stored as MFMA B
+// fragments, unpadded: for column block nb and K half h (k 32h .. 32h + 31 of
+// the tile) a 1 KB block of 64 16-byte slots; lane l's B operand of
+// v_mfma_f32_16x16x32_bf16 (batch row 16*nb + r, k 32h + 8*q .. +7 with
+// r = l%16, q = l/16) sits in slot 16*q + (r ^ (8*h + 2*q)).  A B-fragment
+// read pass (16 lanes: one q, r = 0..15) then covers 16 slots distinct mod
+// 16, and so does a write pass of the X loads (16 threads: two rows r, r ^ 1
+// times the eight 16-byte columns 4*h + q of a row), so neither conflicts on
+// the LDS banks; the loads keep whole 128-byte rows per 8 threads.
+constexpr int kXFragBlock = 1024;
+__device__ __forceinline__ int xfrag_slot(int nb, int h, int q, int r) {
+  return 64 * (2 * nb + h) + 16 * q + (r ^ (8 * h + 2 * q));
+}
+
 }  // namespace zs

@@ -1,15 +1,19 @@
 // zs_gemm.hip -- gfx950 TCA-TBE decompress and ZipGEMM (+ split-K reduce).
 //
-// Both kernels decode one half median tile (16 rows x 32 columns) per wave
+// The kernels decode one half median tile (16 rows x 32 columns) per wave
 // step: lane l owns matrix row l%16, columns 8*(l/16)..+7 (see zs_device.hpp).
 //   * decompress: one workgroup (4 waves) per 64x64 global tile (grid-stride),
 //     wave w = median tile w; each lane stores its 8 decoded bf16 as 16 bytes.
-//   * ZipGEMM: one workgroup per 16-row band x split-K slice x 16*NB output
-//     columns; its waves take interleaved global-tile columns of the slice,
-//     stage each median tile through a wave-private LDS double buffer, and
-//     feed the decoded A fragment to v_mfma_f32_16x16x32_bf16 against 16-byte
-//     X loads (B operand lane l: column l%16, the same 8 k as A).  The
-//     per-wave partial accumulators are tree-summed through LDS.
+//   * ZipGEMM, 16-row workgroups: one workgroup per 16-row band x split-K
+//     slice x 16*NB output columns; its waves take interleaved global-tile
+//     columns of the slice, stage each median tile through a wave-private
+//     LDS buffer ring, and feed the decoded A fragment to
+//     v_mfma_f32_16x16x32_bf16 against 16-byte X loads (B operand lane l:
+//     column l%16, the same 8 k as A).  The per-wave partial accumulators
+//     are tree-summed through LDS.
+//   * ZipGEMM, 64-row workgroups (split-K and wide batches on large grids):
+//     one global-tile row per workgroup, each X tile staged once in LDS as
+//     B fragments for the four median-tile waves of a K phase.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -202,190 +206,244 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(Streams s, int start_e
 }
 
 // ---------------------------------------------------------------------------
-// ZipGEMM, 64-row variant.  A workgroup of 4 waves owns one 64-row band (a
-// row of global tiles) x one K slice x 16*NB output columns; wave w owns
-// median tile w of every global tile.  The 256 threads copy each global tile
-// (bitmap planes 3 x 512 B, its SM bytes from the 16-aligned tile start, its
-// FULL elements) into a 3-deep LDS ring with two unconditional 16-byte loads
-// per thread, three tiles ahead; one barrier per tile publishes a stage.  The
-// tile's streams are contiguous in HBM and every wave reuses the same X
-// columns, so this variant reads long runs and a quarter of the X traffic.
+// ZipGEMM, 64-row workgroups for wider batches (N > 16).  A workgroup of
+// 4*PH waves owns one global-tile row (64 rows) x one split-K slice x 16*NB
+// output columns; wave w stages and decodes median tile w%4 of K tiles
+// kb0 + PH*s + w/4 (PH interleaved phases) through two wave-private LDS
+// stages, as gemm_kernel does.  The 256 threads of a phase load each X tile
+// once into LDS as MFMA B fragments (xfrag_slot) read by its four median
+// waves, so X crosses L2 once per 64 rows instead of once per 16 rows --
+// the traffic that grows with N and bounds the 16-row kernel from N = 32 on.
+// Median tiles are fetched two steps ahead into registers, X tiles two steps
+// ahead into registers and one step ahead into a double-buffered LDS tile;
+// one barrier per step.  Stream offsets come through the scalar cache (the
+// tile index is uniform per wave), one step before the loads that use them.
 // ---------------------------------------------------------------------------
-constexpr int kGtBm = 0;                    // 3 planes x 512 B
-constexpr int kGtSm = 1536;                 // 258 chunks (<= 4111 bytes)
-constexpr int kGtSmBytes = 4128 + 32;       // + read-window slack
-constexpr int kGtFull = kGtSm + kGtSmBytes;  // up to 64 chunks of FULL
-constexpr int kGtFullChunks = 64;
-constexpr int kGtBytes = kGtFull + kGtFullChunks * 16 + 16;
-
-struct GtRegs {
-  u32x4 a, b;
-};
-struct GtMeta {
-  int fg0;          // first FULL element of the global tile
-  int full_direct;  // FULL segment larger than the stage: decode reads global
-};
-struct GtOff {
-  int sm0, f0, sm1, f1;  // stream offsets of the tile and of the next one
-  int msm, mf;           // this wave's median-tile start inside the tile
+template <int NB, int PH>
+struct CWideSmem {
+  static constexpr int kXTile = 2 * NB * kXFragBlock;
+  static constexpr int kX = PH * 2 * kXTile;             // [phase][buffer]
+  static constexpr int kStages = 4 * PH * 2 * kStBytes;  // [wave][buffer]
+  static constexpr int kMain = (int)sizeof(DecodeTables) + kStages + kX;
+  static constexpr int kRed = (PH - 1) * 4 * NB * 64 * 16;
+  static constexpr int kBytes = kMain > kRed ? kMain : kRed;
 };
 
-__device__ __forceinline__ GtOff load_gt_offsets(const Streams& s, int g, int m, bool valid) {
-  GtOff t{0, 0, 0, 0, 0, 0};
-  if (valid) {
-    t.sm0 = s.tog[2 * g];
-    t.f0 = s.tog[2 * g + 1];
-    t.sm1 = s.tog[2 * g + 2];
-    t.f1 = s.tog[2 * g + 3];
-    t.msm = s.tom[2 * (4 * g + m)];
-    t.mf = s.tom[2 * (4 * g + m) + 1];
+// Stream offsets of median tile m of global tile g (both wave-uniform), read
+// through the scalar cache: first SM byte and FULL element of the median tile
+// and of the one after it (the tables of csrc/L_API.cu:356-357, :505-506 and
+// :541-549: TileOffsets_Global holds one more entry than there are tiles).
+__device__ __forceinline__ TileOff med_offsets_s(const Streams& s, int g, int m) {
+  using ci32 = const __attribute__((address_space(4))) int32_t;
+  ci32* tg = (ci32*)(s.tog + 2 * (int64_t)g);
+  ci32* tm = (ci32*)(s.tom + 8 * (int64_t)g + 2 * m);
+  const int t0 = tg[0], tf0 = tg[1];
+  TileOff t;
+  t.hf0 = t0 + tm[0];
+  t.f0 = tf0 + tm[1];
+  if (m < 3) {
+    t.hf1 = t0 + tm[2];
+    t.f1 = tf0 + tm[3];
+  } else {
+    t.hf1 = tg[2];
+    t.f1 = tg[3];
   }
   return t;
 }
 
-// Source pointers of one thread's two loads for global tile g.  Role of
-// thread t for load b: t < 96 bitmap chunk, 96..159 FULL chunk, 160..161 SM
-// chunks 256..257, others a clamped re-read of SM chunk 0.
-__device__ __forceinline__ void gt_issue(const Streams& s, int t, const uint8_t* bm_thread,
-                                         int g, int sm0, int sm1, int f0, int f1, GtRegs& r,
-                                         GtMeta& mt) {
-  const int nsm = (sm1 - sm0 + 15) >> 4;  // <= 257
-  const int nfc = (f1 - f0 + 7) >> 3;
-  mt.fg0 = f0;
-  mt.full_direct = nfc > kGtFullChunks;
-  r.a = *reinterpret_cast<const u32x4*>(s.sm + sm0 + (t < nsm ? 16 * t : 0));
-  const uint8_t* pb = s.sm + sm0;
-  if (t < 96) {
-    pb = bm_thread + 512 * g + 16 * (t & 31);
-  } else if (t < 160) {
-    if (t - 96 < nfc && nfc <= kGtFullChunks)
-      pb = reinterpret_cast<const uint8_t*>(s.full + f0 + 8 * (t - 96));
-  } else if (t < 162) {
-    if (t + 96 < nsm) pb = s.sm + sm0 + 16 * (t + 96);
-  }
-  r.b = *reinterpret_cast<const u32x4*>(pb);
-}
-
-__device__ __forceinline__ void gt_write(uint8_t* st, int t, const GtRegs& r) {
-  *reinterpret_cast<u32x4*>(st + kGtSm + 16 * t) = r.a;
-  if (t < 96)
-    *reinterpret_cast<u32x4*>(st + kGtBm + 512 * (t >> 5) + 16 * (t & 31)) = r.b;
-  else if (t < 160)
-    *reinterpret_cast<u32x4*>(st + kGtFull + 16 * (t - 96)) = r.b;
-  else if (t < 162)
-    *reinterpret_cast<u32x4*>(st + kGtSm + 16 * (t + 96)) = r.b;
-}
-
-template <int NB>
-struct Gemm64Smem {
-  static constexpr int kBytes = (int)sizeof(DecodeTables) + 3 * kGtBytes;
-};
-
-template <int NB>
-__global__ __launch_bounds__(256) void gemm64_kernel(Streams s, int start_exp, const uint16_t* X,
-                                                     uint16_t* Y, int M, int N, int K,
-                                                     int kb_per_split) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[Gemm64Smem<NB>::kBytes];
+template <int NB, int PH, int RD>
+__global__ __launch_bounds__(4 * PH * 64) void cgemm_wide_kernel(Streams s, int start_exp,
+                                                                 const uint16_t* X, uint16_t* Y,
+                                                                 int M, int N, int K,
+                                                                 int kb_per_split) {
+  using S = CWideSmem<NB, PH>;
+  constexpr int kXTile = S::kXTile;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[S::kBytes];
   DecodeTables& T = *reinterpret_cast<DecodeTables*>(smem);
-  build_decode_tables(T, start_exp, threadIdx.x, blockDim.x);
-  uint8_t* stg0 = smem + sizeof(DecodeTables);
-  uint8_t* stg1 = stg0 + kGtBytes;
-  uint8_t* stg2 = stg1 + kGtBytes;
 
-  const int t = threadIdx.x;
-  const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // median tile of this wave
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
+  const int q = w & 3, p = w >> 2;  // median tile, phase
+  const int t = threadIdx.x & 255;  // thread index within the phase
+  uint8_t* stage0 = smem + sizeof(DecodeTables) + w * 2 * kStBytes;
+  uint8_t* stage1 = stage0 + kStBytes;
+  uint8_t* xb0 = smem + sizeof(DecodeTables) + S::kStages + p * 2 * kXTile;
+  uint8_t* xb1 = xb0 + kXTile;
   const int gm = blockIdx.x;
   const int split = blockIdx.y;
   const int n0 = blockIdx.z * NB * 16;
   const int KT = K >> 6;
   const int kb0 = split * kb_per_split;
-  const int n = max(0, min(kb0 + kb_per_split, KT) - kb0);  // tiles of this slice
+  const int kb1 = min(kb0 + kb_per_split, KT);
+  const int span = max(kb1 - kb0, 0);
+  const int steps = (span + PH - 1) / PH;    // same for every phase
+  const int cnt = (span - p + PH - 1) / PH;  // valid tiles of this phase
+  // K tile of step j of this phase, clamped into the slice (clamped steps
+  // repeat an in-bounds load and skip the decode; an empty slice, kb0 >= KT,
+  // clamps to the last tile of the row).
+  auto tile_of = [&](int j) { return min(kb0 + PH * j + p, kb1 - 1); };
+  const int g0 = gm * KT;
 
-  const uint16_t* xrow[NB];
+  // X tile loads of this thread: chunk c = t + 256*i, row c/8 (clamped to
+  // N - 1), 16-byte column c%8 (128*NB chunks per tile; threads past them
+  // load and drop).
+  constexpr int kXC = (2 * NB + 3) / 4;
+  const uint16_t* xsrc[kXC];
+  int xdst[kXC];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int col = min(n0 + nb * 16 + (l & 15), N - 1);
-    xrow[nb] = X + (int64_t)col * K + 8 * (l >> 4);
+  for (int i = 0; i < kXC; ++i) {
+    const int c = t + 256 * i;
+    const int row = min(c >> 3, 16 * NB - 1), cc = c & 7;
+    xsrc[i] = X + (int64_t)min(n0 + row, N - 1) * K + 8 * cc;
+    xdst[i] = c < 128 * NB ? 16 * xfrag_slot(row >> 4, cc >> 2, cc & 3, row & 15) : -1;
   }
   f32x4 acc[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // Threads 0..95 load bitmap chunks: plane t/32.
-  const uint8_t* bm_thread = t < 32 ? s.bm1 : (t < 64 ? s.bm2 : s.bm3);
+  const int brd = 16 * xfrag_slot(0, 0, l >> 4, l & 15);
+  const int brd1 = 16 * xfrag_slot(0, 1, l >> 4, l & 15);
 
-  for (int c0 = 0; c0 < n; c0 += 64) {
-    const int cn = min(n - c0, 64);
-    const int last = cn - 1;
-    const GtOff offs = load_gt_offsets(s, gm * KT + kb0 + c0 + l, w, l < cn);
-    GtRegs R0, R1, R2;
-    GtMeta M0, M1, M2;
-    bf16x8 X0[2][NB], X1[2][NB], X2[2][NB], xc[2][NB];
-    // Tile i's offsets sit in lane i of every wave; the loaders need the
-    // tile's stream bounds, the decoders their own median's start.
-#define ZS_G(J) (gm * KT + kb0 + c0 + (J))
-#define ZS_GISSUE(J, R, MT, XD)                                                          \
-  {                                                                                      \
-    const int jj_ = (J);                                                                 \
-    gt_issue(s, t, bm_thread, ZS_G(jj_), __builtin_amdgcn_readlane(offs.sm0, jj_),       \
-             __builtin_amdgcn_readlane(offs.sm1, jj_),                                   \
-             __builtin_amdgcn_readlane(offs.f0, jj_),                                    \
-             __builtin_amdgcn_readlane(offs.f1, jj_), R, MT);                            \
-    const int kk_ = (kb0 + c0 + jj_) * 64;                                               \
-    _Pragma("unroll") for (int h_ = 0; h_ < 2; ++h_)                                     \
-      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_)                               \
-        XD[h_][nb_] = *reinterpret_cast<const bf16x8*>(xrow[nb_] + kk_ + 32 * h_);       \
+  const uint8_t* bm_lane = l < 8 ? s.bm1 : (l < 16 ? s.bm2 : s.bm3);
+  TileOff po;  // offsets of the next median tile to issue
+  auto offs = [&](int j) { po = med_offsets_s(s, g0 + tile_of(j), q); };
+  auto issue = [&](int j, StageRegs& R, StageMeta& Mt) {
+    stage_issue(s, bm_lane, g0 + tile_of(j), q, po, R, Mt);
+  };
+  auto xload = [&](int j, u32x4 (&XR)[kXC]) {
+    const int kk = tile_of(j) * 64;
+#pragma unroll
+    for (int i = 0; i < kXC; ++i) XR[i] = *reinterpret_cast<const u32x4*>(xsrc[i] + kk);
+  };
+  auto xwrite = [&](uint8_t* xb, const u32x4 (&XR)[kXC]) {
+#pragma unroll
+    for (int i = 0; i < kXC; ++i)
+      if (2 * NB >= 4 * (i + 1) || xdst[i] >= 0) *reinterpret_cast<u32x4*>(xb + xdst[i]) = XR[i];
+  };
+
+  static_assert(RD % 2 == 0, "tile ring of an even number of steps");
+  StageRegs R[RD];
+  StageMeta MT[RD];
+  u32x4 XA[kXC], XB[kXC];
+  {
+    TileOff so[RD + 1];
+#pragma unroll
+    for (int k = 0; k <= RD; ++k) so[k] = med_offsets_s(s, g0 + tile_of(k), q);
+#pragma unroll
+    for (int k = 0; k < RD; ++k) {
+      po = so[k];
+      issue(k, R[k], MT[k]);
+    }
+    po = so[RD];
   }
-#define ZS_GSTEP(J, CUR, NXT, RC, MC, XC, RN)                                            \
-  {                                                                                      \
-    const GtMeta cm_ = MC;                                                               \
-    _Pragma("unroll") for (int h_ = 0; h_ < 2; ++h_)                                     \
-      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) xc[h_][nb_] = XC[h_][nb_];    \
-    gt_write(NXT, t, RN);                                                                \
-    ZS_GISSUE(min((J) + 3, last), RC, MC, XC);                                           \
-    __syncthreads();                                                                     \
-    if ((J) < cn) {                                                                      \
-      const int msm_ = __builtin_amdgcn_readlane(offs.msm, (J));                         \
-      const int mf_ = __builtin_amdgcn_readlane(offs.mf, (J));                           \
-      u32x4 a0_, a1_;                                                                    \
-      decode_median_pair(T, T.e1, CUR + kGtBm + 128 * w, 512, CUR + kGtSm, msm_,               \
-                         reinterpret_cast<const uint16_t*>(CUR + kGtFull), mf_,          \
-                         cm_.full_direct, s.full + cm_.fg0, a0_, a1_);                   \
-      _Pragma("unroll") for (int nb_ = 0; nb_ < NB; ++nb_) {                             \
-        acc[nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0_), xc[0][nb_],   \
-                                                           acc[nb_], 0, 0, 0);           \
-        acc[nb_] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1_), xc[1][nb_],   \
-                                                           acc[nb_], 0, 0, 0);           \
-      }                                                                                  \
-    }                                                                                    \
-  }
-    if (cn > 0) {
-      ZS_GISSUE(0, R0, M0, X0);
-      ZS_GISSUE(min(1, last), R1, M1, X1);
-      ZS_GISSUE(min(2, last), R2, M2, X2);
-      __syncthreads();  // decode tables built; previous chunk's stages drained
-      gt_write(stg0, t, R0);
-      for (int j = 0; j < cn; j += 3) {
-        ZS_GSTEP(j, stg0, stg1, R0, M0, X0, R1);
-        ZS_GSTEP(j + 1, stg1, stg2, R1, M1, X1, R2);
-        ZS_GSTEP(j + 2, stg2, stg0, R2, M2, X2, R0);
+  xload(0, XA);
+  xload(1, XB);
+  build_decode_tables(T, start_exp, threadIdx.x, 4 * PH * 64);
+  stage_write(stage0, R[0]);
+  xwrite(xb0, XA);
+  xload(2, XA);
+  __syncthreads();  // decode tables and X tile 0 visible
+
+  // NB = 8: the step's sixteen B fragments are read before the decode, so
+  // their LDS latency hides behind it.
+  constexpr bool kEarlyB = NB >= 8;
+  auto b_read = [&](const uint8_t* xcur, bf16x8 (&b0)[NB], bf16x8 (&b1)[NB]) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const uint8_t* bp = xcur + nb * kXFragBlock * 2;
+      b0[nb] = *reinterpret_cast<const bf16x8*>(bp + brd);
+      b1[nb] = *reinterpret_cast<const bf16x8*>(bp + brd1);
+    }
+  };
+  auto mfma_step = [&](const uint8_t* xcur, const bf16x8 (&b0)[NB], const bf16x8 (&b1)[NB],
+                       const u32x4& a0, const u32x4& a1) {
+    if constexpr (kEarlyB) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0), b0[nb], acc[nb], 0, 0, 0);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1), b1[nb], acc[nb], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint8_t* bp = xcur + nb * kXFragBlock * 2;
+        const bf16x8 x0 = *reinterpret_cast<const bf16x8*>(bp + brd);
+        const bf16x8 x1 = *reinterpret_cast<const bf16x8*>(bp + brd1);
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0), x0, acc[nb], 0, 0, 0);
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1), x1, acc[nb], 0, 0, 0);
       }
     }
-#undef ZS_GSTEP
-#undef ZS_GISSUE
-#undef ZS_G
-  }
+  };
 
-  uint16_t* out = Y + (int64_t)split * M * N;
-  const int mrow = gm * 64 + w * 16 + 4 * (l >> 4);
+  // Step s: median tile s + 1 goes from registers to its stage, tile s + RD
+  // is issued into the registers tile s used, tile s is decoded from its stage
+  // and multiplied with X tile s (LDS buffer s % 2), X tile s + 1 goes to the
+  // other buffer and X tile s + 3 is loaded into the registers it used.
+#define CW_STEP(S, CUR, NXT, XCUR, XNXT, RC, MC, RN, XR, GUARD)                          \
+  {                                                                                    \
+    bf16x8 b0_[NB], b1_[NB];                                                           \
+    if constexpr (kEarlyB) b_read(XCUR, b0_, b1_);                                     \
+    const StageMeta cm_ = MC;                                                          \
+    stage_write(NXT, RN);                                                              \
+    issue((S) + RD, RC, MC);                                                           \
+    offs((S) + RD + 1);                                                                \
+    if (!(GUARD) || (S) < cnt) {                                                       \
+      u32x4 a0_, a1_;                                                                  \
+      decode_median_pair(T, T.e1, CUR + kStBm, 128, CUR + kStSm, cm_.sm_rel,           \
+                         reinterpret_cast<const uint16_t*>(CUR + kStFull), cm_.full_rel, \
+                         cm_.full_direct, s.full + cm_.fa0, a0_, a1_);                 \
+      mfma_step(XCUR, b0_, b1_, a0_, a1_);                                             \
+    }                                                                                  \
+    xwrite(XNXT, XR);                                                                  \
+    xload((S) + 3, XR);                                                                \
+    __syncthreads();                                                                   \
+  }
+  // Steps s <= steps - 2 have a tile in every phase (cnt >= steps - 1): no
+  // step condition there.
+  // Tile ring: tile s + 1 sits in R[(s + 1) % RD] during step s.
+  int s0 = 0;
+  for (; s0 + RD - 1 <= steps - 2; s0 += RD) {
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const f32x4 v = acc[nb];
-    const int col = n0 + nb * 16 + (l & 15);
-    if (col < N) {
-      const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
-      const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
-      *reinterpret_cast<uint2*>(out + (int64_t)col * M + mrow) = make_uint2(lo, hi);
+    for (int k = 0; k < RD; k += 2) {
+      CW_STEP(s0 + k, stage0, stage1, xb0, xb1, R[k], MT[k], R[k + 1], XB, false);
+      CW_STEP(s0 + k + 1, stage1, stage0, xb1, xb0, R[k + 1], MT[k + 1], R[(k + 2) % RD], XA,
+              false);
+    }
+  }
+  for (; s0 < steps; s0 += RD) {
+#pragma unroll
+    for (int k = 0; k < RD; k += 2) {
+      if (s0 + k < steps)
+        CW_STEP(s0 + k, stage0, stage1, xb0, xb1, R[k], MT[k], R[k + 1], XB, true);
+      if (s0 + k + 1 < steps)
+        CW_STEP(s0 + k + 1, stage1, stage0, xb1, xb0, R[k + 1], MT[k + 1], R[(k + 2) % RD], XA,
+                true);
+    }
+  }
+#undef CW_STEP
+
+  // Phases 1..PH-1 hand their sums to phase 0 through LDS (added in phase
+  // order, so the result is deterministic); phase 0 writes its median rows.
+  f32x4* red = reinterpret_cast<f32x4*>(smem);
+  if (p > 0) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) red[(((p - 1) * 4 + q) * NB + nb) * 64 + l] = acc[nb];
+  }
+  __syncthreads();
+  if (p == 0) {
+    uint16_t* out = Y + (int64_t)split * M * N;
+    const int mrow = gm * 64 + q * 16 + 4 * (l >> 4);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      f32x4 v = acc[nb];
+#pragma unroll
+      for (int pp = 1; pp < PH; ++pp) v += red[(((pp - 1) * 4 + q) * NB + nb) * 64 + l];
+      const int col = n0 + nb * 16 + (l & 15);
+      if (col < N) {
+        const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+        const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
+        *reinterpret_cast<uint2*>(out + (int64_t)col * M + mrow) = make_uint2(lo, hi);
+      }
     }
   }
 }
@@ -445,13 +503,17 @@ static hipError_t launch_gemm(hipStream_t st, const Streams& s, int start_exp, c
   return hipGetLastError();
 }
 
-template <int NB>
-static hipError_t launch_gemm64(hipStream_t st, const Streams& s, int start_exp,
-                                const uint16_t* X, uint16_t* Y, int M, int N, int K, int split_k,
-                                int kb_per_split) {
+// Median tiles in flight per wave: 2 (4 measured 10% slower: the kernel is
+// bound by the decode's LDS and VALU work, not by load latency).
+constexpr int kCWideDepth = 2;
+
+template <int NB, int PH>
+static hipError_t launch_cwide(hipStream_t st, const Streams& s, int start_exp,
+                               const uint16_t* X, uint16_t* Y, int M, int N, int K, int split_k,
+                               int kb_per_split) {
   dim3 grid(M / 64, split_k, (N + NB * 16 - 1) / (NB * 16));
-  hipLaunchKernelGGL((gemm64_kernel<NB>), grid, dim3(256), 0, st, s, start_exp, X, Y, M, N, K,
-                     kb_per_split);
+  hipLaunchKernelGGL((cgemm_wide_kernel<NB, PH, kCWideDepth>), grid, dim3(4 * PH * 64), 0, st, s, start_exp,
+                     X, Y, M, N, K, kb_per_split);
   return hipGetLastError();
 }
 
@@ -518,15 +580,29 @@ extern "C" int zs_bf16_triple_bitmap_mm(void* stream, const uint8_t* sm, const u
   uint16_t* out = split_k == 1 ? C : ws;
   const int nb = (N + 15) / 16;
   hipError_t e;
-  // A split-K launch has enough workgroups to use the 64-row tile kernel
-  // (long contiguous reads, X shared by the four median tiles); a single
-  // slice keeps 16-row bands so that small M still fills the GPU.
-  const bool wide = split_k > 1 && nb <= 8;
-  if (wide) {
-    if (nb <= 1) e = launch_gemm64<1>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
-    else if (nb <= 2) e = launch_gemm64<2>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
-    else if (nb <= 4) e = launch_gemm64<4>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
-    else e = launch_gemm64<8>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
+  // 64-row workgroups (each X tile staged once in LDS for four median
+  // tiles) for every split-K launch, and for one slice at N > 16 when the
+  // grid of 64-row workgroups covers >= 5/8 of the CUs (>= 3/8 for N > 112):
+  // 1.05-2.6x the 16-row kernel there.  Four K phases per workgroup (16
+  // waves) when the grid is small, two when it already covers the GPU.
+  // Otherwise 16-row workgroups: four times the grid, for small M.
+  const int64_t wgs = (int64_t)(M / 64) * split_k;
+  const int64_t cus = device_cu_count();
+  const bool cwide =
+      split_k > 1 || (nb >= 2 && (wgs * 8 >= cus * 5 || (nb >= 8 && wgs * 8 >= cus * 3)));
+  const bool ph4 = wgs < 384;
+  if (cwide) {
+    if (nb <= 1)
+      e = ph4 ? launch_cwide<1, 4>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split)
+              : launch_cwide<1, 2>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
+    else if (nb <= 2)
+      e = ph4 ? launch_cwide<2, 4>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split)
+              : launch_cwide<2, 2>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
+    else if (nb <= 4)
+      e = ph4 ? launch_cwide<4, 4>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split)
+              : launch_cwide<4, 2>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
+    else
+      e = launch_cwide<8, 2>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
   } else if (nb <= 1) e = launch_gemm<1>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
   else if (nb <= 2) e = launch_gemm<2>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
   else if (nb <= 3) e = launch_gemm<3>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split);
