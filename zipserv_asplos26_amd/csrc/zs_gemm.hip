@@ -2,8 +2,9 @@
 //
 // The kernels decode one half median tile (16 rows x 32 columns) per wave
 // step: lane l owns matrix row l%16, columns 8*(l/16)..+7 (see zs_device.hpp).
-//   * decompress: one workgroup (4 waves) per 64x64 global tile (grid-stride),
-//     wave w = median tile w; each lane stores its 8 decoded bf16 as 16 bytes.
+//   * decompress: every wave walks every G-th median tile through a
+//     wave-private LDS stage ring; each lane stores its 8 decoded bf16 of
+//     each half as 16 bytes.
 //   * ZipGEMM, 16-row workgroups: one workgroup per 16-row band x split-K
 //     slice x 16*NB output columns; its waves take interleaved global-tile
 //     columns of the slice, stage each median tile through a wave-private
@@ -24,31 +25,81 @@
 
 namespace zs {
 
-__global__ __launch_bounds__(256) void decompress_kernel(Streams s, int start_exp, uint16_t* out,
-                                                         int M, int K) {
-  __shared__ DecodeTables T;
-  build_decode_tables(T, start_exp, threadIdx.x, blockDim.x);
+// ---------------------------------------------------------------------------
+// Decompress.  Every wave walks median tiles t = wave, wave + waves, ... of
+// the whole matrix (median tile t % 4 of global tile t / 4), copies each into
+// a wave-private LDS stage with two 16-byte loads per lane two tiles ahead
+// (stage_issue; the stream offsets come through the scalar cache one tile
+// before), decodes it from LDS (decode_median_pair) and stores its 16 rows
+// of 64 bf16 as two 16-byte stores per lane.  No barrier after the table
+// build: the stages are private to their wave.
+// ---------------------------------------------------------------------------
+constexpr int kDecompWaves = 16;
+
+__global__ __launch_bounds__(kDecompWaves * 64) void decompress_kernel(Streams s, int start_exp,
+                                                                       uint16_t* out, int M,
+                                                                       int K) {
+  __shared__ __attribute__((aligned(16)))
+  uint8_t smem[sizeof(DecodeTables) + kDecompWaves * 2 * kStBytes];
+  DecodeTables& T = *reinterpret_cast<DecodeTables*>(smem);
+  build_decode_tables(T, start_exp, threadIdx.x, kDecompWaves * 64);
   __syncthreads();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id();
+  uint8_t* stage0 = smem + sizeof(DecodeTables) + w * 2 * kStBytes;
+  uint8_t* stage1 = stage0 + kStBytes;
   const int KT = K >> 6;
-  const int64_t ngt = (int64_t)(M >> 6) * KT;
-  for (int64_t g = blockIdx.x; g < ngt; g += gridDim.x) {
-    const int64_t gm = g / KT, gk = g % KT;
-    int64_t smb = (int64_t)s.tog[2 * g] + s.tom[2 * (4 * g + w)];
-    int64_t fb = (int64_t)s.tog[2 * g + 1] + s.tom[2 * (4 * g + w) + 1];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      int tot;
-      const RowRef r = load_half_median(s, 512 * g + 128 * w + 64 * h, smb, fb, tot);
-      const u32x4 v = decode_row(s, T, r);
-      smb += tot;
-      fb += 512 - tot;
-      const int64_t row = gm * 64 + w * 16 + (l & 15);
-      const int64_t col = gk * 64 + h * 32 + 8 * (l >> 4);
-      *reinterpret_cast<u32x4*>(out + row * K + col) = v;
-    }
+  // median tiles < 2^31 (checked by the host)
+  const int ntiles = (M >> 4) * KT;
+  const int wid = blockIdx.x * kDecompWaves + w, nw = gridDim.x * kDecompWaves;
+  if (wid >= ntiles) return;
+  const int cnt = (ntiles - 1 - wid) / nw + 1;
+  auto tile_of = [&](int j) { return wid + min(j, cnt - 1) * nw; };  // clamped re-reads
+  const uint8_t* bm_lane = l < 8 ? s.bm1 : (l < 16 ? s.bm2 : s.bm3);
+  TileOff po;
+  auto offs = [&](int j) {
+    const int t = tile_of(j);
+    po = med_offsets_s(s, t >> 2, t & 3);
+  };
+  auto issue = [&](int j, StageRegs& R, StageMeta& Mt) {
+    const int t = tile_of(j);
+    stage_issue(s, bm_lane, t >> 2, t & 3, po, R, Mt);
+  };
+  StageRegs R0, R1;
+  StageMeta M0, M1;
+  offs(0);
+  issue(0, R0, M0);
+  offs(1);
+  issue(1, R1, M1);
+  offs(2);
+  stage_write(stage0, R0);
+  // Step j: tile j + 1 to its stage, tile j + 2 issued into the registers
+  // tile j used, tile j decoded and stored.
+#define DC_STEP(J, CUR, NXT, RC, MC, RN)                                                  \
+  {                                                                                      \
+    const StageMeta cm_ = MC;                                                            \
+    stage_write(NXT, RN);                                                                \
+    issue((J) + 2, RC, MC);                                                              \
+    offs((J) + 3);                                                                       \
+    u32x4 o0_, o1_;                                                                      \
+    decode_median_pair(T, T.e1, CUR + kStBm, 128, CUR + kStSm, cm_.sm_rel,               \
+                       reinterpret_cast<const uint16_t*>(CUR + kStFull), cm_.full_rel,   \
+                       cm_.full_direct, s.full + cm_.fa0, o0_, o1_);                     \
+    const int t_ = wid + (J) * nw;                                                       \
+    const int g_ = t_ >> 2, m_ = t_ & 3;                                                 \
+    const int gm_ = g_ / KT, gk_ = g_ - gm_ * KT;                                        \
+    uint16_t* dst_ = out + (int64_t)(gm_ * 64 + m_ * 16 + (l & 15)) * K + gk_ * 64 +     \
+                     8 * (l >> 4);                                                       \
+    *reinterpret_cast<u32x4*>(dst_) = o0_;                                               \
+    *reinterpret_cast<u32x4*>(dst_ + 32) = o1_;                                          \
   }
+  int j = 0;
+  for (; j + 2 <= cnt; j += 2) {
+    DC_STEP(j, stage0, stage1, R0, M0, R1);
+    DC_STEP(j + 1, stage1, stage0, R1, M1, R0);
+  }
+  if (j < cnt) DC_STEP(j, stage0, stage1, R0, M0, R1);
+#undef DC_STEP
 }
 
 // ---------------------------------------------------------------------------
@@ -228,28 +279,6 @@ struct CWideSmem {
   static constexpr int kRed = (PH - 1) * 4 * NB * 64 * 16;
   static constexpr int kBytes = kMain > kRed ? kMain : kRed;
 };
-
-// Stream offsets of median tile m of global tile g (both wave-uniform), read
-// through the scalar cache: first SM byte and FULL element of the median tile
-// and of the one after it (the tables of csrc/L_API.cu:356-357, :505-506 and
-// :541-549: TileOffsets_Global holds one more entry than there are tiles).
-__device__ __forceinline__ TileOff med_offsets_s(const Streams& s, int g, int m) {
-  using ci32 = const __attribute__((address_space(4))) int32_t;
-  ci32* tg = (ci32*)(s.tog + 2 * (int64_t)g);
-  ci32* tm = (ci32*)(s.tom + 8 * (int64_t)g + 2 * m);
-  const int t0 = tg[0], tf0 = tg[1];
-  TileOff t;
-  t.hf0 = t0 + tm[0];
-  t.f0 = tf0 + tm[1];
-  if (m < 3) {
-    t.hf1 = t0 + tm[2];
-    t.f1 = tf0 + tm[3];
-  } else {
-    t.hf1 = tg[2];
-    t.f1 = tg[3];
-  }
-  return t;
-}
 
 template <int NB, int PH, int RD>
 __global__ __launch_bounds__(4 * PH * 64) void cgemm_wide_kernel(Streams s, int start_exp,
@@ -551,9 +580,14 @@ extern "C" int zs_bf16_triple_bitmap_decompress(void* stream, const uint8_t* sm,
   (void)max_full;  // LDS staging sizes of the reference kernel; not needed here
   if (M <= 0 || K <= 0 || (M % 64) || (K % 64)) return ZS_E_INVAL;
   if (!streams_ok(sm, full, b1, b2, b3, tom, tog) || !out) return ZS_E_INVAL;
-  const int64_t ngt = (int64_t)(M / 64) * (K / 64);
-  const int64_t grid = std::min<int64_t>(ngt, (int64_t)device_cu_count() * 8);
-  hipLaunchKernelGGL(decompress_kernel, dim3((unsigned)grid), dim3(256), 0,
+  const int64_t ntiles = (int64_t)(M / 16) * (K / 64);
+  if (ntiles > INT32_MAX) return ZS_E_OVERFLOW;
+  // one 16-wave workgroup per CU (one table build each; two 8-wave ones
+  // measured 5-7% slower, two 12-wave ones the same), each wave on every
+  // G-th median tile
+  const int64_t grid = std::min<int64_t>((ntiles + kDecompWaves - 1) / kDecompWaves,
+                                         (int64_t)device_cu_count());
+  hipLaunchKernelGGL(decompress_kernel, dim3((unsigned)grid), dim3(kDecompWaves * 64), 0,
                      (hipStream_t)stream, make_streams(sm, full, b1, b2, b3, tom, tog),
                      (int)start_exp, out, M, K);
   return status_of(hipGetLastError());

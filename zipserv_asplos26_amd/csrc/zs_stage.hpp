@@ -64,6 +64,28 @@ __device__ __forceinline__ TileOff tile_off_at(const TileOff& v, int i) {
   return t;
 }
 
+// Stream offsets of median tile m of global tile g (both wave-uniform), read
+// through the scalar cache: first SM byte and FULL element of the median tile
+// and of the one after it (the tables of csrc/L_API.cu:356-357, :505-506 and
+// :541-549: TileOffsets_Global holds one more entry than there are tiles).
+__device__ __forceinline__ TileOff med_offsets_s(const Streams& s, int g, int m) {
+  using ci32 = const __attribute__((address_space(4))) int32_t;
+  ci32* tg = (ci32*)(s.tog + 2 * (int64_t)g);
+  ci32* tm = (ci32*)(s.tom + 8 * (int64_t)g + 2 * m);
+  const int t0 = tg[0], tf0 = tg[1];
+  TileOff t;
+  t.hf0 = t0 + tm[0];
+  t.f0 = tf0 + tm[1];
+  if (m < 3) {
+    t.hf1 = t0 + tm[2];
+    t.f1 = tf0 + tm[3];
+  } else {
+    t.hf1 = tg[2];
+    t.f1 = tg[3];
+  }
+  return t;
+}
+
 // `bm_lane` is this lane's bitmap plane (lanes 0-7: plane 1, 8-15: plane 2,
 // 16-23: plane 3), chosen once per kernel.
 __device__ __forceinline__ void stage_issue(const Streams& s, const uint8_t* bm_lane, int g, int m,
