@@ -364,7 +364,7 @@ def bench_kv(torch, zs, dev, gen):
             "decompress_timing": "HIP events, 5 calls", "cases": rows}
 
 
-def kernel_name(N, M, split_k):
+def kernel_name(N, M, split_k, K):
     """Kernel that zs_retiled_mm launches for batch N (mirrors its dispatch):
     N <= 16 -> rgemm_kernel<F, 1, W, D, XD> (F bands per wave: 2 when N > 8
     and M/16 >= 384, else 1; one 16-column block; W = 4 waves when N > 1 and
@@ -376,7 +376,8 @@ def kernel_name(N, M, split_k):
     otherwise), records 2 steps ahead; N > 32 on grids of >= 160 128-row
     workgroups -> rgemm_wide2_kernel<NB, 8, 2> (two bands per wave);
     4 <= N <= 16 on grids of M/64 * split_k >= 7/8 of the CU count ->
-    rgemm_wide_kernel<1, 4, PH, 2>."""
+    rgemm_wide_kernel<1, 4, PH, 2>; NB = 8 outside the two-band case takes 3
+    K phases when the split-K slice has >= 48 K tiles."""
     import torch
     nb = (N + 15) // 16
     cus = torch.cuda.get_device_properties(0).multi_processor_count
@@ -394,6 +395,8 @@ def kernel_name(N, M, split_k):
     if nb == 4 and M % 128 == 0 and (M // 128) * split_k >= 160:
         return "zs::rgemm_wide2_kernel<4, 8, 2>"
     ph = 4 if (nb <= 4 and (M // 64) * split_k < 384) else 2
+    if nb == 8 and ((K // 64) - 1) // split_k + 1 >= 48:
+        ph = 3
     return f"zs::rgemm_wide_kernel<{nb}, 4, {ph}, 2>"
 
 
@@ -739,7 +742,7 @@ def main():
                 if tc is None or t < tc:
                     tc, csk = t, sk_c
                 del cws
-            row = {"shape": name, "M": M, "K": K, "N": N, "kernel": kernel_name(N, M, sk),
+            row = {"shape": name, "M": M, "K": K, "N": N, "kernel": kernel_name(N, M, sk, K),
                    "split_k": sk, "cold_copies": nc,
                    "canonical_us": round(tc * 1e6, 3), "canonical_split_k": csk,
                    "zip_us": round(tz * 1e6, 3),

@@ -92,33 +92,36 @@ __device__ __forceinline__ void build_r_tables_exp(RTables& T, int tid, int nthr
 // together), then the specialisation and the LDS writes.  A kernel issues
 // its first record loads before r_tab_load so that their latency and the
 // image's overlap.
+// For NT not dividing 2048 the last round's surplus threads re-read the
+// image's last chunk (in bounds, no branch) and store nothing.
 template <int NT>
 struct RTabRegs {
-  static_assert(2048 % NT == 0, "table chunks per thread");
-  uint4 v[2048 / NT];
+  static constexpr int kC = (2048 + NT - 1) / NT;
+  uint4 v[kC];
 };
 template <int NT>
 __device__ __forceinline__ void r_tab_load(RTabRegs<NT>& t, int tid) {
   const uint4* src = reinterpret_cast<const uint4*>(kRTabImage.w);
 #pragma unroll
-  for (int k = 0; k < 2048 / NT; ++k) t.v[k] = src[tid + k * NT];
+  for (int k = 0; k < RTabRegs<NT>::kC; ++k) t.v[k] = src[min(tid + k * NT, 2047)];
 }
 template <int NT>
 __device__ __forceinline__ void r_tab_store(RTables& T, const RTabRegs<NT>& t, int tid) {
   uint4* dst = reinterpret_cast<uint4*>(T.tb);
 #pragma unroll
-  for (int k = 0; k < 2048 / NT; ++k) dst[tid + k * NT] = t.v[k];
+  for (int k = 0; k < RTabRegs<NT>::kC; ++k)
+    if (2048 % NT == 0 || tid + k * NT < 2048) dst[tid + k * NT] = t.v[k];
 }
 template <int NT>
 __device__ __forceinline__ void r_tab_store_exp(RTables& T, const RTabRegs<NT>& t, int tid,
                                                 uint32_t exp_lo, uint32_t exp_hi) {
   uint4* dst = reinterpret_cast<uint4*>(T.tb);
 #pragma unroll
-  for (int k = 0; k < 2048 / NT; ++k) {
+  for (int k = 0; k < RTabRegs<NT>::kC; ++k) {
     uint4 v = t.v[k];
     v.x = __builtin_amdgcn_perm(exp_hi, exp_lo, v.x);
     v.z = __builtin_amdgcn_perm(exp_hi, exp_lo, v.z);
-    dst[tid + k * NT] = v;
+    if (2048 % NT == 0 || tid + k * NT < 2048) dst[tid + k * NT] = v;
   }
 }
 

@@ -1284,8 +1284,9 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   // before the second, so consecutive MFMAs never depend on each other
   // (N = 128: 3-11% faster; at NB = 4 the extra registers cost more than
   // the latency they hide: 1-7% slower, so it keeps one read pair per
-  // column block next to its MFMAs).
-  constexpr bool kEarlyB = NB >= 8;
+  // column block next to its MFMAs).  Not with three K phases: the 12-wave
+  // workgroup needs the registers (<= 170 VGPRs for 3 waves per SIMD).
+  constexpr bool kEarlyB = NB >= 8 && PH < 3;
   auto b_read = [&](const uint8_t* xcur, bf16x8 (&b0)[NB], bf16x8 (&b1)[NB]) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
@@ -1990,6 +1991,11 @@ static int retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exp
       // once the 128-row grid still has >= 160 workgroups (measured)
       e = launch_rwide2<8, 8, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k,
                                  kb_per_split, fx);
+    else if (kb_per_split >= 48)
+      // three K phases (12 waves, 3 per SIMD, B fragments read next to
+      // their MFMAs) on long slices: 2-10% faster than two phases with the
+      // early B reads; on slices of <= 32 tiles the uneven phases cost more
+      e = launch_rwide<8, 4, 3>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
     else
       e = launch_rwide<8, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
   } else {
