@@ -372,8 +372,8 @@ def kernel_name(N, M, split_k, K):
     with two; X staged through LDS in XD-row loads: 1 for N <= 2, 2 for
     N <= 4, 4 for N <= 8, none (0) above); N > 16 ->
     rgemm_wide_kernel<NB, 4, PH, 2> with NB = 2, 4 or 8
-    column blocks, 4 row bands, 4 K phases when M/64 * split_k < 384 (2
-    otherwise), records 2 steps ahead; N > 32 on grids of >= 160 128-row
+    column blocks, 4 row bands, 4 K phases when M/64 * split_k <= the CU
+    count (2 otherwise), records 2 steps ahead; N > 32 on grids of >= 160 128-row
     workgroups -> rgemm_wide2_kernel<NB, 8, 2> (two bands per wave);
     4 <= N <= 16 on grids of M/64 * split_k >= 7/8 of the CU count ->
     rgemm_wide_kernel<1, 4, PH, 2>; NB = 8 outside the two-band case takes 3
@@ -382,7 +382,7 @@ def kernel_name(N, M, split_k, K):
     nb = (N + 15) // 16
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     if nb <= 1 and N >= 4 and (M // 64) * split_k * 8 >= cus * 7:
-        ph = 4 if (M // 64) * split_k < 384 else 2
+        ph = 4 if (M // 64) * split_k <= cus else 2
         return f"zs::rgemm_wide_kernel<1, 4, {ph}, 2>"
     if nb <= 1:
         waves = 4 if (N > 1 and M // 16 >= 640) else 8
@@ -394,7 +394,7 @@ def kernel_name(N, M, split_k, K):
         return "zs::rgemm_wide2_kernel<8, 8, 2>"
     if nb == 4 and M % 128 == 0 and (M // 128) * split_k >= 160:
         return "zs::rgemm_wide2_kernel<4, 8, 2>"
-    ph = 4 if (nb <= 4 and (M // 64) * split_k < 384) else 2
+    ph = 4 if (nb <= 4 and (M // 64) * split_k <= cus) else 2
     if nb == 8 and ((K // 64) - 1) // split_k + 1 >= 48:
         ph = 3
     return f"zs::rgemm_wide_kernel<{nb}, 4, {ph}, 2>"

@@ -1964,8 +1964,9 @@ static int retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exp
   const SplitFix fx{C, split_k > 1 ? counters : nullptr, split_k};
   const int nb = (N + 15) / 16;
   // N > 16: 64-row workgroups sharing each X tile through LDS; four K phases
-  // per workgroup (16 waves) when the grid is small, two when it already
-  // covers the GPU; N > 32 on large grids: 128-row workgroups with two
+  // per workgroup (16 waves, one workgroup per CU) when the grid fits one
+  // round of them, two otherwise (a 320-workgroup grid of 16-wave ones took
+  // two rounds: 38 us against 32 us with two phases, 10240x8192 at N = 8); N > 32 on large grids: 128-row workgroups with two
   // bands per wave.  4 <= N <= 16 with at least 7/8 of a workgroup per CU:
   // the same 64-row workgroups over one 16-column block (each X tile crosses
   // L2 once per four bands: 8-24% faster than one band per workgroup at
@@ -1973,7 +1974,7 @@ static int retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exp
   // workgroups of 8 K phases over one or two bands.
   const int64_t wide_wgs = (int64_t)(M / 64) * split_k;
   if (nb >= 2 || (N >= 4 && wide_wgs * 8 >= (int64_t)device_cu_count() * 7)) {
-    const bool ph4 = wide_wgs < 384;
+    const bool ph4 = wide_wgs <= (int64_t)device_cu_count();
     if (nb <= 1)
       e = ph4 ? launch_rwide<1, 4, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx)
               : launch_rwide<1, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
