@@ -618,13 +618,14 @@ extern "C" int zs_bf16_triple_bitmap_mm(void* stream, const uint8_t* sm, const u
   // tiles) for every split-K launch, and for one slice at N > 16 when the
   // grid of 64-row workgroups covers >= 5/8 of the CUs (>= 3/8 for N > 112):
   // 1.05-2.6x the 16-row kernel there.  Four K phases per workgroup (16
-  // waves) when the grid is small, two when it already covers the GPU.
+  // waves, one workgroup per CU) when the grid fits one round of them, two
+  // otherwise.
   // Otherwise 16-row workgroups: four times the grid, for small M.
   const int64_t wgs = (int64_t)(M / 64) * split_k;
   const int64_t cus = device_cu_count();
   const bool cwide =
       split_k > 1 || (nb >= 2 && (wgs * 8 >= cus * 5 || (nb >= 8 && wgs * 8 >= cus * 3)));
-  const bool ph4 = wgs < 384;
+  const bool ph4 = wgs <= cus;
   if (cwide) {
     if (nb <= 1)
       e = ph4 ? launch_cwide<1, 4>(st, s, start_exp, B, out, M, N, K, split_k, kb_per_split)
