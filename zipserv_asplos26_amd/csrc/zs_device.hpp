@@ -28,13 +28,16 @@ constexpr int kWave = 64;
 // them, zs_encode.hip's window check sums them).
 constexpr int kVerifySlices = 16;
 
-// LDS lookup tables used by the row decoder.  Indexed by one bitmap byte
-// (8 positions of a small-tile row); each entry is four dwords = eight 16-bit
-// lanes, lane j for position j.
+// LDS lookup tables used by the row decoder.  e1 is indexed by the plane-1
+// bitmap byte (8 positions of a small-tile row); each entry is four dwords =
+// eight 16-bit lanes, lane j for position j:
 //   e1[v] lane j = (start_exp + bit_j(v)) << 7
-//   e2[v] lane j = bit_j(v) << 8
-//   e3[v] lane j = bit_j(v) << 9
-// so e1[b1] + e2[b2] + e3[b3] = (start_exp + code_j) << 7 = the exponent field.
+// e23 covers planes 2 and 3 of four positions at once: indexed by a nibble
+// of each, u = n2 | n3 << 4, entry = two dwords, lane j (0..3) =
+//   (bit_j(n2) + 2 bit_j(n3)) << 8
+// so e1[b1] + (e23[lo(b2) | lo(b3) << 4], e23[hi(b2) | hi(b3) << 4]) =
+// (start_exp + code_j) << 7 = the exponent field (two 8-byte reads instead of
+// two 16-byte ones, from a 2 KB table).
 // Indexed by the in-window mask v = b1|b2|b3:
 //   sel[v]  dword d = v_perm selector bytes [r_2d, r_2d, r_2d+1, r_2d+1],
 //           r_j = set bits of v below j (rank of position j in the SM window);
@@ -43,17 +46,16 @@ constexpr int kVerifySlices = 16;
 //   omsk[v] dword d = 0xFFFF in the 16-bit lanes that are outliers.
 struct DecodeTables {
   uint4 e1[256];
-  uint4 e2[256];
-  uint4 e3[256];
   uint4 sel[256];
   uint4 osel[256];
   uint4 omsk[256];
+  uint2 e23[256];
 };
 
 __device__ __forceinline__ void build_decode_tables(DecodeTables& T, int start_exp, int tid,
                                                     int nthreads) {
   for (int v = tid; v < 256; v += nthreads) {
-    uint32_t e1[4], e2[4], e3[4], s[4], os[4], om[4];
+    uint32_t e1[4], s[4], os[4], om[4];
     uint32_t r[8], k[8];
     uint32_t rank = 0;
 #pragma unroll
@@ -66,16 +68,16 @@ __device__ __forceinline__ void build_decode_tables(DecodeTables& T, int start_e
     for (int d = 0; d < 4; ++d) {
       const uint32_t lo = (v >> (2 * d)) & 1, hi = (v >> (2 * d + 1)) & 1;
       e1[d] = ((uint32_t)(start_exp + lo) << 7) | ((uint32_t)(start_exp + hi) << 23);
-      e2[d] = (lo << 8) | (hi << 24);
-      e3[d] = (lo << 9) | (hi << 25);
       s[d] = r[2 * d] | (r[2 * d] << 8) | (r[2 * d + 1] << 16) | (r[2 * d + 1] << 24);
       const uint32_t klo = k[2 * d] & 3, khi = k[2 * d + 1] & 3;
       os[d] = (2 * klo) | ((2 * klo + 1) << 8) | ((2 * khi) << 16) | ((2 * khi + 1) << 24);
       om[d] = (lo ? 0u : 0xFFFFu) | (hi ? 0u : 0xFFFF0000u);
     }
     T.e1[v] = make_uint4(e1[0], e1[1], e1[2], e1[3]);
-    T.e2[v] = make_uint4(e2[0], e2[1], e2[2], e2[3]);
-    T.e3[v] = make_uint4(e3[0], e3[1], e3[2], e3[3]);
+    uint32_t c23[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c23[j] = ((v >> j) & 1) + 2 * ((v >> (4 + j)) & 1);
+    T.e23[v] = make_uint2((c23[0] << 8) | (c23[1] << 24), (c23[2] << 8) | (c23[3] << 24));
     T.sel[v] = make_uint4(s[0], s[1], s[2], s[3]);
     T.osel[v] = make_uint4(os[0], os[1], os[2], os[3]);
     T.omsk[v] = make_uint4(om[0], om[1], om[2], om[3]);
@@ -160,17 +162,17 @@ __device__ __forceinline__ u32x4 decode_inwindow(const DecodeTables& T, const ui
                                                  uint32_t ind, uint32_t w0, uint32_t w1,
                                                  uint32_t w2, uint32_t sh) {
   const uint4 x1 = e1[b1];
-  const uint4 x2 = T.e2[b2];
-  const uint4 x3 = T.e3[b3];
+  const uint2 y0 = T.e23[(b2 & 15u) | ((b3 & 15u) << 4)];
+  const uint2 y1 = T.e23[(b2 >> 4) | (b3 & 0xF0u)];
   const uint4 sel = T.sel[ind];
   const uint32_t s0 = __builtin_amdgcn_alignbyte(w1, w0, sh);
   const uint32_t s1 = __builtin_amdgcn_alignbyte(w2, w1, sh);
   const uint32_t msk = 0x807F807Fu;
   u32x4 o;
-  o[0] = (__builtin_amdgcn_perm(s1, s0, sel.x) & msk) | ((x1.x + x2.x + x3.x) & ~msk);
-  o[1] = (__builtin_amdgcn_perm(s1, s0, sel.y) & msk) | ((x1.y + x2.y + x3.y) & ~msk);
-  o[2] = (__builtin_amdgcn_perm(s1, s0, sel.z) & msk) | ((x1.z + x2.z + x3.z) & ~msk);
-  o[3] = (__builtin_amdgcn_perm(s1, s0, sel.w) & msk) | ((x1.w + x2.w + x3.w) & ~msk);
+  o[0] = (__builtin_amdgcn_perm(s1, s0, sel.x) & msk) | ((x1.x + y0.x) & ~msk);
+  o[1] = (__builtin_amdgcn_perm(s1, s0, sel.y) & msk) | ((x1.y + y0.y) & ~msk);
+  o[2] = (__builtin_amdgcn_perm(s1, s0, sel.z) & msk) | ((x1.z + y1.x) & ~msk);
+  o[3] = (__builtin_amdgcn_perm(s1, s0, sel.w) & msk) | ((x1.w + y1.y) & ~msk);
   return o;
 }
 
