@@ -187,3 +187,27 @@ def test_retiled_zipgemm_x_past_2gib(torch_cuda):
     torch.cuda.synchronize()
     err = float((y.float() - ref).abs().max() / ref.abs().max())
     assert err < 1e-2, err
+
+
+@pytest.mark.parametrize("split_k", [1, 2])
+def test_canonical_zipgemm_x_past_2gib(torch_cuda, split_k):
+    # The drop-in entry point addresses X with 64-bit pointers: one launch
+    # over X of more than 2^31 bytes, in the 16-row kernel (one slice) and
+    # the 64-row kernel (split-K), both against an fp32 product
+    import zipserv_asplos26_amd as zs_
+    torch = torch_cuda
+    M, K, N = 64, 4096, (1 << 18) + 48
+    assert N * K * 2 > 2**31 - 1
+    g = torch.Generator(device="cuda")
+    g.manual_seed(17 + split_k)
+    w = (torch.randn(M, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(N, K, device="cuda", generator=g).to(torch.bfloat16)
+    c = zs_.compress(w, window="weights")
+    y = zs_.zipgemm(c, x, split_k=split_k)
+    ref = torch.empty(N, M, dtype=torch.float32, device="cuda")
+    wf = w.float().t().contiguous()
+    for n0 in range(0, N, 1 << 16):
+        ref[n0:n0 + (1 << 16)] = x[n0:n0 + (1 << 16)].float() @ wf
+    torch.cuda.synchronize()
+    err = float((y.float() - ref).abs().max() / ref.abs().max())
+    assert err < 1e-2, err
