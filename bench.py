@@ -56,6 +56,15 @@ def parse():
                     help="profiling mode: only launch ZipGEMM of one shape eagerly ITERS times "
                          "(default 32) over HBM-cold copies (for rocprofv3 counter runs, which "
                          "see no graph replays), then print its mean time")
+    ap.add_argument("--eager-sweep", type=int, default=0, metavar="ITERS",
+                    help="counter mode: after a 256 MiB calibration copy, launch every "
+                         "(shape, N, split-K) ZipGEMM of the step's sweep eagerly ITERS times "
+                         "over HBM-cold copies, in a fixed order (see pmc_sweep_order)")
+    ap.add_argument("--pmc-summary", nargs=2, default=None, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print the markdown summary of two rocprofv3 --pmc runs (FETCH_SIZE, "
+                         "then WRITE_SIZE) of --eager-sweep; no GPU needed")
+    ap.add_argument("--pmc-iters", type=int, default=6,
+                    help="ITERS of the --eager-sweep run that --pmc-summary reads")
     return ap.parse_args()
 
 
@@ -96,9 +105,213 @@ def eager_gemm(spec):
                                 "comp_TBps": round(r.compressed_bytes / t / 1e12, 3)}}))
 
 
+def pmc_sweep_order():
+    """The (shape, M, K, N, split-K) launch groups of --eager-sweep, in the
+    order they are dispatched: every combination the step's split-K search
+    can pick, so the counters cover whatever split a bench run chooses."""
+    return [(name, M, K, N, sk) for name, M, K in SHAPES for N in NS for sk in SPLITS]
+
+
+def eager_sweep(iters):
+    """--eager-sweep: the 256 MiB calibration negation, then for every entry
+    of pmc_sweep_order() `iters` eager ZipGEMM launches (re-tiled layout,
+    in-kernel split-K sum, exactly one GEMM dispatch per call) rotating over
+    HBM-cold copies of that shape's weights (config 2 distribution)."""
+    import torch
+
+    import zipserv_asplos26_amd as zs
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    ca = torch.empty(CALIB_BYTES // 2, device=dev, dtype=torch.bfloat16).fill_(1.0)
+    torch.neg(ca, out=torch.empty_like(ca))
+    torch.cuda.synchronize()
+    del ca
+    order = pmc_sweep_order()
+    for name, M, K in SHAPES:
+        w = torch.randn(M, K, device=dev, generator=g) * 0.02
+        mask = torch.rand(M, K, device=dev, generator=g) < 0.001
+        w = torch.where(mask, w * 30.0, w).to(torch.bfloat16)
+        r = zs.compress_retiled(w)
+        del w, mask
+        nc = max(COLD_MIN_COPIES, -(-COLD_BYTES // r.compressed_bytes))
+        copies = [r] + [clone_retiled(r) for _ in range(nc - 1)]
+        for (n2, _, _, N, sk) in [o for o in order if o[0] == name]:
+            progress(f"eager sweep {name} N={N} split_k={sk}")
+            x = torch.randn(N, K, device=dev, generator=g).to(torch.bfloat16)
+            y = torch.empty(N, M, device=dev, dtype=torch.bfloat16)
+            ws = zs.codec.splitk_workspace(r, N, sk)
+            torch.cuda.synchronize()
+            for i in range(iters):
+                zs.zipgemm(copies[i % nc], x, split_k=sk, out=y, workspace=ws)
+            torch.cuda.synchronize()
+        del copies, r
+        torch.cuda.empty_cache()
+    print(json.dumps({"eager_sweep": {"iters": iters, "groups": len(order)}}))
+
+
+def _read_counter_csv(d):
+    """rocprofv3 counter_collection CSV under directory d -> list of
+    (kernel name, counter value) in dispatch order."""
+    import csv
+    import glob
+    files = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {d}")
+    rows = []
+    for fn in files:
+        with open(fn, newline="") as f:
+            for r in csv.DictReader(f):
+                rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return [(k, v) for _, k, v in rows]
+
+
+def pmc_summary(fetch_dir, write_dir, iters):
+    """Markdown summary of a FETCH_SIZE and a WRITE_SIZE run of --eager-sweep:
+    the negation's reading gives each counter's KiB -> bytes factor, and each
+    (shape, N, split-K) group's mean over its `iters` dispatches gives the
+    HBM bytes per launch that the roofline's `traffic` averages."""
+    fetch, write = _read_counter_csv(fetch_dir), _read_counter_csv(write_dir)
+    out = {}
+    for label, rows in (("FETCH_SIZE", fetch), ("WRITE_SIZE", write)):
+        neg = [v for k, v in rows if "neg" in k.lower()]
+        if not neg:
+            raise SystemExit(f"{label}: no negation (calibration) dispatch found")
+        gem = [(k, v) for k, v in rows if k.startswith("void zs::rgemm") or k.startswith("zs::rgemm")]
+        order = pmc_sweep_order()
+        if len(gem) != iters * len(order):
+            raise SystemExit(f"{label}: {len(gem)} ZipGEMM dispatches, expected "
+                             f"{iters} x {len(order)}")
+        out[label] = (max(neg), gem)
+    cal_f, gf = out["FETCH_SIZE"]
+    cal_w, gw = out["WRITE_SIZE"]
+    f_fac = (CALIB_BYTES / 1024) / cal_f
+    w_fac = (CALIB_BYTES / 1024) / cal_w
+    lines = [
+        f"Calibration: the {CALIB_BYTES >> 20} MiB bf16 negation reads {cal_f:.0f} KiB "
+        f"(FETCH_SIZE factor {f_fac:.4f}) and writes {cal_w:.0f} KiB (WRITE_SIZE factor "
+        f"{w_fac:.4f}).",
+        "",
+        "| shape | M x K | N | split-K | kernel | FETCH KiB | WRITE KiB | HBM bytes per launch |",
+        "|---|---|---|---|---|---|---|---|",
+    ]
+    tail = []
+    for gi, (name, M, K, N, sk) in enumerate(pmc_sweep_order()):
+        fk = [gf[gi * iters + i] for i in range(iters)]
+        wk = [gw[gi * iters + i] for i in range(iters)]
+        kern = fk[0][0].replace("void ", "").split("(")[0]
+        if any(k.replace("void ", "").split("(")[0] != kern for k, _ in fk + wk):
+            raise SystemExit(f"group {name} N={N} split_k={sk}: mixed kernels")
+        f = sum(v for _, v in fk) / iters
+        w = sum(v for _, v in wk) / iters
+        b = int(round(f * 1024 * f_fac + w * 1024 * w_fac))
+        lines.append(f"| {name} | {M}x{K} | {N} | {sk} | `{kern}` | {f:.0f} | {w:.0f} | {b} |")
+        tail.append(f"traffic {name} N={N} split_k={sk} kernel=`{kern}`: {b}")
+    return "\n".join(lines + [""] + tail) + "\n"
+
+
+PMC_PROFILE = os.path.join("profiles", "zs_rgemm_kernel_pmc_llama3-8b_sweep.md")
+
+
+def traffic_table(path=None):
+    """{(shape, N, split_k): (kernel, HBM bytes per launch)} from the committed
+    counter summary, {} when it is absent."""
+    path = path or os.path.join(ROOT, PMC_PROFILE)
+    tab = {}
+    if not os.path.exists(path):
+        return tab
+    with open(path) as f:
+        for line in f:
+            if not line.startswith("traffic "):
+                continue
+            head, val = line.rsplit(":", 1)
+            parts = head.split()
+            name = parts[1]
+            N = int(parts[2].split("=")[1])
+            sk = int(parts[3].split("=")[1])
+            kern = head.split("kernel=`", 1)[1].rstrip("`")
+            tab[(name, N, sk)] = (kern, int(val.strip()))
+    return tab
+
+
+def roofline_traffic(per, kernel, table):
+    """Mean counted HBM bytes per launch of `kernel` over the step's launches
+    of it (each (shape, N) at the split-K the step uses), or None unless the
+    counter table holds every one of those launches under the same kernel."""
+    vals = []
+    for row in per:
+        if row["kernel"] != kernel:
+            continue
+        hit = table.get((row["shape"], row["N"], row["split_k"]))
+        if hit is None or hit[0] != kernel:
+            return None
+        vals.append(hit[1])
+    return int(sum(vals) / len(vals)) if vals else None
+
+
 def progress(msg):
     """One progress line on stderr (the JSON result alone goes to stdout)."""
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def detail(name, data):
+    """One stdout line of detail (`{"detail": name, "data": ...}`), printed
+    before the final result line."""
+    print(json.dumps({"detail": name, "data": data}), flush=True)
+
+
+def final_line(res):
+    """The compact result line (the last stdout line): the contract's keys,
+    the roofline, the CPU baseline and one short summary per benchmark
+    config; the per-launch, per-kernel, KV, attention and 70B-sweep rows go
+    on the detail lines before it."""
+    out = {k: res[k] for k in ("metric", "value", "unit", "n_gpus", "steps", "warmup",
+                               "ms_per_step", "higher_is_better", "scaling", "vs_baseline",
+                               "dtype", "data", "config", "compression_ratio",
+                               "dense_TBps_effective", "speedup_vs_dense")}
+    rl = res["roofline"]
+    out["roofline"] = {k: rl[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic",
+                                          "kernel", "avg_launch_us", "launches",
+                                          "alg_bytes_per_launch")}
+    cb = res.get("cpu_baseline")
+    if cb is not None:
+        out["cpu_baseline"] = {k: cb[k] for k in ("value", "unit", "cores", "kind", "sample",
+                                                  "host_cpu", "compression_ratio",
+                                                  "round_trip_bit_exact")}
+        out["cpu_baseline"]["value_1core"] = cb["single_core"]["value"]
+    per = res.get("per_launch", [])
+    if per:
+        sp = [r["speedup"] for r in per if "speedup" in r]
+        out["per_launch_summary"] = {
+            "launches": len(per),
+            "speedup_min": min(sp) if sp else None, "speedup_max": max(sp) if sp else None,
+            "below_dense": sum(1 for s in sp if s < 1.0)}
+    c3 = res.get("c3_70b")
+    if c3 is not None:
+        out["c3_70b"] = {
+            "ratio": c3["compression_ratio"], "gpu_compress_GBps": c3["gpu_compress_GBps"],
+            "gpu_compress_kernels_GBps": c3["gpu_compress_kernels_GBps"],
+            "per_N [ms/token, comp TB/s, x dense]": {
+                str(r["N"]): [r["zip_ms_per_token"], r["comp_TBps"], r["speedup"]]
+                for r in c3["per_N"]}}
+    at = res.get("attention")
+    if at is not None:
+        cs = at["cases"]
+        out["attention"] = {
+            "cases": len(cs), "speedup_min": min(r["speedup"] for r in cs),
+            "speedup_max": max(r["speedup"] for r in cs),
+            "B64_T32k_us": next((r["zip_us"] for r in cs if r["B"] == 64 and r["T"] == 32768),
+                                None)}
+    kv = res.get("kv_cache")
+    if kv is not None:
+        cs = kv["cases"]
+        out["kv_cache"] = {
+            "cases": len(cs),
+            "bit_exact": all(r.get("bit_exact", True) and r["bit_exact_retiled"] for r in cs),
+            "ratio_retiled": [min(r["ratio_retiled"] for r in cs),
+                              max(r["ratio_retiled"] for r in cs)]}
+    return out
 
 
 def capture(torch, stream, fn):
@@ -216,11 +429,30 @@ def bench_c3(torch, zs, stream, gen, dev):
                     torch.matmul(xs[K], dense[li * 5 + si].t(), out=ys[M])
         tz = timed(torch, stream, [capture(torch, stream, zrun)], 3, 1) / 3
         td = timed(torch, stream, [capture(torch, stream, drun)], 3, 1) / 3 * (C3_LAYERS / 8)
+        # each shape alone: its 80 resident layers in one graph (ZipGEMM), its
+        # 8 dense copies (hipBLASLt), time per GEMM
+        shapes = []
+        for si, (name, M, K) in enumerate(C3_SHAPES):
+            def zone(si=si, M=M, K=K):
+                for L in comp:
+                    zs.zipgemm(L[si], xs[K], split_k=sk_of[si], out=ys[M], workspace=ws_of[si])
+
+            def done(si=si, M=M, K=K):
+                for li in range(8):
+                    torch.matmul(xs[K], dense[li * 5 + si].t(), out=ys[M])
+            t1 = timed(torch, stream, [capture(torch, stream, zone)], 3, 1) / (3 * C3_LAYERS)
+            d1 = timed(torch, stream, [capture(torch, stream, done)], 3, 1) / (3 * 8)
+            cb = sum(L[si].compressed_bytes for L in comp) / C3_LAYERS
+            shapes.append({"shape": name, "M": M, "K": K, "split_k": sk_of[si],
+                           "zip_us": round(t1 * 1e6, 2), "dense_us": round(d1 * 1e6, 2),
+                           "speedup": round(d1 / t1, 3),
+                           "comp_TBps": round(cb / t1 / 1e12, 3),
+                           "eff_TBps": round(2 * M * K / t1 / 1e12, 3)})
         rows.append({"N": N, "split_k": [sk_of[i] for i in range(len(C3_SHAPES))],
                      "zip_ms_per_token": round(tz * 1e3, 3),
                      "dense_ms_per_token": round(td * 1e3, 3), "speedup": round(td / tz, 3),
                      "eff_TBps": round(dense_bytes / tz / 1e12, 3),
-                     "comp_TBps": round(comp_bytes / tz / 1e12, 3)})
+                     "comp_TBps": round(comp_bytes / tz / 1e12, 3), "per_shape": shapes})
         del xs, ys
     del comp, dense
     torch.cuda.empty_cache()
@@ -400,21 +632,6 @@ def kernel_name(N, M, split_k, K):
     return f"zs::rgemm_wide_kernel<{nb}, 4, {ph}, 2>"
 
 
-def traffic_from_profile(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
-    summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a copy kernel of
-    known size); None when the summary has no line for this kernel."""
-    path = os.path.join(ROOT, "profiles", "zs_rgemm_kernel_pmc_llama3-8b_sweep.md")
-    if not os.path.exists(path):
-        return None
-    with open(path) as f:
-        for line in f:
-            if line.startswith("traffic_bytes_per_launch") and f"`{kernel}`" in line:
-                return {"bytes_per_launch": int(line.rsplit(":", 1)[1].strip()),
-                        "source": os.path.relpath(path, ROOT)}
-    return None
-
-
 def compress_kernel_seconds(torch, zs, x, window="kv", reps=3):
     """Device time of the re-tiled GPU encoder's kernels on the bf16 matrix x
     (window guess from a sample, fixed parts + counts + full histogram in one
@@ -589,6 +806,9 @@ def cpu_baseline(threads_cap=16):
 
 def main():
     args = parse()
+    if args.pmc_summary:
+        print(pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.pmc_iters), end="")
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1 "
                           "(multi-GPU sharding is a design note, not a run mode)"}))
@@ -603,6 +823,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.eager:
         eager_gemm(args.eager)
+        return
+    if args.eager_sweep:
+        eager_sweep(args.eager_sweep)
         return
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
@@ -784,7 +1007,7 @@ def main():
     dominant = max(kernels, key=lambda n: kernels[n]["time_s"])
     dk = kernels[dominant]
     achieved = dk["alg_bytes"] / dk["time_s"] / 1e9
-    traffic = traffic_from_profile(dominant)
+    traffic = roofline_traffic(per, dominant, traffic_table())
     out = {
         "metric": METRIC,
         "value": round(value, 4),
@@ -803,9 +1026,7 @@ def main():
             "shapes": {n: [m, k] for n, m, k in SHAPES},
             "N": NS,
             "split_k": "per (shape, N), fastest of 1/2/4 (see per_launch)",
-            "layout": "CDNA4 re-tiled records (zs_retiled_mm); canonical_us = the drop-in "
-                      "zs_bf16_triple_bitmap_mm on the canonical streams (its own fastest "
-                      "split-K of 1/2/4: canonical_split_k)",
+            "layout": "CDNA4 re-tiled records (zs_retiled_mm_fused)",
             "layers_resident": args.layers,
             "weights": "N(0,0.02) bf16, 0.1% x30 outliers",
             "parallelism": "single-gpu",
@@ -823,13 +1044,14 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None if traffic is None else traffic["bytes_per_launch"],
+            "traffic": traffic,
             "kernel": dominant,
+            "launches": dk["launches"],
             "avg_launch_us": dk["avg_us"],
             "alg_bytes_per_launch": dk["avg_alg_bytes"],
             "algorithmic_bytes": "comp_bytes(W) + 2*N*K + 2*N*M (+ 4*S*M*N split-K partials) per "
                                  "launch, averaged over the launches of this instantiation in one step",
-            "traffic_source": None if traffic is None else traffic["source"],
+            "traffic_source": PMC_PROFILE if traffic is not None else None,
         },
         "kernels": kernels,
         "per_launch": per,
@@ -846,7 +1068,11 @@ def main():
         out["attention"] = bench_attention(torch, zs, stream, gen, dev)
     if not args.no_c3:
         out["c3_70b"] = bench_c3(torch, zs, stream, gen, dev)
-    print(json.dumps(out))
+    for key in ("per_launch", "kernels", "cpu_baseline", "kv_cache", "attention", "c3_70b"):
+        if key in out:
+            detail(key, out[key])
+    detail("roofline", out["roofline"])
+    print(json.dumps(final_line(out)), flush=True)
 
 
 if __name__ == "__main__":

@@ -217,7 +217,8 @@ int zs_compress_retiled_fixed_gpu(void* stream, const uint16_t* d_input, int M, 
 /* zs_analyze_* + zs_compress_retiled_fixed_gpu in one input pass (when the
  * guess holds): the window (rule ZS_WINDOW_KV or ZS_WINDOW_WEIGHTS) is
  * guessed from a sample of the input (every 32nd 4096-byte chunk, or sparser
- * so that at most 512 chunks are read), the fixed parts,
+ * so that at most 128 chunks are read; a partial last chunk is not sampled),
+ * the fixed parts,
  * counts and slots are written under the guess while the full exponent
  * histogram is counted (d_hist, 256 x uint64, out), the rule picks the window
  * from the full histogram (d_top, out), and only if it differs from the guess
@@ -278,11 +279,13 @@ int zs_retiled_mm_fused(void* stream, const uint8_t* d_fixed, const uint8_t* d_e
  * static device array of the library, 32 MiB of partials + 64 Ki counters,
  * one copy per GPU held until the process ends: Split_K > 1 requires
  * Split_K * M * N * 2 <= 32 MiB and zs_retiled_mm_counters(M, N) <= 65536,
- * else ZS_E_OVERFLOW before any launch.  The first call on a device looks
- * the array up and clears its counters on `stream` (make it outside graph
- * capture); every completed call leaves them zero.  All calls on one GPU
- * share the array: calls that overlap in time on one GPU (other streams,
- * other threads) race and must not be issued. */
+ * else ZS_E_OVERFLOW before any launch.  Arguments are validated before
+ * the array is touched; Split_K == 1 never touches it.  The first Split_K > 1
+ * call on a device looks the array up and clears its counters with a fill
+ * kernel on `stream` (no memset node, so that call may also be captured);
+ * every completed call leaves them zero.  All calls on one GPU share the
+ * array: calls that overlap in time on one GPU (other streams, other
+ * threads) race and must not be issued. */
 int zs_retiled_mm_fused_noalloc(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
                                 const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B,
                                 uint16_t* C, int M, int N, int K, int Split_K);

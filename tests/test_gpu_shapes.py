@@ -25,6 +25,15 @@ sampled rows of W (first and last band included) against the CPU oracle
 zso_gemm_f32_mt, and on every element against an fp32 GEMM of the same bf16
 operands on the GPU.  Batches of one shape are the first N rows of one X, so
 one oracle GEMM per shape serves every N.
+
+That normwise bound cannot see one wrong weight (an exponent off by one moves
+Y by less than the tolerance at these sizes), so every C2 and C3 shape is
+also probed exactly (test_*_exact_probes): rows of X are unit vectors e_k
+(tests/zs_testutil.py probe_columns: one k in every K tile, the first and
+last column of every split-K slice), and every probed output column must
+equal the bf16 weight column W[:, k] bit for bit (as values: +0 == -0), for
+the re-tiled and the canonical (drop-in) kernels at every N and split-K
+{1, 2, 4} -- the mirror of test_mm.cu:861-936's full compare, made exact.
 """
 import hashlib
 import json
@@ -35,7 +44,8 @@ import pytest
 
 import oracle as zo
 import zipserv_asplos26_amd as zs
-from zs_testutil import from_torch_bf16, to_torch_bf16
+from zs_testutil import (from_torch_bf16, probe_batches, probe_columns, probe_mismatches,
+                         to_torch_bf16)
 
 pytestmark = pytest.mark.gpu
 
@@ -183,14 +193,52 @@ def test_c2_zipgemm(torch_cuda, name, M, K, N):
     _run_all_splits(torch, c, N, f"C2 {name} {M}x{K} N={N}")
 
 
+def _exact_probes(torch, c, m, N, sk, what):
+    """Unit-vector rows of X through ZipGEMM over `m` (re-tiled or canonical
+    streams of c.w) in batches of N at split-K sk: every probed output column
+    must equal the weight column it selects."""
+    cols = probe_columns(c.K, sk)
+    flat = [k for b in probe_batches(cols, N) for k in b]
+    P = len(flat)
+    idx = torch.tensor(flat, device="cuda")
+    X = torch.zeros(P, c.K, dtype=torch.bfloat16, device="cuda")
+    X[torch.arange(P, device="cuda"), idx] = 1.0
+    Y = torch.full((P, c.M), float("nan"), dtype=torch.bfloat16, device="cuda")
+    ws = zs.codec.splitk_workspace(m, N, sk) if sk > 1 else None
+    for j in range(0, P, N):
+        zs.zipgemm(m, X[j:j + N], split_k=sk, out=Y[j:j + N], workspace=ws)
+    want = c.w[:, idx].t()
+    bad = probe_mismatches(Y.float(), want.float())
+    assert bad == 0, f"{what}: {bad} of {P * c.M} probed weights differ ({len(cols)} columns)"
+
+
+def _probe_all(torch, c, ns, what):
+    canon = zs.compress(c.w, window="weights")
+    for N in ns:
+        for sk in SPLITS:
+            print(f"{what} N={N} split_k={sk}", flush=True)
+            _exact_probes(torch, c, c.r, N, sk, f"{what} re-tiled N={N} split_k={sk}")
+            _exact_probes(torch, c, canon, N, sk, f"{what} canonical N={N} split_k={sk}")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("name,M,K", C2_SHAPES)
+def test_c2_exact_probes(torch_cuda, name, M, K):
+    torch = torch_cuda
+    c = _case(torch, ("c2", name), M, K, max(C2_NS), 1000 + M + K, True)
+    _probe_all(torch, c, C2_NS, f"C2 {name} {M}x{K}")
+
+
 @pytest.mark.parametrize("name,M,K", C2_SHAPES)
 def test_c2_canonical_zipgemm(torch_cuda, name, M, K):
     # the drop-in entry point over the canonical streams at the real shapes
+    # (N = 17..32 at split-K 2 on the 14336-row shapes reaches the two-phase
+    # 64-row canonical kernel, cgemm_wide_kernel<2, 2, 2>)
     torch = torch_cuda
     c = _case(torch, ("c2", name), M, K, max(C2_NS), 1000 + M + K, True)
     canon = zs.compress(c.w, window="weights")
-    for N in (1, 16, 128):
-        for sk in (1, 2):
+    for N in C2_NS:
+        for sk in SPLITS:
             y = zs.zipgemm(canon, c.x[:N], split_k=sk)
             c.check(torch, y, N, f"C2 canonical {name} N={N} split_k={sk}")
 
@@ -208,6 +256,25 @@ def test_c3_zipgemm(torch_cuda, name, M, K, N):
     torch = torch_cuda
     c = _case(torch, ("c3", name), M, K, max(C3_NS), 2000 + M + K, False)
     _run_all_splits(torch, c, N, f"C3 {name} {M}x{K} N={N}")
+
+
+@pytest.mark.parametrize("name,M,K", C3_SHAPES)
+def test_c3_exact_probes(torch_cuda, name, M, K):
+    torch = torch_cuda
+    c = _case(torch, ("c3", name), M, K, max(C3_NS), 2000 + M + K, False)
+    _probe_all(torch, c, C3_NS, f"C3 {name} {M}x{K}")
+
+
+@pytest.mark.parametrize("name,M,K", C3_SHAPES)
+def test_c3_canonical_zipgemm(torch_cuda, name, M, K):
+    # the drop-in entry point over the canonical streams at the 70B shapes
+    torch = torch_cuda
+    c = _case(torch, ("c3", name), M, K, max(C3_NS), 2000 + M + K, False)
+    canon = zs.compress(c.w, window="weights")
+    for N in C3_NS:
+        for sk in SPLITS:
+            y = zs.zipgemm(canon, c.x[:N], split_k=sk)
+            c.check(torch, y, N, f"C3 canonical {name} N={N} split_k={sk}")
 
 
 @pytest.mark.parametrize("M,K,N", [(10240, 20480, 8), (1024, 36864, 1)])

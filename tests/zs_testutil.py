@@ -65,3 +65,44 @@ def attention_tolerance(ref, absv):
     does, flash_fwd_kernel.h:892-1074: each weight moves by at most 2^-8 of
     itself).  Arithmetic in fp32 adds far less than 2e-3 at these sizes."""
     return 2e-3 + 2.0 ** -8 * np.abs(ref) + 2.0 ** -8 * absv
+
+
+def probe_columns(K, split_k):
+    """Columns k of W probed with unit-vector rows of X (X[n] = e_k, so that
+    Y[n] = W[:, k] exactly: one exact product per output, every other term
+    zero, split-K partials W or 0).  One column in every 64-wide K tile (its
+    position inside the tile moving with the tile), the first and last
+    column of every split-K slice (the reference's partition, ceil(KT / S)
+    tiles per slice, L_Kernel.cuh:316-326), and k = 0, K - 1.  Every K tile
+    is one record per band, so every wave's K range, its first tile and any
+    tile past a wave's 64th are among them."""
+    kt = K // 64
+    cols = {0, K - 1}
+    for t in range(kt):
+        cols.add(64 * t + (37 * t + 11) % 64)
+    per = (kt - 1) // split_k + 1
+    for s in range(split_k):
+        t0, t1 = s * per, min(kt, (s + 1) * per)
+        if t0 < kt:
+            cols.update((64 * t0, 64 * t1 - 1))
+    return sorted(cols)
+
+
+def probe_batches(cols, n):
+    """`cols` in batches of exactly n (the kernel choice depends on N): the
+    last batch is filled up by repeating columns from the start."""
+    out = []
+    for i in range(0, len(cols), n):
+        b = cols[i:i + n]
+        while len(b) < n:
+            b = b + cols[:n - len(b)]
+        out.append(b)
+    return out
+
+
+def probe_mismatches(y, w_cols):
+    """Entries of Y that differ from the probed W columns (Y[n][m] against
+    W[m][k_n]), compared as values so that +0 and -0 are equal; works on
+    numpy float arrays and on torch tensors (returns the count)."""
+    diff = y != w_cols
+    return int(diff.sum())

@@ -699,8 +699,9 @@ static int analyze(hipStream_t st, const uint16_t* d_input, int64_t numel, C* d_
 
 namespace zs {
 
-// Window guess from a sample of the input (chunks of 2048 elements; numel a
-// multiple of 2048, input 16-byte aligned) into `guess`; the per-workgroup
+// Window guess from a sample of the input (chunks of 2048 elements, at most
+// kSampleChunks of them; a partial last chunk, when numel is not a multiple
+// of 2048, is not sampled; input 16-byte aligned) into `guess`; the per-workgroup
 // sample bins go to `sample` (kSampleGroups x 256), and `zero`
 // (kVerifySlices x 256 entries) is cleared on the way.
 hipError_t launch_window_sample(hipStream_t st, const uint16_t* in, int64_t numel,

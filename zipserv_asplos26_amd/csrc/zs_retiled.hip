@@ -1929,19 +1929,29 @@ extern "C" int zs_retiled_decompress(void* stream, const uint8_t* d_fixed, const
 
 // Split-K partial sums go to ws; with `counters` the GEMM kernel itself adds
 // them (last workgroup per tile), without it rsplitk_reduce_kernel does.
-static int retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
-                      const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B, uint16_t* C,
-                      int M, int N, int K, uint16_t* ws, int split_k, int32_t* counters) {
+// Argument checks of retiled_mm that do not depend on the split-K buffers.
+static int retiled_mm_args(const uint8_t* d_fixed, const uint8_t* d_exps, const int32_t* d_eoff,
+                           const uint16_t* B, const uint16_t* C, int M, int N, int K,
+                           int split_k) {
   if (!shape_ok(M, K) || N <= 0 || !d_fixed || !d_exps || !d_eoff || !B || !C) return ZS_E_INVAL;
   if ((reinterpret_cast<uintptr_t>(d_fixed) & 15) || (reinterpret_cast<uintptr_t>(d_exps) & 15) ||
       (reinterpret_cast<uintptr_t>(B) & 15) || (K % 8))
     return ZS_E_INVAL;
   const int KT = K / 64;
   if (split_k < 1 || split_k > KT) return ZS_E_INVAL;
-  if (split_k > 1 && !ws) return ZS_E_INVAL;
   // a band's records are addressed with 32-bit scalar offsets
   if ((int64_t)KT * kRecBytes > (int64_t)UINT32_MAX) return ZS_E_OVERFLOW;
   if ((int64_t)M * N * split_k > INT32_MAX * 2LL) return ZS_E_OVERFLOW;
+  return ZS_OK;
+}
+
+static int retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
+                      const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B, uint16_t* C,
+                      int M, int N, int K, uint16_t* ws, int split_k, int32_t* counters) {
+  const int chk = retiled_mm_args(d_fixed, d_exps, d_eoff, B, C, M, N, K, split_k);
+  if (chk != ZS_OK) return chk;
+  if (split_k > 1 && !ws) return ZS_E_INVAL;
+  const int KT = K / 64;
   if ((int64_t)N * K * 2 > INT32_MAX) {
     // The kernels address X with 32-bit byte offsets: run row blocks of X
     // and Y that stay below 2^31 bytes, one after another on the stream.
@@ -2098,16 +2108,18 @@ extern "C" int zs_retiled_mm_fused_noalloc(void* stream, const uint8_t* d_fixed,
                                            const uint8_t* d_exps, const int32_t* d_eoff,
                                            uint8_t start_exp, const uint16_t* B, uint16_t* C,
                                            int M, int N, int K, int split_k) {
-  if (M <= 0 || N <= 0 || split_k < 1) return ZS_E_INVAL;
-  if (split_k > 1) {
-    // the partial slabs [split_k][N][M] and the tile counters must fit
-    if ((int64_t)split_k * M * N * 2 > kScratchSlabBytes) return ZS_E_OVERFLOW;
-    if (zs_retiled_mm_counters(M, N) > kScratchCounters) return ZS_E_OVERFLOW;
-  }
+  const int chk = retiled_mm_args(d_fixed, d_exps, d_eoff, B, C, M, N, K, split_k);
+  if (chk != ZS_OK) return chk;
+  if (split_k == 1)  // no partial sums: the scratch array is not touched
+    return retiled_mm(stream, d_fixed, d_exps, d_eoff, start_exp, B, C, M, N, K, nullptr, 1,
+                      nullptr);
+  // the partial slabs [split_k][N][M] and the tile counters must fit
+  if ((int64_t)split_k * M * N * 2 > kScratchSlabBytes) return ZS_E_OVERFLOW;
+  if (zs_retiled_mm_counters(M, N) > kScratchCounters) return ZS_E_OVERFLOW;
   uint8_t* base = nullptr;
   const int st = scratch_of((hipStream_t)stream, &base);
   if (st != ZS_OK) return st;
-  uint16_t* ws = split_k > 1 ? reinterpret_cast<uint16_t*>(base) : nullptr;
-  int32_t* cnt = split_k > 1 ? reinterpret_cast<int32_t*>(base + kScratchSlabBytes) : nullptr;
-  return retiled_mm(stream, d_fixed, d_exps, d_eoff, start_exp, B, C, M, N, K, ws, split_k, cnt);
+  return retiled_mm(stream, d_fixed, d_exps, d_eoff, start_exp, B, C, M, N, K,
+                    reinterpret_cast<uint16_t*>(base), split_k,
+                    reinterpret_cast<int32_t*>(base + kScratchSlabBytes));
 }
