@@ -301,6 +301,8 @@ def final_line(res):
         out["attention"] = {
             "cases": len(cs), "speedup_min": min(r["speedup"] for r in cs),
             "speedup_max": max(r["speedup"] for r in cs),
+            "token_major_vs_head_major": [min(r["token_major_vs_head_major"] for r in cs),
+                                          max(r["token_major_vs_head_major"] for r in cs)],
             "B64_T32k_us": next((r["zip_us"] for r in cs if r["B"] == 64 and r["T"] == 32768),
                                 None)}
     kv = res.get("kv_cache")
@@ -489,10 +491,21 @@ def bench_attention(torch, zs, stream, gen, dev):
         canonical = k.numel() <= 2**31 - 1
         ck, cv = (za.compress_kv(k), za.compress_kv(v)) if canonical else (None, None)
         rk, rv = za.compress_kv(k, retiled=True), za.compress_kv(v, retiled=True)
-        # staged comparator (bench_zipserv_decode_attention.py:752-796): token-major
-        # compressed caches decompressed into a dense workspace, then the dense kernel
+        # token-major caches (rows b * batch_stride + t * Hkv + h): fused attention,
+        # and the staged comparator (bench_zipserv_decode_attention.py:752-796) --
+        # the caches decompressed into dense buffers, then the dense kernel
         sk_, sv_ = (za.compress_kv(k, layout="token_major", retiled=True),
                     za.compress_kv(v, layout="token_major", retiled=True))
+        kbuf = torch.empty(sk_.rows, sk_.cols, dtype=torch.bfloat16, device=dev)
+        vbuf = torch.empty(sv_.rows, sv_.cols, dtype=torch.bfloat16, device=dev)
+        cap = sk_.rows // B // 8
+        sl = torch.full((B,), T, dtype=torch.int32, device=dev)
+
+        def staged():
+            zs.decompress_retiled(sk_, kbuf)
+            zs.decompress_retiled(sv_, vbuf)
+            za.flash_attn_with_kvcache_dense(q, kbuf.view(B, cap, 8, 128), vbuf.view(B, cap, 8, 128),
+                                             cache_seqlens=sl)
         torch.cuda.synchronize()
         reps = 10
         tc = timed(torch, stream, [capture(torch, stream, lambda: [
@@ -502,25 +515,31 @@ def bench_attention(torch, zs, stream, gen, dev):
             za.flash_attn_with_kvcache_zipserv(q, rk, rv, 8, T) for _ in range(reps)])], 3, 1) / (3 * reps)
         td = timed(torch, stream, [capture(torch, stream, lambda: [
             za.flash_attn_with_kvcache_dense(q, k, v) for _ in range(reps)])], 3, 1) / (3 * reps)
-        ts = timed(torch, stream, [capture(torch, stream, lambda: [
+        tt = timed(torch, stream, [capture(torch, stream, lambda: [
             za.flash_attn_with_kvcache_zipserv(q, sk_, sv_, 8, T) for _ in range(reps)])], 3, 1) / (
             3 * reps)
+        ts = timed(torch, stream, [capture(torch, stream, lambda: [
+            staged() for _ in range(reps)])], 3, 1) / (3 * reps)
         comp = rk.compressed_bytes + rv.compressed_bytes
         dense = 2 * k.numel() * 2
         rows.append({"B": B, "T": T, "zip_us": round(tz * 1e6, 2),
                      "canonical_us": round(tc * 1e6, 2) if tc else None,
                      "dense_us": round(td * 1e6, 2),
+                     "token_major_us": round(tt * 1e6, 2),
                      "staged_us": round(ts * 1e6, 2),
                      "speedup": round(td / tz, 3), "speedup_vs_staged": round(ts / tz, 3),
+                     "token_major_vs_head_major": round(tz / tt, 3),
+                     "token_major_speedup": round(td / tt, 3),
                      "ratio": round(dense / comp, 4),
                      "comp_TBps": round((comp + 2 * 2 * B * 64 * 128) / tz / 1e12, 3),
                      "dense_TBps": round((dense + 2 * 2 * B * 64 * 128) / td / 1e12, 3)})
-        del k, v, q, ck, cv, rk, rv, sk_, sv_
+        del k, v, q, ck, cv, rk, rv, sk_, sv_, kbuf, vbuf
         torch.cuda.empty_cache()
     return {"heads": 64, "heads_k": 8, "head_dim": 128, "kv": "N(0,1) x lognormal(0,1) per channel",
             "note": "reps captured in one HIP graph; time per call; zip_us = fused over re-tiled "
-                    "head-major KV, canonical_us = fused over canonical TCA-TBE KV, staged_us = "
-                    "token-major re-tiled KV decompressed into a workspace then the dense kernel, "
+                    "head-major KV, canonical_us = fused over canonical TCA-TBE KV, "
+                    "token_major_us = fused over re-tiled token-major KV, staged_us = the "
+                    "token-major caches decompressed into dense buffers then the dense kernel, "
                     "dense_us = the dense kernel over bf16 KV", "cases": rows}
 
 

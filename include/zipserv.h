@@ -354,12 +354,24 @@ typedef struct zs_kv_retiled {
   int32_t layout; /* ZS_LAYOUT_*                                           */
 } zs_kv_retiled_t;
 
+/* TOKEN_MAJOR re-tiled caches with num_heads_k == 8 and head_dim 128 are
+ * decoded inside the attention kernel (flash_fwd_kernel.h:325-430, :449,
+ * :522-536 decode token-major tiles in the kernel too): one workgroup per
+ * (batch, split) decodes each record once for all 8 heads and exchanges the
+ * rows through LDS; same result, bit for bit, as the dense kernel with one
+ * wave per (batch, head, split).  Other token-major caches run staged as in
+ * zs_decode_attention. */
 int zs_decode_attention_retiled(void* stream, const uint16_t* q, const zs_kv_retiled_t* k,
                                 const zs_kv_retiled_t* v, const int32_t* cache_seqlens,
                                 int seqlen_k, int batch, int num_heads, int num_heads_k,
                                 int head_dim, float softmax_scale, uint16_t* out,
                                 float* softmax_lse, void* workspace, size_t workspace_bytes,
                                 int num_splits);
+/* Staging bytes zs_decode_attention_retiled needs for one cache in front of
+ * its split workspace: 0 for head-major caches and for fused token-major
+ * ones (num_heads_k == 8, cols == 128), zs_kv_staging_bytes otherwise; -1
+ * for bad arguments.  No counterpart in the reference. */
+int64_t zs_kv_retiled_staging_bytes(int layout, int rows, int cols, int num_heads_k);
 
 /* The uncompressed comparator (bench_zipserv_decode_attention.py:629-631,
  * dense flash_attn_with_kvcache): same kernel with K/V read from dense bf16

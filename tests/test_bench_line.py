@@ -38,6 +38,8 @@ def _stub_result():
                     for N in bench.C3_NS]}
     att = {"cases": [{"B": B, "T": T, "zip_us": 16.23, "canonical_us": 24.51, "dense_us": 11.71,
                       "staged_us": 31.4, "speedup": 0.722, "speedup_vs_staged": 1.935,
+                      "token_major_us": 18.5, "token_major_vs_head_major": 0.88,
+                      "token_major_speedup": 0.63,
                       "ratio": 1.3509, "comp_TBps": 0.767, "dense_TBps": 1.435}
                      for B, T in bench.ATTN_CASES]}
     kv = {"cases": [{"B": B, "T": T, "ratio_retiled": 1.35, "bit_exact": True,

@@ -52,10 +52,11 @@ def _run(torch_cuda, B, T, Hkv, H, seqlens=None, splits=0, seed=0, q_zero=False,
             from_torch_bf16(outd.view(B, H, D)), lsed.cpu().numpy(), ref, ref_lse, absv)
 
 
-def _check(res, seqlens=None):
+def _check(res, seqlens=None, exact=True):
     q, k, v, out, lse, outd, lsed, ref, ref_lse, absv = res
-    np.testing.assert_array_equal(out, outd)  # compressed == dense, bit for bit
-    np.testing.assert_array_equal(lse, lsed)
+    if exact:
+        np.testing.assert_array_equal(out, outd)  # compressed == dense, bit for bit
+        np.testing.assert_array_equal(lse, lsed)
     o = _bf16_f32(out)
     tol = attention_tolerance(ref, absv)
     err = np.abs(o - ref)
@@ -112,10 +113,54 @@ def test_attention_ragged_seqlens(torch_cuda, splits):
     (4, 300, 8, 64, 0, [300, 17, 0, 64]),
 ])
 def test_attention_token_major(torch_cuda, retiled, B, T, Hkv, H, splits, seqlens):
-    # token-major caches (row b*batch_stride + t*Hkv + h) run staged: the
-    # result equals the dense kernel's bit for bit, and the oracle's
+    # token-major caches (row b*batch_stride + t*Hkv + h): canonical ones and
+    # re-tiled ones with Hkv != 8 run staged (the result equals the dense
+    # kernel's bit for bit); re-tiled ones with Hkv == 8 run fused, whose
+    # splits follow their own rule -- the oracle bound holds either way
+    fused = retiled and Hkv == 8
     _check(_run(torch_cuda, B, T, Hkv, H, seqlens=seqlens, splits=splits, seed=11,
-                retiled=retiled, layout="token_major"), seqlens)
+                retiled=retiled, layout="token_major"), seqlens, exact=not fused)
+
+
+@pytest.mark.parametrize("B,T,splits,seqlens", [
+    (1, 64, 1, None),
+    (2, 1000, 16, None),            # 64-token chunks, masked tail
+    (3, 100, 2, None),              # T * 8 not a multiple of 64: padded batch rows
+    (4, 300, 5, [300, 17, 0, 64]),  # ragged lengths, an empty sequence
+    (8, 4096, 32, None),            # 2048 (batch, head, split) items, 128-token chunks
+])
+def test_attention_token_major_fused_exact(torch_cuda, B, T, splits, seqlens):
+    # Fused token-major attention (8 KV heads, 64 query heads): with splits
+    # whose chunks the dense kernel also walks with one wave per (batch,
+    # head, split) -- 64-token chunks, or >= 2048 items -- both run the same
+    # operands through the same arithmetic: bit-identical, and within the
+    # oracle bound
+    _check(_run(torch_cuda, B, T, 8, 64, seqlens=seqlens, splits=splits, seed=29, retiled=True,
+                layout="token_major"), seqlens)
+
+
+@pytest.mark.parametrize("B,T,H,splits,seqlens", [
+    (1, 4096, 64, 0, None),          # automatic splits (config-5 shape)
+    (2, 1000, 64, 3, None),          # 336-token chunks
+    (2, 700, 8, 0, None),            # MHA-sized group 1
+    (2, 333, 128, 0, None),          # GQA group 16
+    (4, 300, 64, 0, [300, 17, 0, 64]),
+    (2, 100, 64, 6, None),           # 32-token chunks: the last two splits are empty
+    (5, 17, 64, 0, [17, 1, 16, 9, 0]),
+])
+def test_attention_token_major_fused_oracle(torch_cuda, B, T, H, splits, seqlens):
+    _check(_run(torch_cuda, B, T, 8, H, seqlens=seqlens, splits=splits, seed=31, retiled=True,
+                layout="token_major"), seqlens, exact=False)
+
+
+def test_attention_token_major_fused_needs_no_staging(torch_cuda):
+    import zipserv_asplos26_amd as zs
+    L = zs.lib()
+    tm, hm = zs._lib.ZS_LAYOUT_TOKEN_MAJOR, zs._lib.ZS_LAYOUT_HEAD_MAJOR
+    assert L.zs_kv_retiled_staging_bytes(tm, 1024, 128, 8) == 0
+    assert L.zs_kv_retiled_staging_bytes(tm, 1024, 128, 4) == 1024 * 128 * 2
+    assert L.zs_kv_retiled_staging_bytes(hm, 1024, 128, 8) == 0
+    assert L.zs_kv_retiled_staging_bytes(7, 1024, 128, 8) == -1
 
 
 def test_attention_single_token_returns_v(torch_cuda):
@@ -310,9 +355,11 @@ def test_compress_kv_paged_staged(torch_cuda, retiled):
     ref_pages, per_seq = za.make_batched_paged_kv_cache(kd, page)
     assert torch.equal(kp.view(torch.int16), ref_pages.view(torch.int16))
     bt = torch.arange(B * per_seq, dtype=torch.int32, device="cuda").view(B, per_seq)
-    # one split each: the same token chunks although seqlen_k differs (300 / 304)
-    out = za.flash_attn_with_kvcache_zipserv(qd.view(B, 1, H, D), ck, cv, Hkv, T, num_splits=1)
+    # five splits each: the same 64-token chunks although seqlen_k differs
+    # (300 / 304), one wave per (batch, head, split) in every kernel (the
+    # re-tiled cache runs fused, the canonical one staged)
+    out = za.flash_attn_with_kvcache_zipserv(qd.view(B, 1, H, D), ck, cv, Hkv, T, num_splits=5)
     outp = za.flash_attn_with_kvcache_dense(qd.view(B, 1, H, D), kp, vp, cache_seqlens=T,
-                                            block_table=bt, num_splits=1)
+                                            block_table=bt, num_splits=5)
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), outp.view(torch.int16))

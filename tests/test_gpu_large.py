@@ -12,7 +12,11 @@ cache and within 2e-3 (plus the bf16 rounding terms of test_gpu_attention)
 of an fp32 reference on sampled batch entries, lse included.  The same at
 benchmark config 4's largest cache (B = 32, T = 128k: 2^32 elements per
 tensor, a fixed part past 4 GiB), and config-5 points (B = 8, T = 16k;
-B = 32, T = 32k) against the fp64 oracle on sampled batch entries.
+B = 32, T = 32k) against the fp64 oracle on sampled batch entries.  The
+token-major layout's fused attention runs on the 2.16 G-element caches and
+the config-5 points too: bit-identical to the dense kernel where both walk
+the same chunks with one wave per (batch, head, split), and within the
+oracle bound with its own automatic splits.
 """
 import math
 
@@ -124,6 +128,20 @@ def test_retiled_kv_and_attention_past_int32(torch_cuda):
     B = 64
     q, k, v, _, out, lse = _large_kv_case(torch, B, 33000, 11, True)
     _check_sampled(torch, q, k, v, out, lse, (0, 37, B - 1))
+    # the same caches token-major (fused attention): 4 splits give both the
+    # fused and the dense kernel 8256-token chunks and 2048 (batch, head,
+    # split) items of one wave each, so the outputs are the same bit for bit
+    import zipserv_asplos26_amd.attention as za
+    del out, lse
+    tk = za.compress_kv(k, layout="token_major", retiled=True)
+    tv = za.compress_kv(v, layout="token_major", retiled=True)
+    outt, lset = za.flash_attn_with_kvcache_zipserv(q, tk, tv, 8, 33000, num_splits=4,
+                                                    return_softmax_lse=True)
+    outd, lsed = za.flash_attn_with_kvcache_dense(q, k, v, num_splits=4, return_softmax_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(outt.view(torch.int16), outd.view(torch.int16))
+    assert torch.equal(lset, lsed)
+    _check_sampled(torch, q, k, v, outt, lset, (0, B - 1))
 
 
 def test_retiled_kv_past_4g_elements(torch_cuda):
@@ -157,14 +175,24 @@ def test_attention_config5_points_against_oracle(torch_cuda, B, T):
     outd = za.flash_attn_with_kvcache_dense(q, k, v)
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), outd.view(torch.int16))
+    # token-major caches, fused: automatic splits against the oracle, and with
+    # T / 512 splits (>= 2048 one-wave items, equal chunks) against dense
+    tk = za.compress_kv(k, layout="token_major", retiled=True)
+    tv = za.compress_kv(v, layout="token_major", retiled=True)
+    outt, lset = za.flash_attn_with_kvcache_zipserv(q, tk, tv, Hkv, T, return_softmax_lse=True)
+    oute = za.flash_attn_with_kvcache_zipserv(q, tk, tv, Hkv, T, num_splits=T // 512)
+    outde = za.flash_attn_with_kvcache_dense(q, k, v, num_splits=T // 512)
+    torch.cuda.synchronize()
+    assert torch.equal(oute.view(torch.int16), outde.view(torch.int16))
     for b in (0, B - 1):
         qb = from_torch_bf16(q[b:b + 1, 0])
         kb, vb = from_torch_bf16(k[b:b + 1]), from_torch_bf16(v[b:b + 1])
         ref, ref_lse, absv = zo.decode_attention_f64(qb, kb, vb, return_absv=True)
-        o = zo.bf16_to_f32(from_torch_bf16(out[b:b + 1, 0])).astype(np.float64)
-        err = np.abs(o - ref)
-        assert np.all(err <= attention_tolerance(ref, absv)), (b, err.max())
-        np.testing.assert_allclose(lse[b:b + 1].cpu().numpy(), ref_lse, rtol=1e-4, atol=1e-3)
+        for o_, l_ in ((out, lse), (outt, lset)):
+            o = zo.bf16_to_f32(from_torch_bf16(o_[b:b + 1, 0])).astype(np.float64)
+            err = np.abs(o - ref)
+            assert np.all(err <= attention_tolerance(ref, absv)), (b, err.max())
+            np.testing.assert_allclose(l_[b:b + 1].cpu().numpy(), ref_lse, rtol=1e-4, atol=1e-3)
 
 
 def test_retiled_zipgemm_x_past_2gib(torch_cuda):

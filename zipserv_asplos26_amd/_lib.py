@@ -84,6 +84,7 @@ SIGNATURES = {
         C.c_int, [_p, _p, _p, _p, _p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                   _p, _p, _p, C.c_size_t, C.c_int]),
     "zs_kv_staging_bytes": (C.c_int64, [C.c_int, C.c_int, C.c_int]),
+    "zs_kv_retiled_staging_bytes": (C.c_int64, [C.c_int, C.c_int, C.c_int, C.c_int]),
     "zs_decode_attention_workspace_bytes": (
         C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "zs_decode_attention_retiled": (

@@ -243,8 +243,9 @@ def flash_attn_with_kvcache_zipserv(q, zipserv_k, zipserv_v, zipserv_num_heads_k
     sl = _seqlens(cache_seqlens, B, q.device)
     L = lib()
     wsb = int(L.zs_decode_attention_workspace_bytes(B, H, D, seqlen_k, num_splits))
-    for d in (dk, dv):  # token-major caches are decompressed into the workspace first
-        wsb += int(L.zs_kv_staging_bytes(d.layout, d.rows, d.cols))
+    for d in (dk, dv):  # staged token-major caches are decompressed into the workspace first
+        wsb += int(L.zs_kv_retiled_staging_bytes(d.layout, d.rows, d.cols, zipserv_num_heads_k)
+                   if retiled else L.zs_kv_staging_bytes(d.layout, d.rows, d.cols))
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=q.device)
     import ctypes
     fn_name = "zs_decode_attention_retiled" if retiled else "zs_decode_attention"

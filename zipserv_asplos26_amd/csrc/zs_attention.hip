@@ -108,6 +108,74 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
          ((uint32_t)__builtin_bit_cast(unsigned short, hb) << 16);
 }
 
+// Per-wave attention state over one (batch, KV head, token range): the q^T
+// fragments (B operand, lane l -> head l%16 of the group, dims 32c +
+// 8*(l/16)..+7), the O^T accumulators (lane l: head l%16, dims 16*i +
+// 4*(l/16) + r of O[i]), the running max and sum (log2 domain), and the
+// current 16 tokens' scores S^T and softmax weights P^T (bf16 pairs).
+struct AttnWave {
+  bf16x8 Q[4];
+  f32x4 O[8];
+  float m_run, l_run;
+  f32x4 S;
+  uint32_t pb0, pb1;
+};
+
+// K step TY (0: dims 0..63, 1: dims 64..127) of 16 tokens: S^T += K q^T with
+// the K fragment (lane l: token l%16, dims 8*(l/16)..+7 in a0, +32 in a1) as
+// the A operand.
+__device__ __forceinline__ void attn_k_step(AttnWave& a, int TY, u32x4 a0, u32x4 a1) {
+  if (TY == 0) a.S = f32x4{0.f, 0.f, 0.f, 0.f};
+  a.S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0), a.Q[2 * TY], a.S, 0, 0, 0);
+  a.S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1), a.Q[2 * TY + 1], a.S, 0, 0, 0);
+}
+
+// Online softmax over the 16 tokens of S^T (log2 domain): this lane holds
+// tokens tb..tb+3 of head l%16; tokens >= t1 are masked.  Rescales O and
+// leaves the bf16 weights in pb0 / pb1 (the B operand P^T of the V steps).
+__device__ __forceinline__ void attn_softmax(AttnWave& a, int tb, int t1, float scale_log2) {
+  float s[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    s[r] = (tb + r < t1) ? a.S[r] * scale_log2 : -INFINITY;
+    mx = fmaxf(mx, s[r]);
+  }
+  mx = wave_max16(mx);
+  const float m_new = fmaxf(a.m_run, mx);
+  const float m_use = m_new == -INFINITY ? 0.f : m_new;
+  const float alpha = __builtin_amdgcn_exp2f(a.m_run - m_use);
+  float pr[4], ps = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    pr[r] = __builtin_amdgcn_exp2f(s[r] - m_use);
+    ps += pr[r];
+  }
+  ps = wave_sum16(ps);
+  a.l_run = a.l_run * alpha + ps;
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a.O[i] *= alpha;
+  }
+  a.m_run = m_new;
+  a.pb0 = pack_bf16x2(pr[0], pr[1]);
+  a.pb1 = pack_bf16x2(pr[2], pr[3]);
+}
+
+// V step TY (2: dims 0..63, 3: dims 64..127): O^T += V^T P^T, the A operand
+// V^T read with ds_read_b64_tr_b16 from the 16-token x 64-dim V tile in LDS
+// (row pitch kVRow), `vt` = the tile + this lane's transposed-read offset.
+__device__ __forceinline__ void attn_v_step(AttnWave& a, int TY, const uint8_t* vt) {
+  const v4i16 pbv = __builtin_bit_cast(v4i16, (uint2){a.pb0, a.pb1});
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    const v4i16 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16*)(vt + 32 * blk));
+    const int oi = 4 * (TY - 2) + blk;
+    a.O[oi] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pbv, a.O[oi], 0, 0, 0);
+  }
+}
+
 // Median tile `med` (16 tokens) of the wave's range, column tile c, of K or V:
 // global tile index in the compressed 2D matrix (2 column tiles of 64).
 __device__ __forceinline__ int kv_tile(int rowbase, int med, int c) {
@@ -175,16 +243,15 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
   const int g = l & 15;
   const int qh = h * p.group + (g < p.group ? g : 0);
   const uint16_t* qrow = p.q + ((int64_t)b * p.heads + qh) * kHeadDim + 8 * (l >> 4);
-  bf16x8 Q[4];
+  AttnWave A;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) Q[c] = *reinterpret_cast<const bf16x8*>(qrow + 32 * c);
-
-  f32x4 O[8];
+  for (int c = 0; c < 4; ++c) A.Q[c] = *reinterpret_cast<const bf16x8*>(qrow + 32 * c);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x4 S = f32x4{0.f, 0.f, 0.f, 0.f};
-  uint32_t pb0 = 0, pb1 = 0;  // P^T of the current 16 tokens, bf16 pairs
+  for (int i = 0; i < 8; ++i) A.O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  A.m_run = -INFINITY;
+  A.l_run = 0.f;
+  A.S = f32x4{0.f, 0.f, 0.f, 0.f};
+  A.pb0 = A.pb1 = 0;
 
   // tr16 read address of the V tile: token 4*(l/16) + (l%16)/4, dim 4*(l%4)
   // (+16 per 16-dim block) -> lane gets V[4*(l/16)+j][16*blk + l%16], j=0..3.
@@ -223,51 +290,13 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
   // 2 = V0, 3 = V1) for median `med`.
   auto consume = [&](int TY, int med, u32x4 a0, u32x4 a1) {
     if (TY < 2) {
-      if (TY == 0) S = f32x4{0.f, 0.f, 0.f, 0.f};
-      S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0), Q[2 * TY], S, 0, 0, 0);
-      S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1), Q[2 * TY + 1], S, 0, 0, 0);
-      if (TY == 1) {
-        // online softmax over this median's 16 tokens (log2 domain)
-        const int tb = t0 + 16 * med + 4 * (l >> 4);
-        float s[4];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          s[r] = (tb + r < t1) ? S[r] * p.scale_log2 : -INFINITY;
-          mx = fmaxf(mx, s[r]);
-        }
-        mx = wave_max16(mx);
-        const float m_new = fmaxf(m_run, mx);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        float pr[4], ps = 0.f;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          pr[r] = __builtin_amdgcn_exp2f(s[r] - m_use);
-          ps += pr[r];
-        }
-        ps = wave_sum16(ps);
-        l_run = l_run * alpha + ps;
-        if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) O[i] *= alpha;
-        }
-        m_run = m_new;
-        pb0 = pack_bf16x2(pr[0], pr[1]);
-        pb1 = pack_bf16x2(pr[2], pr[3]);
-      }
+      attn_k_step(A, TY, a0, a1);
+      if (TY == 1) attn_softmax(A, t0 + 16 * med + 4 * (l >> 4), t1, p.scale_log2);
     } else {
       // V^T P^T for the 64 dims of this column tile, via the LDS transpose
       *reinterpret_cast<u32x4*>(vbuf + vwr) = a0;
       *reinterpret_cast<u32x4*>(vbuf + vwr + 64) = a1;
-      const v4i16 pbv = __builtin_bit_cast(v4i16, (uint2){pb0, pb1});
-#pragma unroll
-      for (int blk = 0; blk < 4; ++blk) {
-        const v4i16 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) v4i16*)(vbuf + vtr + 32 * blk));
-        const int oi = 4 * (TY - 2) + blk;
-        O[oi] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pbv, O[oi], 0, 0, 0);
-      }
+      attn_v_step(A, TY, vbuf + vtr);
     }
   };
 
@@ -459,9 +488,9 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) cb[(4 * i + r) * 64] = O[i][r];
-    cb[32 * 64] = m_run;
-    cb[33 * 64] = l_run;
+      for (int r = 0; r < 4; ++r) cb[(4 * i + r) * 64] = A.O[i][r];
+    cb[32 * 64] = A.m_run;
+    cb[33 * 64] = A.l_run;
     __syncthreads();
     if (w != 0) return;
     const float* c0 = reinterpret_cast<const float*>(attn_smem) + l;
@@ -471,7 +500,7 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
     const float m_use = m == -INFINITY ? 0.f : m;
     float lsum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 8; ++i) A.O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int v = 0; v < kWpi; ++v) {
       const float lv = c0[(v * 34 + 33) * 64];
@@ -480,39 +509,263 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
 #pragma unroll
       for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) O[i][r] += c0[(v * 34 + 4 * i + r) * 64] * sc;
+        for (int r = 0; r < 4; ++r) A.O[i][r] += c0[(v * 34 + 4 * i + r) * 64] * sc;
     }
-    m_run = m;
-    l_run = lsum;
+    A.m_run = m;
+    A.l_run = lsum;
   }
 
-  // Results: lane l holds head g = l%16, dims 16*i + 4*(l/16) + r of O[i].
+  // Results: lane l holds head g = l%16, dims 16*i + 4*(l/16) + r of A.O[i].
   const int head = h * p.group + g;
   const bool own = g < p.group;
   const int d0 = 4 * (l >> 4);
   if (p.splits == 1) {
     if (own) {
-      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+      const float inv = A.l_run > 0.f ? 1.f / A.l_run : 0.f;
       uint16_t* orow = p.out + ((int64_t)b * p.heads + head) * kHeadDim + d0;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         uint2 v;
-        v.x = pack_bf16x2(O[i][0] * inv, O[i][1] * inv);
-        v.y = pack_bf16x2(O[i][2] * inv, O[i][3] * inv);
+        v.x = pack_bf16x2(A.O[i][0] * inv, A.O[i][1] * inv);
+        v.y = pack_bf16x2(A.O[i][2] * inv, A.O[i][3] * inv);
         *reinterpret_cast<uint2*>(orow + 16 * i) = v;
       }
       if (p.lse && l < 16)
         p.lse[(int64_t)b * p.heads + head] =
-            l_run > 0.f ? (m_run + __log2f(l_run)) * 0.6931471805599453f : -INFINITY;
+            A.l_run > 0.f ? (A.m_run + __log2f(A.l_run)) * 0.6931471805599453f : -INFINITY;
     }
   } else if (own) {
     const int64_t slot = ((int64_t)b * p.heads + head) * p.splits + sp;
     float* wo = p.ws_o + slot * kHeadDim + d0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<f32x4*>(wo + 16 * i) = O[i];
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<f32x4*>(wo + 16 * i) = A.O[i];
     if (l < 16) {
-      p.ws_ml[2 * slot] = m_run;
-      p.ws_ml[2 * slot + 1] = l_run;
+      p.ws_ml[2 * slot] = A.m_run;
+      p.ws_ml[2 * slot + 1] = A.l_run;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fused decode attention over a token-major re-tiled cache with 8 KV heads
+// (rows b * batch_stride + t * 8 + h, bench_zipserv_decode_attention.py:
+// 337-344): a 16-row record band holds tokens 2j, 2j+1 of all 8 heads, so
+// one head's 16 tokens are spread over 8 bands.  A workgroup of 8 waves
+// takes one (batch, split) item and walks it 16 tokens (8 bands) at a time
+// in four phases (K dims 0..63, K dims 64..127, V dims 0..63, V 64..127):
+//   decode: wave w decodes the phase's record of band w -- lane l holds row
+//           l%16 = (token 2w + (l%16)/8, head l%8) -- and writes its two
+//           16-byte halves into the phase's exchange tile in LDS, laid out
+//           per head as 16 tokens x 64 dims (row pitch kVRow);
+//   barrier;
+//   compute: wave h reads head h's tile -- as the K fragment (A operand of
+//           S^T = K q^T) or through ds_read_b64_tr_b16 as V^T -- and runs
+//           the head-major kernel's arithmetic on it (attn_k_step,
+//           attn_softmax, attn_v_step).
+// Every record is decoded once (the reference decodes each token-major tile
+// once per KV head and keeps the rows of that head,
+// flash_fwd_kernel.h:325-430), and head h's operands are the values the
+// dense kernel reads for it, in the same order, so with one wave per (batch,
+// head, split) in both the results are the same bit for bit.  Phases
+// alternate between two exchange tiles, so one barrier per phase orders both
+// the writes before the reads and the reads before the next writes to the
+// same tile.  Records are fetched four phases (one step) ahead into
+// registers, outlier bytes staged one phase ahead, as in attn_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kTmHeads = 8;                      // KV heads of the fused layout
+constexpr int kTmWaves = 8;                      // one wave per band / KV head
+// one head's 16 x 64 tile, padded by 16 bytes: a decoding wave's lanes 0..7
+// write the same row of 8 heads' tiles, which 16 x kVRow bytes apart would
+// all start in one LDS bank (640 dwords, a multiple of the 64 banks)
+constexpr int kTmTile = 16 * kVRow + 16;
+constexpr int kTmPhase = kTmHeads * kTmTile;     // one phase's exchange tile
+constexpr int kTmLds = (int)sizeof(RTables) + kTmWaves * 2 * kExpStage + 2 * kTmPhase;
+
+template <int D>
+__global__ __launch_bounds__(kTmWaves * 64, D == 4 ? 4 : 2) void attn_tm_kernel(AttnParams p) {
+  static_assert(D % 4 == 0, "the ring holds whole steps");
+  __shared__ __attribute__((aligned(16))) uint8_t attn_smem[kTmLds];
+  RTables& RT = *reinterpret_cast<RTables*>(attn_smem);
+  const RExp kex = r_exp(p.k_start), vex = r_exp(p.v_start);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = lane_id();
+  const int item = blockIdx.x;
+  const int sp = item % p.splits;
+  const int b = item / p.splits;
+  int L = p.seqlen_k;
+  if (p.seqlens) L = min(L, __builtin_amdgcn_readfirstlane(p.seqlens[b]));
+  L = max(L, 0);
+  const int t0 = sp * p.chunk;
+  const int t1 = min(t0 + p.chunk, L);
+  const int nmed = t1 > t0 ? (t1 - t0 + 15) >> 4 : 0;  // uniform over the workgroup
+
+  uint8_t* stage0 = attn_smem + sizeof(RTables) + w * 2 * kExpStage;
+  uint8_t* stage1 = stage0 + kExpStage;
+  uint8_t* xch = attn_smem + sizeof(RTables) + kTmWaves * 2 * kExpStage;
+
+  // compute role: KV head h = w, query heads h * group + l%16 (past the group:
+  // head 0's, dropped)
+  const int h = w;
+  const int g = l & 15;
+  const int qh = h * p.group + (g < p.group ? g : 0);
+  const uint16_t* qrow = p.q + ((int64_t)b * p.heads + qh) * kHeadDim + 8 * (l >> 4);
+  AttnWave A;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) A.Q[c] = *reinterpret_cast<const bf16x8*>(qrow + 32 * c);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) A.O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  A.m_run = -INFINITY;
+  A.l_run = 0.f;
+  A.S = f32x4{0.f, 0.f, 0.f, 0.f};
+  A.pb0 = A.pb1 = 0;
+  // head h's tile: K fragment read (token l%16, dims 8*(l/16), +32 dims at
+  // +64 bytes) and V^T transposed read (token 4*(l/16) + (l%16)/4, dim 4*(l%4))
+  const int krd = h * kTmTile + (l & 15) * kVRow + 16 * (l >> 4);
+  const int vtr = h * kTmTile + (4 * (l >> 4) + ((l & 15) >> 2)) * kVRow + 8 * (l & 3);
+  // decode role: row l%16 of band w is (token 2w + (l%16)/8, head l%8)
+  const int xwr = (l & 7) * kTmTile + (2 * w + ((l & 15) >> 3)) * kVRow + 16 * (l >> 4);
+
+  // Band of step `med` for this wave (clamped to the cache: a last step past
+  // the rows of the last batch reads real, finite records whose tokens are
+  // masked), record = band * 2 + column tile.
+  const int nbands_k = p.k_nrec >> 1, nbands_v = p.v_nrec >> 1;
+  const int kb0 = (int)(((int64_t)b * p.k_bsr) >> 4) + (t0 >> 1);
+  const int vb0 = (int)(((int64_t)b * p.v_bsr) >> 4) + (t0 >> 1);
+  auto rrec = [&](int j) {  // record of phase j of this wave's sequence
+    const int ty = j & 3, med = j >> 2;
+    const int band = ty < 2 ? min(kb0 + 8 * med + w, nbands_k - 1)
+                            : min(vb0 + 8 * med + w, nbands_v - 1);
+    return (int64_t)band * 2 + (ty & 1);
+  };
+  const int64_t kr0 = (int64_t)min(kb0 + w, nbands_k - 1) * 2;
+  const int64_t vr0 = (int64_t)min(vb0 + w, nbands_v - 1) * 2;
+  const __amdgpu_buffer_rsrc_t kfr =
+      r_buffer(p.kfix + kr0 * kRecBytes, r_range((p.k_nrec - kr0) * kRecBytes));
+  const __amdgpu_buffer_rsrc_t vfr =
+      r_buffer(p.vfix + vr0 * kRecBytes, r_range((p.v_nrec - vr0) * kRecBytes));
+
+  // Start-up, branch-free: the first chunk's outlier offsets, the decode
+  // table's image and phases 0..D-1's fixed parts go out together, the
+  // outlier bytes once the offsets land; then the table is written.
+  RStage R[D];
+  RMeta MT[D];
+  int oe0 = 0, oe1 = 0;
+  const int nstep = 4 * nmed;
+  {
+    const int lastc = max(min(nstep, 64) - 1, D - 1);
+    const int j = min(l, lastc);
+    const int64_t rec = rrec(j);
+    const int32_t* eo = (j & 3) < 2 ? p.keo : p.veo;
+    oe0 = eo[rec];
+    oe1 = eo[rec + 1];
+  }
+  {
+    RTabRegs<kTmWaves * 64> tab;
+    r_tab_load<kTmWaves * 64>(tab, threadIdx.x);
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+      r_issue_fixed_r((k & 3) < 2 ? kfr : vfr,
+                      (uint32_t)(rrec(k) - ((k & 3) < 2 ? kr0 : vr0)) * kRecBytes, R[k]);
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+      r_issue_exps((k & 3) < 2 ? p.kexp : p.vexp, __builtin_amdgcn_readlane(oe0, k),
+                   __builtin_amdgcn_readlane(oe1, k), R[k], MT[k]);
+    r_tab_store<kTmWaves * 64>(RT, tab, threadIdx.x);
+  }
+  __syncthreads();
+
+  for (int c0 = 0; c0 < nstep; c0 += 64) {
+    const int n = min(nstep - c0, 64);
+    const int lastc = n - 1;
+    if (c0 > 0) {
+      const int j = c0 + min(l, lastc);
+      const int64_t rec = rrec(j);
+      const int32_t* eo = (j & 3) < 2 ? p.keo : p.veo;
+      oe0 = eo[rec];
+      oe1 = eo[rec + 1];
+    }
+#define ZT_ISSUE(J, I, R, MT)                                                              \
+  {                                                                                        \
+    const int jj_ = (J);                                                                   \
+    const int64_t rec_ = rrec(c0 + jj_);                                                   \
+    r_issue_fixed_r((I) < 2 ? kfr : vfr, (uint32_t)(rec_ - ((I) < 2 ? kr0 : vr0)) * kRecBytes, R); \
+    r_issue_exps((I) < 2 ? p.kexp : p.vexp, __builtin_amdgcn_readlane(oe0, jj_),          \
+                 __builtin_amdgcn_readlane(oe1, jj_), R, MT);                              \
+  }
+#define ZT_CLAMP(J, I) ((J) <= lastc ? (J) : ((lastc & ~3) | (I)))
+    // (a chunk of n phases, n a multiple of 4 but maybe not of D: the issue
+    // clamp keeps every fetch in the chunk, and steps past n are skipped)
+#define ZT_STEP(J, I, CUR, NXT, RC, MC, RN, MN)                                            \
+  {                                                                                        \
+    const RStage cs_ = RC;                                                                 \
+    const RMeta cm_ = MC;                                                                  \
+    r_stage(NXT, RN, MN);                                                                  \
+    ZT_ISSUE(ZT_CLAMP((J) + D, I), I, RC, MC);                                             \
+    u32x4 a0_, a1_;                                                                        \
+    if (r_staged(cm_))                                                                     \
+      r_decode(RT, (I) < 2 ? kex : vex, cs_.r, (const uint8_t*)(CUR), cm_.rel, a0_, a1_);  \
+    else                                                                                   \
+      r_decode(RT, (I) < 2 ? kex : vex, cs_.r, ((I) < 2 ? p.kexp : p.vexp) + cm_.e0, 0,    \
+               a0_, a1_);                                                                  \
+    uint8_t* xt_ = xch + ((I) & 1) * kTmPhase;                                             \
+    *reinterpret_cast<u32x4*>(xt_ + xwr) = a0_;                                            \
+    *reinterpret_cast<u32x4*>(xt_ + xwr + 64) = a1_;                                       \
+    __syncthreads();                                                                       \
+    if ((I) < 2) {                                                                         \
+      const u32x4 k0_ = *reinterpret_cast<const u32x4*>(xt_ + krd);                        \
+      const u32x4 k1_ = *reinterpret_cast<const u32x4*>(xt_ + krd + 64);                   \
+      attn_k_step(A, (I), k0_, k1_);                                                       \
+      if ((I) == 1)                                                                        \
+        attn_softmax(A, t0 + 16 * ((c0 + (J)) >> 2) + 4 * (l >> 4), t1, p.scale_log2);    \
+    } else {                                                                               \
+      attn_v_step(A, (I), xt_ + vtr);                                                      \
+    }                                                                                      \
+  }
+    if (c0 > 0) {  // chunk 0's first phases were issued at start-up
+#pragma unroll
+      for (int k = 0; k < D; ++k) ZT_ISSUE(min(k, (lastc & ~3) | (k & 3)), k & 3, R[k], MT[k]);
+    }
+    r_stage(stage0, R[0], MT[0]);
+    for (int j = 0; j < n; j += D) {
+#pragma unroll
+      for (int k = 0; k < D; ++k) {
+        if (k < 4 || j + k < n)
+          ZT_STEP(j + k, k & 3, (k & 1) ? stage1 : stage0, (k & 1) ? stage0 : stage1, R[k],
+                  MT[k], R[(k + 1) % D], MT[(k + 1) % D]);
+      }
+    }
+#undef ZT_STEP
+#undef ZT_CLAMP
+#undef ZT_ISSUE
+  }
+
+  // Results, as attn_kernel: lane l holds head h * group + l%16.
+  const int head = h * p.group + g;
+  const bool own = g < p.group;
+  const int d0 = 4 * (l >> 4);
+  if (p.splits == 1) {
+    if (own) {
+      const float inv = A.l_run > 0.f ? 1.f / A.l_run : 0.f;
+      uint16_t* orow = p.out + ((int64_t)b * p.heads + head) * kHeadDim + d0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint2 v;
+        v.x = pack_bf16x2(A.O[i][0] * inv, A.O[i][1] * inv);
+        v.y = pack_bf16x2(A.O[i][2] * inv, A.O[i][3] * inv);
+        *reinterpret_cast<uint2*>(orow + 16 * i) = v;
+      }
+      if (p.lse && l < 16)
+        p.lse[(int64_t)b * p.heads + head] =
+            A.l_run > 0.f ? (A.m_run + __log2f(A.l_run)) * 0.6931471805599453f : -INFINITY;
+    }
+  } else if (own) {
+    const int64_t slot = ((int64_t)b * p.heads + head) * p.splits + sp;
+    float* wo = p.ws_o + slot * kHeadDim + d0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<f32x4*>(wo + 16 * i) = A.O[i];
+    if (l < 16) {
+      p.ws_ml[2 * slot] = A.m_run;
+      p.ws_ml[2 * slot + 1] = A.l_run;
     }
   }
 }
@@ -681,6 +934,60 @@ static size_t staging_bytes(int layout, int rows, int cols) {
   return ((size_t)rows * cols * 2 + 255) / 256 * 256;
 }
 
+int device_cu_count();  // zs_gemm.hip
+
+// Fused token-major attention (attn_tm_kernel) takes re-tiled caches with
+// kTmHeads KV heads; other token-major caches run staged.
+static bool tm_fused(int heads_k, int cols) { return heads_k == kTmHeads && cols == kHeadDim; }
+
+// Splits of the fused token-major kernel: one 8-wave workgroup per (batch,
+// split), about kTmItems of them (two per CU), at least kTmMinTokens
+// tokens and at most kTmMaxSplits splits per sequence (the combine reads
+// every split's partial of every head); an explicit count is used as given
+// (at most one split per 16 tokens).  The chunk is a multiple of 16 tokens
+// (a step).  Measured over B = 1 / 8 / 32, T = 4k..32k: the best of 16..512
+// splits in every case.
+constexpr int kTmItems = 512;
+constexpr int kTmMinTokens = 32;
+constexpr int kTmMaxSplits = 256;
+
+static int tm_splits(int batch, int seqlen_k, int num_splits) {
+  const int steps = std::max(1, (seqlen_k + 15) / 16);
+  if (num_splits > 0) return std::min(num_splits, steps);
+  const int max_splits = std::max(1, (seqlen_k + kTmMinTokens - 1) / kTmMinTokens);
+  return std::min(std::min(max_splits, kTmMaxSplits),
+                  std::max(1, (kTmItems + batch - 1) / batch));
+}
+
+static int tm_chunk(int seqlen_k, int splits) {
+  const int steps = std::max(1, (seqlen_k + 15) / 16);
+  return ((steps + splits - 1) / splits) * 16;
+}
+
+static int attn_tm_launch(hipStream_t st, AttnParams& p, void* workspace, size_t ws_bytes) {
+  if (p.splits > 1) {
+    if (!workspace || ws_bytes < attn_ws_bytes(p.batch, p.heads, p.splits)) return ZS_E_INVAL;
+    p.ws_o = reinterpret_cast<float*>(workspace);
+    p.ws_ml = p.ws_o + (size_t)p.batch * p.heads * p.splits * kHeadDim;
+  }
+  // Grids of at most one workgroup per CU take the ring of two steps (eight
+  // records per wave in flight; two waves per SIMD leave it the registers),
+  // larger grids the ring of one step at four waves per SIMD.
+  const int items = p.batch * p.splits;
+  if (items <= device_cu_count())
+    hipLaunchKernelGGL(attn_tm_kernel<8>, dim3(items), dim3(kTmWaves * 64), 0, st, p);
+  else
+    hipLaunchKernelGGL(attn_tm_kernel<4>, dim3(items), dim3(kTmWaves * 64), 0, st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  if (p.splits > 1) {
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(p.batch * p.heads), dim3(kCombineThreads), 0, st,
+                       p);
+    e = hipGetLastError();
+  }
+  return e == hipSuccess ? ZS_OK : (int)e;
+}
+
 // Token-major caches run staged: both caches are decompressed into the
 // workspace (dense [B][head_stride][Hkv][D] views of their rows) and the
 // attention kernel runs in its dense mode on them.
@@ -706,11 +1013,21 @@ extern "C" size_t zs_decode_attention_workspace_bytes(int batch, int num_heads, 
                                                       int seqlen_k, int num_splits) {
   if (batch <= 0 || num_heads <= 0 || head_dim != kHeadDim || seqlen_k < 0) return 0;
   // num_splits == 0 asks for the automatic choice, which never exceeds
-  // min(ceil(T/256), ceil(2048/batch)) splits.
-  const int splits = num_splits > 0
-                         ? num_splits
-                         : std::min(std::max(1, (seqlen_k + 255) / 256), (2048 + batch - 1) / batch);
+  // min(ceil(T/256), ceil(2048/batch)) splits, or for fused token-major
+  // caches min(ceil(T/16), ceil(kTmItems/batch)).
+  const int splits =
+      num_splits > 0
+          ? num_splits
+          : std::max(std::min(std::max(1, (seqlen_k + 255) / 256), (2048 + batch - 1) / batch),
+                     std::min(std::max(1, (seqlen_k + 15) / 16), (kTmItems + batch - 1) / batch));
   return attn_ws_bytes(batch, num_heads, splits);
+}
+
+extern "C" int64_t zs_kv_retiled_staging_bytes(int layout, int rows, int cols, int num_heads_k) {
+  if (rows <= 0 || cols <= 0 || num_heads_k <= 0) return -1;
+  if (layout != ZS_LAYOUT_HEAD_MAJOR && layout != ZS_LAYOUT_TOKEN_MAJOR) return -1;
+  if (layout == ZS_LAYOUT_TOKEN_MAJOR && tm_fused(num_heads_k, cols)) return 0;
+  return (int64_t)staging_bytes(layout, rows, cols);
 }
 
 extern "C" int zs_decode_attention(void* stream, const uint16_t* q, const zs_kv_compressed_t* k,
@@ -837,11 +1154,16 @@ extern "C" int zs_decode_attention_retiled(void* stream, const uint16_t* q,
   p.heads = num_heads;
   p.heads_k = num_heads_k;
   p.group = num_heads / num_heads_k;
+  p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  if (k->layout == ZS_LAYOUT_TOKEN_MAJOR && tm_fused(num_heads_k, k->cols)) {
+    p.splits = tm_splits(batch, seqlen_k, num_splits);
+    p.chunk = tm_chunk(seqlen_k, p.splits);
+    return attn_tm_launch((hipStream_t)stream, p, workspace, workspace_bytes);
+  }
   p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k,
                                                                  k->layout != ZS_LAYOUT_TOKEN_MAJOR);
   p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
   p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
-  p.scale_log2 = softmax_scale * 1.4426950408889634f;
   if (k->layout == ZS_LAYOUT_TOKEN_MAJOR) {
     const size_t sk = staging_bytes(k->layout, k->rows, k->cols);
     const size_t sv = staging_bytes(v->layout, v->rows, v->cols);
