@@ -272,6 +272,24 @@ int zs_retiled_mm_fused(void* stream, const uint8_t* d_fixed, const uint8_t* d_e
                         const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B, uint16_t* C,
                         int M, int N, int K, uint16_t* Reduction_Workspace, int Split_K,
                         int32_t* d_counters);
+/* Stream-K schedule of the re-tiled ZipGEMM for N <= 16 (no counterpart in
+ * the reference, whose Split_K cuts every band's K range into equal slices):
+ * one round of workgroups, each over an equal contiguous range of the
+ * M/16 x K/64 records in band-major order, so no CU idles for a band count
+ * that does not divide over the workgroups and no band pays a workgroup
+ * start-up; bands shared between workgroups are added from fp32 partials
+ * (no bf16 rounding of partials) in a fixed order, so results are
+ * deterministic on one device.  `workspace`: workspace_bytes >=
+ * zs_retiled_mm_streamk_workspace_bytes(M, N, K) (for the current device),
+ * 16-byte aligned; `d_counters`: >= M/16 int32, zero before the first call
+ * and left zero by every call (as zs_retiled_mm_fused's).  Returns
+ * ZS_E_UNSUPPORTED for N > 16 and for shapes whose ranges would meet more
+ * than 8 bands (zs_retiled_mm_streamk_workspace_bytes returns 0 for them). */
+int64_t zs_retiled_mm_streamk_workspace_bytes(int M, int N, int K);
+int zs_retiled_mm_streamk(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
+                          const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B, uint16_t* C,
+                          int M, int N, int K, void* workspace, size_t workspace_bytes,
+                          int32_t* d_counters);
 /* zs_retiled_mm_fused that allocates nothing and takes no workspace: no
  * counterpart in the reference; it is for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid

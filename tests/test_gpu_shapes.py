@@ -119,6 +119,8 @@ def _case(torch, key, M, K, nmax, seed, outliers):
 
 def _run_all_splits(torch, c, n, what):
     x = c.x[:n]
+    if n <= 16:  # stream-K schedule (fp32 partials)
+        c.check(torch, zs.zipgemm(c.r, x, split_k=0), n, f"{what} stream-K")
     for sk in SPLITS:
         yf = zs.zipgemm(c.r, x, split_k=sk)                   # in-kernel split-K sum
         c.check(torch, yf, n, f"{what} split_k={sk}")
@@ -197,14 +199,14 @@ def _exact_probes(torch, c, m, N, sk, what):
     """Unit-vector rows of X through ZipGEMM over `m` (re-tiled or canonical
     streams of c.w) in batches of N at split-K sk: every probed output column
     must equal the weight column it selects."""
-    cols = probe_columns(c.K, sk)
+    cols = probe_columns(c.K, max(sk, 1))
     flat = [k for b in probe_batches(cols, N) for k in b]
     P = len(flat)
     idx = torch.tensor(flat, device="cuda")
     X = torch.zeros(P, c.K, dtype=torch.bfloat16, device="cuda")
     X[torch.arange(P, device="cuda"), idx] = 1.0
     Y = torch.full((P, c.M), float("nan"), dtype=torch.bfloat16, device="cuda")
-    ws = zs.codec.splitk_workspace(m, N, sk) if sk > 1 else None
+    ws = zs.codec.splitk_workspace(m, N, sk) if sk != 1 else None
     for j in range(0, P, N):
         zs.zipgemm(m, X[j:j + N], split_k=sk, out=Y[j:j + N], workspace=ws)
     want = c.w[:, idx].t()
@@ -215,6 +217,9 @@ def _exact_probes(torch, c, m, N, sk, what):
 def _probe_all(torch, c, ns, what):
     canon = zs.compress(c.w, window="weights")
     for N in ns:
+        if N <= 16:
+            print(f"{what} N={N} stream-K", flush=True)
+            _exact_probes(torch, c, c.r, N, 0, f"{what} re-tiled N={N} stream-K")
         for sk in SPLITS:
             print(f"{what} N={N} split_k={sk}", flush=True)
             _exact_probes(torch, c, c.r, N, sk, f"{what} re-tiled N={N} split_k={sk}")

@@ -76,6 +76,9 @@ SIGNATURES = {
     "zs_retiled_mm": (C.c_int, [_p, _p, _p, _p, C.c_uint8, _p, _p, C.c_int, C.c_int, C.c_int,
                                 _p, C.c_int]),
     "zs_retiled_mm_counters": (C.c_int64, [C.c_int, C.c_int]),
+    "zs_retiled_mm_streamk_workspace_bytes": (C.c_int64, [C.c_int, C.c_int, C.c_int]),
+    "zs_retiled_mm_streamk": (C.c_int, [_p, _p, _p, _p, C.c_uint8, _p, _p, C.c_int, C.c_int,
+                                        C.c_int, _p, C.c_size_t, _p]),
     "zs_retiled_mm_fused": (C.c_int, [_p, _p, _p, _p, C.c_uint8, _p, _p, C.c_int, C.c_int,
                                       C.c_int, _p, C.c_int, _p]),
     "zs_retiled_mm_fused_noalloc": (C.c_int, [_p, _p, _p, _p, C.c_uint8, _p, _p, C.c_int,

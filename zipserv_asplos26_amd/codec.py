@@ -406,7 +406,16 @@ def decompress(c: ZipservCompressed, out=None):
 
 
 def splitk_workspace(c, n: int, split_k: int):
+    """Workspace of zipgemm(c, x[n], split_k): the bf16 partial slabs of
+    split-K, or with split_k == 0 (stream-K, re-tiled layout) the fp32
+    partials of the bands shared between workgroups; None when none is
+    needed."""
     torch = _torch()
+    if split_k == 0:
+        nbytes = int(lib().zs_retiled_mm_streamk_workspace_bytes(c.rows, n, c.cols))
+        if nbytes <= 0:
+            return None
+        return torch.empty(nbytes, dtype=torch.uint8, device=c.device)
     nbytes = int(lib().zs_splitk_workspace_bytes(c.rows, n, split_k))
     if nbytes == 0:
         return None
@@ -583,7 +592,11 @@ def zipgemm(c, x, split_k: int = 1, out=None, workspace=None, fused: bool = True
     Split-K over the re-tiled layout adds the partial sums inside the GEMM
     kernel (zs_retiled_mm_fused) when `fused`, with `counters` or the current
     stream's buffer from splitk_counters(); same results as the two-kernel
-    reduction, which `fused=False` selects (as do the canonical streams)."""
+    reduction, which `fused=False` selects (as do the canonical streams).
+
+    split_k == 0 (re-tiled layout, N <= 16) selects the stream-K schedule
+    (zs_retiled_mm_streamk: one round of workgroups over equal record
+    ranges, fp32 partials); shapes it does not take run split-K 1."""
     torch = _torch()
     _check_cuda(x, "x", torch.bfloat16)
     if x.dim() != 2 or x.shape[1] != c.cols:
@@ -592,6 +605,24 @@ def zipgemm(c, x, split_k: int = 1, out=None, workspace=None, fused: bool = True
     if out is None:
         out = torch.empty((n, c.rows), dtype=torch.bfloat16, device=x.device)
     retiled = isinstance(c, ZipservRetiled)
+    if split_k == 0:
+        if not retiled:
+            raise ValueError("split_k == 0 (stream-K) takes the re-tiled layout")
+        L = lib()
+        if n <= 16 and int(L.zs_retiled_mm_streamk_workspace_bytes(c.rows, n, c.cols)) > 0:
+            if workspace is None:
+                workspace = splitk_workspace(c, n, 0)
+            if counters is None:
+                counters = splitk_counters(c.rows, n, x.device)
+            if counters is not None and counters.numel() >= c.rows // 16:
+                check("zs_retiled_mm_streamk",
+                      L.zs_retiled_mm_streamk(_stream(), _dptr(c.fixed), _dptr(c.exps),
+                                              _dptr(c.eoff), c.start_exp & 0xFF, _dptr(x),
+                                              _dptr(out), c.rows, n, c.cols, _dptr(workspace),
+                                              workspace.numel() * workspace.element_size(),
+                                              _dptr(counters)))
+                return out
+        split_k = 1
     if split_k > 1 and workspace is None:
         workspace = splitk_workspace(c, n, split_k)
     if retiled:

@@ -302,8 +302,8 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
 
   // Re-tiled start-up (branch-free, so the compiler's wait counts stay
   // exact): the first chunk's outlier offsets and the fixed parts of steps
-  // 0..3 go out with the decode table's image; the outlier bytes follow as
-  // soon as the offsets land, then the table is written and the workgroup
+  // 0..3 go out together; the outlier bytes follow as soon as the offsets
+  // land, the decode table is computed meanwhile, and the workgroup
   // synchronises.  Waves without tokens fetch clamped, in-bounds records.
   RStage R0, R1, R2, R3;
   RMeta M0, M1, M2, M3;
@@ -323,8 +323,6 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
       oe0 = eo[rec];
       oe1 = eo[rec + 1];
     }
-    RTabRegs<kNT> tab;
-    r_tab_load<kNT>(tab, threadIdx.x);
     r_issue_fixed(p.kfix, rrec(0), R0);
     r_issue_fixed(p.kfix, rrec(1), R1);
     r_issue_fixed(p.vfix, rrec(2), R2);
@@ -333,7 +331,7 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
     r_issue_exps(p.kexp, __builtin_amdgcn_readlane(oe0, 1), __builtin_amdgcn_readlane(oe1, 1), R1, M1);
     r_issue_exps(p.vexp, __builtin_amdgcn_readlane(oe0, 2), __builtin_amdgcn_readlane(oe1, 2), R2, M2);
     r_issue_exps(p.vexp, __builtin_amdgcn_readlane(oe0, 3), __builtin_amdgcn_readlane(oe1, 3), R3, M3);
-    r_tab_store<kNT>(RT, tab, threadIdx.x);
+    build_r_tables(RT, threadIdx.x, kNT);
     __syncthreads();
     if (item0 >= nitems) return;  // uniform when kWpi > 1
   }
@@ -644,9 +642,9 @@ __global__ __launch_bounds__(kTmWaves * 64, D == 4 ? 4 : 2) void attn_tm_kernel(
   const __amdgpu_buffer_rsrc_t vfr =
       r_buffer(p.vfix + vr0 * kRecBytes, r_range((p.v_nrec - vr0) * kRecBytes));
 
-  // Start-up, branch-free: the first chunk's outlier offsets, the decode
-  // table's image and phases 0..D-1's fixed parts go out together, the
-  // outlier bytes once the offsets land; then the table is written.
+  // Start-up, branch-free: the first chunk's outlier offsets and phases
+  // 0..D-1's fixed parts go out together, the outlier bytes once the
+  // offsets land; the decode table is computed meanwhile.
   RStage R[D];
   RMeta MT[D];
   int oe0 = 0, oe1 = 0;
@@ -660,8 +658,6 @@ __global__ __launch_bounds__(kTmWaves * 64, D == 4 ? 4 : 2) void attn_tm_kernel(
     oe1 = eo[rec + 1];
   }
   {
-    RTabRegs<kTmWaves * 64> tab;
-    r_tab_load<kTmWaves * 64>(tab, threadIdx.x);
 #pragma unroll
     for (int k = 0; k < D; ++k)
       r_issue_fixed_r((k & 3) < 2 ? kfr : vfr,
@@ -670,7 +666,7 @@ __global__ __launch_bounds__(kTmWaves * 64, D == 4 ? 4 : 2) void attn_tm_kernel(
     for (int k = 0; k < D; ++k)
       r_issue_exps((k & 3) < 2 ? p.kexp : p.vexp, __builtin_amdgcn_readlane(oe0, k),
                    __builtin_amdgcn_readlane(oe1, k), R[k], MT[k]);
-    r_tab_store<kTmWaves * 64>(RT, tab, threadIdx.x);
+    build_r_tables(RT, threadIdx.x, kTmWaves * 64);
   }
   __syncthreads();
 

@@ -44,84 +44,41 @@ struct RTables {
   uint2 tb[4096];
 };
 
-// The table's image, evaluated at compile time (it does not depend on the
-// matrix) and copied into LDS by each workgroup: 16-byte loads that hit L2
-// after the first workgroup, instead of ~200 VALU per thread to compute it.
-struct RTabImage {
-  uint32_t w[2 * 4096];
-  constexpr RTabImage() : w() {
-    for (int q = 0; q < 4096; ++q) {
-      uint32_t codes = 0, sel = 0, rank = 0;
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t c = (uint32_t)(q >> (3 * j)) & 7u;
-        codes |= c << (8 * j);
-        sel |= (c ? 4u + (uint32_t)j : rank) << (8 * j);
-        rank += c ? 0u : 1u;
-      }
-      w[2 * q] = codes;
-      w[2 * q + 1] = sel;
-    }
-  }
-};
-__device__ const RTabImage kRTabImage = RTabImage();
+// Table entries are computed from their index, in registers, by each
+// workgroup at start-up: for q = 12 code bits, the codes as bytes cb, the
+// in-window flags per byte from a carry-free byte add (c + 0x7F sets bit 7
+// exactly when c >= 1), the outlier ranks as a byte prefix sum (one multiply:
+// the flags are 0 / 1 and the sums at most 3), and the selectors merged
+// with one bit-field insert -- 17 VALU per entry.  (A 32 KB image copied
+// from global memory instead costs every workgroup 32 KB of L2 -> CU
+// traffic while its first records are in flight: 1-6% slower ZipGEMM.)
+__device__ __forceinline__ uint2 r_tab_entry(uint32_t q) {
+  const uint32_t cb = (q & 7u) | ((q & 0x38u) << 5) | ((q & 0x1C0u) << 10) | ((q & 0xE00u) << 15);
+  const uint32_t t = (cb + 0x7F7F7F7Fu) & 0x80808080u;   // bit 7: in window
+  const uint32_t rank = ((t ^ 0x80808080u) >> 7) * 0x01010100u;
+  const uint32_t m = t | (t - (t >> 7));                 // 0xFF per in-window byte
+  return make_uint2(cb, (m & 0x07060504u) | (~m & rank));
+}
 
+// The table by `nthreads` threads (tid = this thread's index among them).
 __device__ __forceinline__ void build_r_tables(RTables& T, int tid, int nthreads) {
-  const uint4* src = reinterpret_cast<const uint4*>(kRTabImage.w);
   uint4* dst = reinterpret_cast<uint4*>(T.tb);
-  for (int i = tid; i < 2048; i += nthreads) dst[i] = src[i];
+  for (int i = tid; i < 2048; i += nthreads) {
+    const uint2 a = r_tab_entry(2u * i), b = r_tab_entry(2u * i + 1u);
+    dst[i] = make_uint4(a.x, a.y, b.x, b.y);
+  }
 }
 
 // The same table specialised to one window: entry .x holds the group's four
 // in-window exponent bytes (v_perm of EXP_HI:EXP_LO by the codes) instead of
-// the codes, which saves that v_perm per group in every decode.  Built while
-// copying the image (one v_perm per entry).
+// the codes, which saves that v_perm per group in every decode.
 __device__ __forceinline__ void build_r_tables_exp(RTables& T, int tid, int nthreads,
                                                    uint32_t exp_lo, uint32_t exp_hi) {
-  const uint4* src = reinterpret_cast<const uint4*>(kRTabImage.w);
   uint4* dst = reinterpret_cast<uint4*>(T.tb);
   for (int i = tid; i < 2048; i += nthreads) {
-    uint4 v = src[i];
-    v.x = __builtin_amdgcn_perm(exp_hi, exp_lo, v.x);
-    v.z = __builtin_amdgcn_perm(exp_hi, exp_lo, v.z);
-    dst[i] = v;
-  }
-}
-
-// The same copy in two steps for a workgroup of NT threads: every load of
-// the image first (one 16-byte chunk per NT threads each, all in flight
-// together), then the specialisation and the LDS writes.  A kernel issues
-// its first record loads before r_tab_load so that their latency and the
-// image's overlap.
-// For NT not dividing 2048 the last round's surplus threads re-read the
-// image's last chunk (in bounds, no branch) and store nothing.
-template <int NT>
-struct RTabRegs {
-  static constexpr int kC = (2048 + NT - 1) / NT;
-  uint4 v[kC];
-};
-template <int NT>
-__device__ __forceinline__ void r_tab_load(RTabRegs<NT>& t, int tid) {
-  const uint4* src = reinterpret_cast<const uint4*>(kRTabImage.w);
-#pragma unroll
-  for (int k = 0; k < RTabRegs<NT>::kC; ++k) t.v[k] = src[min(tid + k * NT, 2047)];
-}
-template <int NT>
-__device__ __forceinline__ void r_tab_store(RTables& T, const RTabRegs<NT>& t, int tid) {
-  uint4* dst = reinterpret_cast<uint4*>(T.tb);
-#pragma unroll
-  for (int k = 0; k < RTabRegs<NT>::kC; ++k)
-    if (2048 % NT == 0 || tid + k * NT < 2048) dst[tid + k * NT] = t.v[k];
-}
-template <int NT>
-__device__ __forceinline__ void r_tab_store_exp(RTables& T, const RTabRegs<NT>& t, int tid,
-                                                uint32_t exp_lo, uint32_t exp_hi) {
-  uint4* dst = reinterpret_cast<uint4*>(T.tb);
-#pragma unroll
-  for (int k = 0; k < RTabRegs<NT>::kC; ++k) {
-    uint4 v = t.v[k];
-    v.x = __builtin_amdgcn_perm(exp_hi, exp_lo, v.x);
-    v.z = __builtin_amdgcn_perm(exp_hi, exp_lo, v.z);
-    if (2048 % NT == 0 || tid + k * NT < 2048) dst[tid + k * NT] = v;
+    const uint2 a = r_tab_entry(2u * i), b = r_tab_entry(2u * i + 1u);
+    dst[i] = make_uint4(__builtin_amdgcn_perm(exp_hi, exp_lo, a.x), a.y,
+                        __builtin_amdgcn_perm(exp_hi, exp_lo, b.x), b.y);
   }
 }
 

@@ -642,19 +642,17 @@ __global__ __launch_bounds__(kDecWaves * 64) void rdecompress_kernel(const uint8
 #define RD_EXPS(J, RR, MM)                                                        \
   r_issue_exps(exps, __builtin_amdgcn_readlane(oe0, (J)),                       \
                  __builtin_amdgcn_readlane(oe1, (J)), RR, MM)
-  // Start-up (branch-free): offsets, table image and the first records'
-  // fixed parts together; outlier bytes once the offsets land; then the
-  // table is written.
+  // Start-up (branch-free): offsets and the first records' fixed parts
+  // together; outlier bytes once the offsets land; the decode table is
+  // computed while they are in flight.
   {
     const int last = max(min(cnt, 64) - 1, 0);
-    RTabRegs<kDecWaves * 64> tab;
     RD_OFFSETS(last);
-    r_tab_load<kDecWaves * 64>(tab, threadIdx.x);
 #pragma unroll
     for (int k = 0; k < kDecDepth; ++k) RD_FIXED(min(k, last), R[k]);
 #pragma unroll
     for (int k = 0; k < kDecDepth; ++k) RD_EXPS(min(k, last), R[k], MT[k]);
-    r_tab_store_exp<kDecWaves * 64>(T, tab, threadIdx.x, ex.lo, ex.hi);
+    build_r_tables_exp(T, threadIdx.x, kDecWaves * 64, ex.lo, ex.hi);
   }
   __syncthreads();
 
@@ -1033,17 +1031,14 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
     RZ_ISSUE(min((J) + D, last), RC, MC);                                                  \
     if constexpr (XD > 0) RZ_LOADXS(min((J) + D, last), xr[SC]);                           \
   }
-  // Start-up: chunk 0's outlier offsets, the decode table's image, the first
-  // records' fixed parts and the first X tile go out together; the records'
-  // outlier bytes follow as soon as the offsets are in (loads return in
-  // issue order), and the table is written to LDS after that.
-  // (No branches here: the wait counts the compiler places for the table
-  // writes stay exact.)
+  // Start-up: chunk 0's outlier offsets, the first records' fixed parts and
+  // the first X tile go out together; the records' outlier bytes follow as
+  // soon as the offsets are in (loads return in issue order), and the decode
+  // table is computed into LDS while they are in flight.  (No branches
+  // here: the wait counts the compiler places stay exact.)
   {
     const int last = max(min(cnt, 64) - 1, 0);
-    RTabRegs<WAVES * 64> tab;
     RZ_OFFSETS();
-    r_tab_load<WAVES * 64>(tab, threadIdx.x);
 #pragma unroll
     for (int k = 0; k < D; ++k) {
       RZ_ISSUE_FIXED(min(k, last), R[k]);
@@ -1052,7 +1047,7 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
     if constexpr (XD == 0) RZ_LOADX(0, xn);
 #pragma unroll
     for (int k = 0; k < D; ++k) RZ_ISSUE_EXPS(min(k, last), R[k], MT[k]);
-    r_tab_store_exp<WAVES * 64>(T, tab, threadIdx.x, ex.lo, ex.hi);
+    build_r_tables_exp(T, threadIdx.x, WAVES * 64, ex.lo, ex.hi);
   }
   __syncthreads();
 
@@ -1128,6 +1123,304 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 8 && F == 1) ? 6 : 1) void rg
   }
   if (fx.cnt)
     splitk_finish<16 * F, 16 * NB, WAVES * 64>(fx, Y, M, N, band0 * 16, n0, w == 0);
+}
+
+// ---------------------------------------------------------------------------
+// ZipGEMM over the re-tiled layout, narrow batches (N <= 16), stream-K
+// schedule.  The band-per-workgroup grid of rgemm_kernel leaves CUs idle
+// whenever the band count is not a multiple of the resident workgroups (640
+// bands on 256 CUs x 3 slots: half the CUs hold 3, half 2) and pays a
+// workgroup start-up per band.  Here the grid is exactly kSkPerCu
+// workgroups per CU, one round, and workgroup g takes the contiguous record
+// range [g R / G, (g + 1) R / G) of the R = bands x K/64 records in band-major
+// order; its waves take records r_lo + w, r_lo + w + 8, ... (consecutive
+// waves read consecutive records), crossing band boundaries on the way, so
+// the record ring never drains inside a workgroup.
+//
+// Partial sums, deterministic and barrier-free:
+//  * a wave that moves on to a new band flushes its accumulator for the old
+//    one into an LDS slot of that band segment (16 rows x N columns fp32)
+//    and counts itself with an LDS atomic; the wave that completes the
+//    count (the segment's records are shared by min(8, length) waves) adds
+//    the slots in wave order;
+//  * a segment that is a whole band is written to Y as bf16; a band split
+//    between workgroups (at most the first and the last segment of a range)
+//    has each workgroup's fp32 partial stored device-coherently in the
+//    workspace (slot 2g for its first band, 2g + 1 for its last), counted
+//    with an agent-scope atomic per band, and the last arrival adds the
+//    partials in workgroup order, writes Y and returns the counter to zero
+//    (the protocol of splitk_finish, with fp32 partials).
+// The sums differ from rgemm_kernel's only in fp32 summation order; no
+// partial is rounded to bf16.
+// ---------------------------------------------------------------------------
+constexpr int kSkWaves = 8;
+constexpr int kSkPerCu = 3;       // resident 8-wave workgroups per CU (LDS, 80 VGPRs)
+constexpr int kSkMaxSegments = 8; // segment slots per workgroup (LDS)
+constexpr int64_t kCuLdsBytes = 160 * 1024;  // LDS per CU on gfx950
+
+template <int XD>
+struct RSkSmem {
+  static constexpr int kStages = 2;  // outlier stages per wave (ping-pong)
+  static constexpr int kXPitch = 144;
+  static constexpr int kXRows = 2 * XD;
+  static constexpr int kXStage = XD > 0 ? kXRows * kXPitch : 0;
+  static constexpr int kXAt = kSkWaves * kStages * kExpStage;
+  static constexpr int kTabAt = (kXAt + kSkWaves * kXStage + 15) / 16 * 16;
+  static constexpr int kSlotsAt = kTabAt + (int)sizeof(RTables);
+  // + S segment slots of kSkWaves x 16 rows x N columns fp32, + S counters
+  static constexpr int64_t bytes(int S, int N) {
+    return (int64_t)kSlotsAt + (int64_t)S * kSkWaves * 64 * N + 4 * S;
+  }
+};
+
+// workgroup holding record r of R over G workgroups (range starts g R / G)
+__device__ __forceinline__ int sk_wg_of(int64_t r, int64_t R, int G) {
+  return (int)(((r + 1) * G - 1) / R);
+}
+
+// The kernel's state a segment's completion needs (LDS slots, the
+// workspace, the band counters, the range of this workgroup).
+struct SkCtx {
+  float* slots;
+  float* ws;
+  int32_t* bcnt;
+  uint16_t* Y;
+  int M, N, KT;
+  int64_t R;
+  int G, g;
+  int64_t r_lo, r_hi;
+  int band_lo;
+};
+
+// Completion of segment `s` (band band_lo + s of this workgroup's range) by
+// the wave that counted last into it: adds the waves' slots in wave order,
+// writes Y for a whole band, and otherwise stores the workgroup's fp32
+// partial and, as the band's last arrival, adds the partials of its
+// workgroups in order and writes Y.  Runs after the record loop.
+__device__ __forceinline__ void sk_finish(const SkCtx& c, int s) {
+  const int l = lane_id();
+  const int col = l & 15;
+  const int N = c.N, KT = c.KT;
+  const int band = c.band_lo + s;
+  const int64_t lo = max(c.r_lo, (int64_t)band * KT), hi = min(c.r_hi, (int64_t)(band + 1) * KT);
+  const int64_t len = hi - lo;
+  const float* sl = c.slots + (int64_t)s * kSkWaves * 16 * N;
+  // wave v holds records of the segment when (v - wave of record lo) mod 8 < len
+  const int wb = (int)((lo - c.r_lo) % kSkWaves);
+  f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (col < N) {
+#pragma unroll
+    for (int v = 0; v < kSkWaves; ++v)
+      if ((v - wb + kSkWaves) % kSkWaves < len)
+        sum += *reinterpret_cast<const f32x4*>(sl + (v * N + col) * 16 + 4 * (l >> 4));
+  }
+  const int mrow = band * 16 + 4 * (l >> 4);
+  if (lo == (int64_t)band * KT && hi == (int64_t)(band + 1) * KT) {
+    if (col < N)
+      store4(c.Y + (int64_t)col * c.M + mrow,
+             f32_to_bf16_bits(sum[0]) | (f32_to_bf16_bits(sum[1]) << 16),
+             f32_to_bf16_bits(sum[2]) | (f32_to_bf16_bits(sum[3]) << 16), false);
+    return;
+  }
+  // a band shared with other workgroups
+  float* part = c.ws + (int64_t)(band == c.band_lo ? 2 * c.g : 2 * c.g + 1) * 16 * N;
+  if (col < N) {
+    uint64_t* pp = reinterpret_cast<uint64_t*>(part + col * 16 + 4 * (l >> 4));
+    __hip_atomic_store(pp, (uint64_t)__float_as_uint(sum[0]) | ((uint64_t)__float_as_uint(sum[1]) << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(pp + 1, (uint64_t)__float_as_uint(sum[2]) | ((uint64_t)__float_as_uint(sum[3]) << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  wait_stores();
+  int prev = 0;
+  if (l == 0)
+    prev = __hip_atomic_fetch_add(&c.bcnt[band], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  prev = __builtin_amdgcn_readfirstlane(prev);
+  const int ga = sk_wg_of((int64_t)band * KT, c.R, c.G);
+  const int gb = sk_wg_of((int64_t)(band + 1) * KT - 1, c.R, c.G);
+  if (prev != gb - ga) return;
+  f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int gg = ga; gg <= gb; ++gg) {
+    const int fb = (int)(((int64_t)gg * c.R / c.G) / KT);  // first band of workgroup gg
+    const float* pq = c.ws + (int64_t)(fb == band ? 2 * gg : 2 * gg + 1) * 16 * N;
+    if (col < N) {
+      const uint16_t* q = reinterpret_cast<const uint16_t*>(pq + col * 16 + 4 * (l >> 4));
+      const uint64_t x0 = load_agent(q), x1 = load_agent(q + 4);
+      tot += f32x4{__uint_as_float((uint32_t)x0), __uint_as_float((uint32_t)(x0 >> 32)),
+                   __uint_as_float((uint32_t)x1), __uint_as_float((uint32_t)(x1 >> 32))};
+    }
+  }
+  if (col < N)
+    store4(c.Y + (int64_t)col * c.M + mrow,
+           f32_to_bf16_bits(tot[0]) | (f32_to_bf16_bits(tot[1]) << 16),
+           f32_to_bf16_bits(tot[2]) | (f32_to_bf16_bits(tot[3]) << 16), false);
+  if (l == 0) splitk_reset(&c.bcnt[band]);
+}
+
+template <int D, int XD>
+__global__ __launch_bounds__(kSkWaves * 64, 6) void rgemm_sk_kernel(
+    const uint8_t* fixed, const uint8_t* exps, const int32_t* eoff, int start_exp,
+    const uint16_t* X, uint16_t* Y, int M, int N, int K, int64_t R, int G, int S, float* ws,
+    int32_t* bcnt) {
+  using SM = RSkSmem<XD>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  RTables& T = *reinterpret_cast<RTables*>(smem + SM::kTabAt);
+  float* slots = reinterpret_cast<float*>(smem + SM::kSlotsAt);
+  int32_t* scnt = reinterpret_cast<int32_t*>(smem + SM::kSlotsAt + (int64_t)S * kSkWaves * 64 * N);
+  const RExp ex = r_exp(start_exp);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = lane_id();
+  const int KT = K >> 6;
+  const int g = blockIdx.x;
+  const int64_t r_lo = (int64_t)g * R / G, r_hi = (int64_t)(g + 1) * R / G;
+  const int band_lo = (int)(r_lo / KT);
+  // this wave's steps: records r_lo + w + 8 i, i < nw (a wave without one
+  // runs the start-up on record r_lo and stops there)
+  const int64_t first = r_lo + w < r_hi ? r_lo + w : r_lo;
+  const int nw = r_lo + w < r_hi ? (int)((r_hi - r_lo - w + kSkWaves - 1) / kSkWaves) : 0;
+  const int lastw = max(nw - 1, 0);
+  uint8_t* stg = smem + w * SM::kStages * kExpStage;
+  const __amdgpu_buffer_rsrc_t frs =
+      r_buffer(fixed + r_lo * kRecBytes, r_range((r_hi - r_lo) * kRecBytes));
+  const __amdgpu_buffer_rsrc_t xrs = r_buffer(X, 0x80000000u);
+  // X: staged rows (XD > 0) or B fragments straight from memory (XD == 0),
+  // as rgemm_kernel
+  const int xrow = (XD * l) >> 5, xcol = (4 * XD * l) & 127;
+  const uint32_t xloff = xrow < N ? 2u * (uint32_t)xrow * (uint32_t)K + (uint32_t)xcol : 0x80000000u;
+  uint8_t* xst = smem + SM::kXAt + w * SM::kXStage;
+  uint8_t* xst_w = xst + xrow * SM::kXPitch + xcol;
+  const uint8_t* xst_r =
+      xst + min(l & 15, (XD > 0 ? SM::kXRows : 1) - 1) * SM::kXPitch + 16 * (l >> 4);
+  const uint32_t xoff = (l & 15) < N ? 2u * ((uint32_t)(l & 15) * (uint32_t)K + 8u * (uint32_t)(l >> 4))
+                                     : 0x80000000u;
+
+  // Per chunk of up to 64 steps, lane i holds step c0 + i's record (clamped
+  // to the chunk): its K tile | (band - band_lo) << 24 (a range meets at
+  // most kSkMaxSegments bands, K / 64 < 2^24) and its outlier offsets.
+  int c0 = 0;
+  int lmeta = 0, oe0 = 0, oe1 = 0;
+  auto chunk_meta = [&](int last) {
+    const int64_t rec = first + (int64_t)kSkWaves * (c0 + min(l, last));
+    const int64_t band = rec / KT;
+    lmeta = (int)(rec - band * KT) | ((int)(band - band_lo) << 24);
+    oe0 = eoff[rec];
+    oe1 = eoff[rec + 1];
+  };
+  RStage Rg[D];
+  RMeta MT[D];
+  XFrag<XD> xr[D];
+  bf16x8 xc[2], xn[2];
+#define SK_FIXED(J, R_)                                                                        \
+  r_issue_fixed_r(frs, (uint32_t)(w + kSkWaves * (c0 + (J))) * (uint32_t)kRecBytes, R_)
+#define SK_EXPS(J, R_, MT_)                                                                   \
+  r_issue_exps(exps, __builtin_amdgcn_readlane(oe0, (J)), __builtin_amdgcn_readlane(oe1, (J)), R_, \
+               MT_)
+#define SK_XS(J, DST) \
+  x_load<XD>(xrs, xloff, ((uint32_t)__builtin_amdgcn_readlane(lmeta, (J)) & 0xFFFFFFu) * 128u, DST)
+#define SK_XB(J, DST)                                                                           \
+  {                                                                                             \
+    const uint32_t xs_ = ((uint32_t)__builtin_amdgcn_readlane(lmeta, (J)) & 0xFFFFFFu) * 128u;  \
+    DST[0] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff, xs_, 0)); \
+    DST[1] = __builtin_bit_cast(bf16x8,                                                         \
+                                __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + 64u, xs_, 0)); \
+  }
+  // Start-up (branch-free): chunk 0's metadata, the first D records' fixed
+  // parts and X, then their outlier bytes; the decode table and the segment
+  // counters are written before the barrier.
+  {
+    const int last = min(lastw, 63);
+    chunk_meta(last);
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      SK_FIXED(min(k, last), Rg[k]);
+      if constexpr (XD > 0) SK_XS(min(k, last), xr[k]);
+    }
+    if constexpr (XD == 0) SK_XB(0, xn);
+#pragma unroll
+    for (int k = 0; k < D; ++k) SK_EXPS(min(k, last), Rg[k], MT[k]);
+    build_r_tables_exp(T, threadIdx.x, kSkWaves * 64, ex.lo, ex.hi);
+    if ((int)threadIdx.x < S) scnt[threadIdx.x] = 0;
+  }
+  __syncthreads();
+
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  int acc_band = -1;
+  uint32_t done = 0;  // segments whose count this wave completed (bit s)
+  const int col = l & 15;
+  // A wave moving past band `band`: its sum into the segment's slot, then the
+  // count; the wave that completes it finishes the segment after the loop.
+  auto flush = [&](int band) {
+    const int s_ = band - band_lo;
+    const int64_t lo = max(r_lo, (int64_t)band * KT), hi = min(r_hi, (int64_t)(band + 1) * KT);
+    const int need = (int)min<int64_t>(kSkWaves, hi - lo);
+    float* sl = slots + ((int64_t)s_ * kSkWaves + w) * 16 * N;
+    if (col < N) *reinterpret_cast<f32x4*>(sl + col * 16 + 4 * (l >> 4)) = acc;
+    int prev = 0;
+    if (l == 0)
+      prev = __hip_atomic_fetch_add(&scnt[s_], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (__builtin_amdgcn_readfirstlane(prev) == need - 1) done |= 1u << s_;
+  };
+
+#define SK_STEP(J, SC, SN, RC, MC, RN, MN)                                                     \
+  {                                                                                           \
+    if constexpr (XD == 0) {                                                                  \
+      xc[0] = xn[0];                                                                          \
+      xc[1] = xn[1];                                                                          \
+      SK_XB(min((J) + 1, last), xn);                                                          \
+    }                                                                                         \
+    r_stage_all(stg + (SN) * kExpStage, RN);                                                  \
+    if constexpr (XD > 0) {                                                                   \
+      x_stage<XD>(xst_w, xr[SC]);                                                             \
+      xc[0] = *reinterpret_cast<const bf16x8*>(xst_r);                                        \
+      xc[1] = *reinterpret_cast<const bf16x8*>(xst_r + 64);                                   \
+    }                                                                                         \
+    if ((J) < n) {                                                                            \
+      const int bj_ = band_lo + (__builtin_amdgcn_readlane(lmeta, (J)) >> 24);                \
+      if (bj_ != acc_band) {                                                                  \
+        if (acc_band >= 0) flush(acc_band);                                                   \
+        acc = f32x4{0.f, 0.f, 0.f, 0.f};                                                      \
+        acc_band = bj_;                                                                       \
+      }                                                                                       \
+      u32x4 a0_, a1_;                                                                         \
+      r_decode_staged<true>(T, ex, RC, MC, stg + ((J) & 1) * kExpStage, exps, a0_, a1_);      \
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0_), xc[0], acc, 0, 0, 0);     \
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1_), xc[1], acc, 0, 0, 0);     \
+    }                                                                                         \
+    SK_FIXED(min((J) + D, last), RC);                                                         \
+    SK_EXPS(min((J) + D, last), RC, MC);                                                      \
+    if constexpr (XD > 0) SK_XS(min((J) + D, last), xr[SC]);                                  \
+  }
+  for (; c0 < nw; c0 += 64) {
+    const int n = min(nw - c0, 64);
+    const int last = n - 1;
+    if (c0 > 0) {
+      chunk_meta(last);
+#pragma unroll
+      for (int k = 0; k < D; ++k) {
+        SK_FIXED(min(k, last), Rg[k]);
+        SK_EXPS(min(k, last), Rg[k], MT[k]);
+        if constexpr (XD > 0) SK_XS(min(k, last), xr[k]);
+      }
+      if constexpr (XD == 0) SK_XB(0, xn);
+    }
+    r_stage_all(stg, Rg[0]);
+    for (int j = 0; j < n; j += D) {
+#pragma unroll
+      for (int k = 0; k < D; ++k)
+        SK_STEP(j + k, k, (k + 1) & 1, Rg[k], MT[k], Rg[(k + 1) % D], MT[(k + 1) % D]);
+    }
+  }
+#undef SK_STEP
+#undef SK_XB
+#undef SK_XS
+#undef SK_EXPS
+#undef SK_FIXED
+  if (acc_band >= 0) flush(acc_band);
+  if (done) {
+    const SkCtx cx{slots, ws, bcnt, Y, M, N, KT, R, G, g, r_lo, r_hi, band_lo};
+    for (int s_ = 0; s_ < kSkMaxSegments; ++s_)
+      if (done & (1u << s_)) sk_finish(cx, s_);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1250,11 +1543,10 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
   RMeta MT[RD];
   u32x4 XA[kXC], XB[kXC];
   // Start-up, branch-free (an empty slice runs it on clamped tiles and then
-  // no steps): the first outlier offsets, the decode table's image, the
-  // first records' fixed parts and two X tiles go out together; the outlier
-  // bytes follow as soon as the offsets land, then the table is written.
+  // no steps): the first outlier offsets, the first records' fixed parts and
+  // two X tiles go out together; the outlier bytes follow as soon as the
+  // offsets land; the decode table is computed meanwhile.
   {
-    RTabRegs<BANDS * PH * 64> tab;
     int se0[RD + 1], se1[RD + 1];
 #pragma unroll
     for (int k = 0; k <= RD; ++k) {
@@ -1262,7 +1554,6 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
       se0[k] = eoffs[ti];
       se1[k] = eoffs[ti + 1];
     }
-    r_tab_load<BANDS * PH * 64>(tab, threadIdx.x);
 #pragma unroll
     for (int k = 0; k < RD; ++k) r_issue_fixed_r(frs, (uint32_t)tile_of(k) * kRecBytes, R[k]);
     xload(0, XA);
@@ -1271,7 +1562,7 @@ __global__ __launch_bounds__(BANDS * PH * 64) void rgemm_wide_kernel(const uint8
     for (int k = 0; k < RD; ++k) r_issue_exps(exps, se0[k], se1[k], R[k], MT[k]);
     pe0 = se0[RD];
     pe1 = se1[RD];
-    r_tab_store_exp<BANDS * PH * 64>(T, tab, threadIdx.x, ex.lo, ex.hi);
+    build_r_tables_exp(T, threadIdx.x, BANDS * PH * 64, ex.lo, ex.hi);
   }
   r_stage_all(stage0, R[0]);
   xwrite(xb0, XA);
@@ -1486,6 +1777,59 @@ static hipError_t launch_rgemm(hipStream_t st, const uint8_t* fixed, const uint8
                                           split_k, kb_per_split, fx);
 }
 
+// Stream-K narrow ZipGEMM: grid, segment slots and LDS of one launch.
+struct SkPlan {
+  int G = 0;          // workgroups (0: not applicable, use the band kernels)
+  int S = 0;          // segment slots per workgroup
+  int64_t lds = 0;    // dynamic LDS bytes
+};
+
+template <int XD>
+static SkPlan sk_plan_x(int M, int N, int K) {
+  SkPlan p;
+  const int KT = K / 64;
+  const int64_t R = (int64_t)(M / 16) * KT;
+  if (N < 1 || N > 16 || R <= 0) return p;
+  // the most workgroups per CU (of kSkPerCu) whose LDS fits one CU together,
+  // so that the whole grid is resident in one round
+  for (int per = kSkPerCu; per >= 1; --per) {
+    const int64_t G = std::min<int64_t>((int64_t)device_cu_count() * per, R);
+    // a range of at most L = ceil(R / G) records meets at most
+    // ceil((L - 1) / KT) + 1 bands
+    const int64_t L = (R + G - 1) / G;
+    const int64_t S = (L - 1 + KT - 1) / KT + 1;
+    if (S > kSkMaxSegments) continue;
+    const int64_t lds = RSkSmem<XD>::bytes((int)S, N);
+    if (lds > 65536 || lds * per > kCuLdsBytes) continue;
+    p.G = (int)G;
+    p.S = (int)S;
+    p.lds = lds;
+    return p;
+  }
+  return p;
+}
+
+static SkPlan sk_plan(int M, int N, int K) {
+  if (N <= 2) return sk_plan_x<1>(M, N, K);
+  if (N <= 4) return sk_plan_x<2>(M, N, K);
+  if (N <= 8) return sk_plan_x<4>(M, N, K);
+  return sk_plan_x<0>(M, N, K);
+}
+
+// fp32 partial slots of the stream-K kernel: two per workgroup
+static int64_t sk_workspace_bytes(const SkPlan& p, int N) { return (int64_t)2 * p.G * 16 * N * 4; }
+
+template <int XD>
+static hipError_t launch_sk_x(hipStream_t st, const SkPlan& p, const uint8_t* fixed,
+                              const uint8_t* exps, const int32_t* eoff, int start_exp,
+                              const uint16_t* X, uint16_t* Y, int M, int N, int K, float* ws,
+                              int32_t* cnt) {
+  const int64_t R = (int64_t)(M / 16) * (K / 64);
+  hipLaunchKernelGGL((rgemm_sk_kernel<4, XD>), dim3(p.G), dim3(kSkWaves * 64), (size_t)p.lds, st,
+                     fixed, exps, eoff, start_exp, X, Y, M, N, K, R, p.G, p.S, ws, cnt);
+  return hipGetLastError();
+}
+
 constexpr int kWideDepth = 2;  // records in flight per wave (ring of RD steps)
 
 // ---------------------------------------------------------------------------
@@ -1601,11 +1945,10 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
     RMeta M0[2], M1[2];
     u32x4 XA[kXC], XB[kXC];
     // Start-up, branch-free (an empty slice, kb0 >= KT, runs it on the
-    // clamped last tile and then no steps): offsets, table image, fixed parts
-    // and two X tiles in flight together; outlier bytes as soon as the
-    // offsets land; then the table is written.
+    // clamped last tile and then no steps): offsets, fixed parts and two X
+    // tiles in flight together; outlier bytes as soon as the offsets land;
+    // the decode table is computed meanwhile.
     {
-      RTabRegs<BANDS / 2 * PH * 64> tab;
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
         const int64_t ri = rowrec[f] + tile_of(l);
@@ -1613,7 +1956,6 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
         oe1[f] = eoff[ri + 1];
       }
       ochunk = 0;
-      r_tab_load<BANDS / 2 * PH * 64>(tab, threadIdx.x);
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
         r_issue_fixed_r(frs[f], (uint32_t)tile_of(0) * kRecBytes, R0[f]);
@@ -1628,7 +1970,7 @@ __global__ __launch_bounds__(BANDS / 2 * PH * 64) void rgemm_wide2_kernel(
         r_issue_exps(exps, __builtin_amdgcn_readlane(oe0[f], 1),
                      __builtin_amdgcn_readlane(oe1[f], 1), R1[f], M1[f]);
       }
-      r_tab_store_exp<BANDS / 2 * PH * 64>(T, tab, threadIdx.x, ex.lo, ex.hi);
+      build_r_tables_exp(T, threadIdx.x, BANDS / 2 * PH * 64, ex.lo, ex.hi);
     }
 #pragma unroll
     for (int f = 0; f < 2; ++f) r_stage_all(stage_of(0, f), R0[f]);
@@ -2056,6 +2398,40 @@ extern "C" int zs_retiled_mm_fused(void* stream, const uint8_t* d_fixed, const u
     return ZS_E_INVAL;
   return retiled_mm(stream, d_fixed, d_exps, d_eoff, start_exp, B, C, M, N, K, ws, split_k,
                     counters);
+}
+
+// Stream-K schedule (rgemm_sk_kernel) for N <= 16.
+extern "C" int64_t zs_retiled_mm_streamk_workspace_bytes(int M, int N, int K) {
+  if (!shape_ok(M, K) || N <= 0) return -1;
+  const SkPlan p = sk_plan(M, N, K);
+  return p.G ? sk_workspace_bytes(p, N) : 0;
+}
+
+extern "C" int zs_retiled_mm_streamk(void* stream, const uint8_t* d_fixed, const uint8_t* d_exps,
+                                     const int32_t* d_eoff, uint8_t start_exp, const uint16_t* B,
+                                     uint16_t* C, int M, int N, int K, void* workspace,
+                                     size_t workspace_bytes, int32_t* counters) {
+  const int chk = retiled_mm_args(d_fixed, d_exps, d_eoff, B, C, M, N, K, 1);
+  if (chk != ZS_OK) return chk;
+  if (N > 16) return ZS_E_UNSUPPORTED;
+  if ((int64_t)N * K * 2 > INT32_MAX) return ZS_E_OVERFLOW;
+  const SkPlan p = sk_plan(M, N, K);
+  if (!p.G) return ZS_E_UNSUPPORTED;
+  if (!workspace || (int64_t)workspace_bytes < sk_workspace_bytes(p, N) || !counters ||
+      (reinterpret_cast<uintptr_t>(workspace) & 15) || (reinterpret_cast<uintptr_t>(counters) & 3))
+    return ZS_E_INVAL;
+  hipStream_t st = (hipStream_t)stream;
+  float* ws = static_cast<float*>(workspace);
+  hipError_t e;
+  if (N <= 2)
+    e = launch_sk_x<1>(st, p, d_fixed, d_exps, d_eoff, start_exp, B, C, M, N, K, ws, counters);
+  else if (N <= 4)
+    e = launch_sk_x<2>(st, p, d_fixed, d_exps, d_eoff, start_exp, B, C, M, N, K, ws, counters);
+  else if (N <= 8)
+    e = launch_sk_x<4>(st, p, d_fixed, d_exps, d_eoff, start_exp, B, C, M, N, K, ws, counters);
+  else
+    e = launch_sk_x<0>(st, p, d_fixed, d_exps, d_eoff, start_exp, B, C, M, N, K, ws, counters);
+  return status_of(e);
 }
 
 // ---------------------------------------------------------------------------
