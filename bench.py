@@ -105,11 +105,17 @@ def eager_gemm(spec):
                                 "comp_TBps": round(r.compressed_bytes / t / 1e12, 3)}}))
 
 
+def schedules(N, splits=SPLITS):
+    """Split-K values the step's search tries for batch N: the given
+    split-K slices, and for N <= 16 the stream-K schedule (0)."""
+    return ([0] if N <= 16 else []) + list(splits)
+
+
 def pmc_sweep_order():
     """The (shape, M, K, N, split-K) launch groups of --eager-sweep, in the
     order they are dispatched: every combination the step's split-K search
     can pick, so the counters cover whatever split a bench run chooses."""
-    return [(name, M, K, N, sk) for name, M, K in SHAPES for N in NS for sk in SPLITS]
+    return [(name, M, K, N, sk) for name, M, K in SHAPES for N in NS for sk in schedules(N)]
 
 
 def eager_sweep(iters):
@@ -137,7 +143,7 @@ def eager_sweep(iters):
         nc = max(COLD_MIN_COPIES, -(-COLD_BYTES // r.compressed_bytes))
         copies = [r] + [clone_retiled(r) for _ in range(nc - 1)]
         for (n2, _, _, N, sk) in [o for o in order if o[0] == name]:
-            progress(f"eager sweep {name} N={N} split_k={sk}")
+            progress(f"eager sweep {name} N={N} split_k={sk} (0: stream-K)")
             x = torch.randn(N, K, device=dev, generator=g).to(torch.bfloat16)
             y = torch.empty(N, M, device=dev, dtype=torch.bfloat16)
             ws = zs.codec.splitk_workspace(r, N, sk)
@@ -410,7 +416,7 @@ def bench_c3(torch, zs, stream, gen, dev):
         sk_of, ws_of = {}, {}
         for si, (name, M, K) in enumerate(C3_SHAPES):
             best = None
-            for sk in SPLITS:
+            for sk in schedules(N):
                 ws = zs.codec.splitk_workspace(comp[0][si], N, sk)
                 def srun(si=si, M=M, K=K, sk=sk, ws=ws):
                     for li in range(4):
@@ -632,6 +638,9 @@ def kernel_name(N, M, split_k, K):
     import torch
     nb = (N + 15) // 16
     cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if split_k == 0:  # stream-K schedule (narrow batches)
+        xd = 1 if N <= 2 else (2 if N <= 4 else (4 if N <= 8 else 0))
+        return f"zs::rgemm_sk_kernel<4, {xd}>"
     if nb <= 1 and N >= 4 and (M // 64) * split_k * 8 >= cus * 7:
         ph = 4 if (M // 64) * split_k <= cus else 2
         return f"zs::rgemm_wide_kernel<1, 4, {ph}, 2>"
@@ -908,7 +917,7 @@ def main():
     for si, (name, M, K) in enumerate(SHAPES):
         for N in NS:
             best = None
-            for sk in [int(v) for v in args.splits.split(",")]:
+            for sk in schedules(N, [int(v) for v in args.splits.split(",")]):
                 ws = zs.codec.splitk_workspace(layers[0][si][5], N, sk)
                 def srun(si=si, N=N, M=M, K=K, sk=sk, ws=ws):
                     for cp in colds[si]:
@@ -1044,7 +1053,7 @@ def main():
             "workload": "llama3-8b-projections ZipGEMM sweep (benchmark config 2)",
             "shapes": {n: [m, k] for n, m, k in SHAPES},
             "N": NS,
-            "split_k": "per (shape, N), fastest of 1/2/4 (see per_launch)",
+            "split_k": "per (shape, N), fastest of split-K 1/2/4 and, N <= 16, stream-K (0)",
             "layout": "CDNA4 re-tiled records (zs_retiled_mm_fused)",
             "layers_resident": args.layers,
             "weights": "N(0,0.02) bf16, 0.1% x30 outliers",

@@ -56,7 +56,7 @@ def _stub_result():
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "llama3-8b-projections ZipGEMM sweep (benchmark config 2)",
                    "shapes": {n: [m, k] for n, m, k in bench.SHAPES}, "N": bench.NS,
-                   "split_k": "per (shape, N), fastest of 1/2/4 (see per_launch)",
+                   "split_k": "per (shape, N), fastest of split-K 1/2/4 and, N <= 16, stream-K (0)",
                    "layout": "CDNA4 re-tiled records (zs_retiled_mm_fused)",
                    "layers_resident": 4, "weights": "N(0,0.02) bf16, 0.1% x30 outliers",
                    "parallelism": "single-gpu"},
