@@ -524,3 +524,35 @@ def test_explicit_window_encoder_bytes(torch_cuda, first):
     np.testing.assert_array_equal(r.eoff.cpu().numpy(), o.eoff)
     np.testing.assert_array_equal(r.exps[: r.num_outliers].cpu().numpy(), o.exps)
     np.testing.assert_array_equal(from_torch_bf16(zs.decompress_retiled(r)), W)
+
+
+@pytest.mark.parametrize("window,lookahead", [("kv", 2), ("weights", 0), ("explicit", 9)])
+def test_batched_encoder_equals_one_call_per_matrix(torch_cuda, window, lookahead):
+    # compress_retiled_many (outlier totals read back asynchronously, the
+    # host waiting `lookahead` matrices behind the GPU) against
+    # compress_retiled per matrix and the oracle, byte for byte, over matrices
+    # of different shapes and outlier densities (one with no outliers at all)
+    torch = torch_cuda
+    rng = np.random.default_rng(811)
+    mats = [weights_bf16(rng, (1024, 2048), outlier_frac=0.01),
+            weights_bf16(rng, (64, 64), outlier_frac=0.2),
+            np.zeros((128, 192), np.uint16),
+            rng.integers(0, 65536, size=(256, 512), dtype=np.uint16),
+            weights_bf16(rng, (4096, 448), outlier_frac=0.001)]
+    win = list(range(115, 122)) if window == "explicit" else window
+    xs = [to_torch_bf16(W) for W in mats]
+    many = zs.compress_retiled_many(iter(xs), window=win, lookahead=lookahead)
+    assert zs.compress_retiled_many([], window=win) == []
+    assert len(many) == len(mats)
+    for W, x, r in zip(mats, xs, many):
+        one = zs.compress_retiled(x, window=win)
+        torch.cuda.synchronize()
+        assert (r.rows, r.cols, r.start_exp, r.num_outliers, r.compressed_bytes) == \
+            (one.rows, one.cols, one.start_exp, one.num_outliers, one.compressed_bytes)
+        assert torch.equal(r.fixed, one.fixed)
+        assert torch.equal(r.eoff, one.eoff)
+        assert torch.equal(r.exps, one.exps)
+        o = zo.compress_retiled(W, r.start_exp)
+        np.testing.assert_array_equal(r.fixed.cpu().numpy(), o.fixed)
+        np.testing.assert_array_equal(r.exps[: r.num_outliers].cpu().numpy(), o.exps)
+        np.testing.assert_array_equal(from_torch_bf16(zs.decompress_retiled(r)), W)

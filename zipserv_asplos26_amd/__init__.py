@@ -15,6 +15,7 @@ from .codec import (  # noqa: F401
     compress,
     compress_host,
     compress_retiled,
+    compress_retiled_many,
     compress_zipserv,
     decompress,
     decompress_retiled,
@@ -28,7 +29,7 @@ from .codec import (  # noqa: F401
 
 __all__ = [
     "LIB_PATH", "ZipServError", "build", "lib", "HostCompressed", "ZipservCompressed",
-    "ZipservRetiled", "compress_retiled", "decompress_retiled", "retile",
+    "ZipservRetiled", "compress_retiled", "compress_retiled_many", "decompress_retiled", "retile",
     "analyze_exponents", "compress", "compress_host", "compress_zipserv", "decompress",
     "decompress_zipserv", "decompress_zipserv_into", "make_zipserv_compressed", "to_device",
     "zipgemm", "container",

@@ -490,14 +490,12 @@ def _retiled_alloc(rows, cols, total, dev):
     return fixed, exps, nrec
 
 
-def compress_retiled(input, logical_rows=None, logical_cols=None, layout="by_kv_head",
-                     window="kv") -> ZipservRetiled:
-    """bf16 [rows, cols] on the GPU -> re-tiled layout.  The window is chosen on
-    the GPU, by default with the rule of zipserv_decode_attention_ext.cu:35-135
-    ("kv"); "weights" applies kernel_benchmark/utils.h:189-272 instead (see
-    _device_window).  Under a rule the encoder reads the input once when the
-    window guessed from a sample of it is the rule's (zs_compress_retiled_auto_gpu),
-    twice otherwise; an explicit window is one more input pass."""
+def _retiled_encode(input, window):
+    """First phase of the re-tiled GPU encoder on the current stream: the
+    window, the fixed parts, the per-record outlier counts and offsets, and
+    the outlier bytes in per-record slots; the outlier total and the window
+    land in one int64 [5] tensor (`meta`) that the host reads to size the
+    exponent stream.  Returns the state _retiled_finish takes."""
     torch = _torch()
     _check_cuda(input, "input", torch.bfloat16)
     if input.dim() != 2:
@@ -534,19 +532,77 @@ def compress_retiled(input, logical_rows=None, logical_cols=None, layout="by_kv_
               L.zs_compress_retiled_fixed_gpu(st, _dptr(input), rows, cols, _dptr(top),
                                               _dptr(fixed), _dptr(cnt), _dptr(eoff),
                                               _dptr(total), _dptr(tmp)))
-    host = meta.cpu()  # synchronises (sizes the stream)
-    tot, top0 = int(host[0]), int(host[1:].view(torch.int32)[0])
+    return dict(input=input, rows=rows, cols=cols, nrec=nrec, meta=meta, top=top, eoff=eoff,
+                fixed=fixed, tmp=tmp)
+
+
+def _retiled_finish(s, host_meta, logical_rows, logical_cols, layout) -> ZipservRetiled:
+    """Second phase: the exponent stream sized from the host copy of `meta`
+    and the outlier bytes moved into it."""
+    torch = _torch()
+    tot, top0 = int(host_meta[0]), int(host_meta[1:].view(torch.int32)[0])
     if tot > 2**31 - 1:
         raise OverflowError("outlier count exceeds the int32 offsets")
-    exps = torch.zeros(tot + _lib.ZS_STREAM_SLACK_BYTES, dtype=torch.uint8, device=dev)
+    rows, cols, nrec = s["rows"], s["cols"], s["nrec"]
+    exps = torch.zeros(tot + _lib.ZS_STREAM_SLACK_BYTES, dtype=torch.uint8,
+                       device=s["input"].device)
     check("zs_compress_retiled_exps_gpu",
-          L.zs_compress_retiled_exps_gpu(st, _dptr(input), rows, cols, _dptr(top), _dptr(eoff),
-                                         _dptr(tmp), _dptr(exps)))
-    del tmp  # stream-ordered: the allocator reuses it only after the compaction
-    return ZipservRetiled(fixed, exps, eoff, rows, cols,
+          lib().zs_compress_retiled_exps_gpu(_stream(), _dptr(s["input"]), rows, cols,
+                                             _dptr(s["top"]), _dptr(s["eoff"]), _dptr(s["tmp"]),
+                                             _dptr(exps)))
+    s.pop("tmp")  # stream-ordered: the allocator reuses it only after the compaction
+    return ZipservRetiled(s["fixed"], exps, s["eoff"], rows, cols,
                           rows if logical_rows is None else logical_rows,
                           cols if logical_cols is None else logical_cols,
                           (top0 - 1) & 0xFF, tot, nrec * 1408 + tot + 4 * (nrec + 1), layout)
+
+
+def compress_retiled(input, logical_rows=None, logical_cols=None, layout="by_kv_head",
+                     window="kv") -> ZipservRetiled:
+    """bf16 [rows, cols] on the GPU -> re-tiled layout.  The window is chosen on
+    the GPU, by default with the rule of zipserv_decode_attention_ext.cu:35-135
+    ("kv"); "weights" applies kernel_benchmark/utils.h:189-272 instead (see
+    _device_window).  Under a rule the encoder reads the input once when the
+    window guessed from a sample of it is the rule's (zs_compress_retiled_auto_gpu),
+    twice otherwise; an explicit window is one more input pass.  The host
+    synchronises once, to size the exponent stream (compress_retiled_many
+    overlaps that wait with the next matrices' encoding)."""
+    s = _retiled_encode(input, window)
+    host = s["meta"].cpu()  # synchronises (sizes the stream)
+    return _retiled_finish(s, host, logical_rows, logical_cols, layout)
+
+
+def compress_retiled_many(inputs, window="kv", layout="by_kv_head", lookahead=2) -> list:
+    """compress_retiled over several bf16 matrices without the GPU idling
+    between them: each matrix's outlier total (the one figure the host needs,
+    to size its exponent stream) comes back by an asynchronous copy into pinned
+    memory, and the host waits for it only once the first phases of the next
+    `lookahead` matrices are queued behind it.  Same bytes as one call per
+    matrix (a model's weights are compressed this way, layer by layer).  At
+    most lookahead + 1 matrices hold their outlier slots (256 bytes per 1024
+    elements, an eighth of the bf16 bytes) at once."""
+    torch = _torch()
+    if lookahead < 0:
+        raise ValueError("lookahead must be >= 0")
+    out, pending = [], []
+
+    def finish_oldest():
+        s, host, done = pending.pop(0)
+        done.synchronize()
+        out.append(_retiled_finish(s, host, None, None, layout))
+
+    for x in inputs:
+        s = _retiled_encode(x, window)
+        host = torch.empty(5, dtype=torch.int64, pin_memory=True)
+        host.copy_(s["meta"], non_blocking=True)
+        done = torch.cuda.Event()
+        done.record(torch.cuda.current_stream(x.device))
+        pending.append((s, host, done))
+        if len(pending) > lookahead:
+            finish_oldest()
+    while pending:
+        finish_oldest()
+    return out
 
 
 def retile(c: ZipservCompressed) -> ZipservRetiled:
