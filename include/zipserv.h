@@ -209,7 +209,8 @@ int zs_compress_retiled_emit_gpu(void* stream, const uint16_t* d_input, int M, i
  * (*d_total as above) and parks up to ZS_RETILED_EXP_SLOT_BYTES outlier bytes
  * per record in d_tmp (num_records * ZS_RETILED_EXP_SLOT_BYTES bytes); once d_exps is allocated (*d_total +
  * ZS_STREAM_SLACK_BYTES), zs_compress_retiled_exps_gpu moves them into the
- * exponent stream (records with more outliers re-read their input tile). */
+ * exponent stream (records with more outliers re-read their input tile) and
+ * writes the ZS_STREAM_SLACK_BYTES bytes after it as zeros. */
 int zs_compress_retiled_fixed_gpu(void* stream, const uint16_t* d_input, int M, int K,
                                   const int32_t* d_top_exponents, uint8_t* d_fixed,
                                   int32_t* d_counts, int32_t* d_eoff, int64_t* d_total,

@@ -544,7 +544,8 @@ def _retiled_finish(s, host_meta, logical_rows, logical_cols, layout) -> Zipserv
     if tot > 2**31 - 1:
         raise OverflowError("outlier count exceeds the int32 offsets")
     rows, cols, nrec = s["rows"], s["cols"], s["nrec"]
-    exps = torch.zeros(tot + _lib.ZS_STREAM_SLACK_BYTES, dtype=torch.uint8,
+    # every byte is written by the compaction, the slack bytes as zeros
+    exps = torch.empty(tot + _lib.ZS_STREAM_SLACK_BYTES, dtype=torch.uint8,
                        device=s["input"].device)
     check("zs_compress_retiled_exps_gpu",
           lib().zs_compress_retiled_exps_gpu(_stream(), _dptr(s["input"]), rows, cols,

@@ -92,7 +92,8 @@ __global__ __launch_bounds__(kHistThreads) void hist_kernel(const uint16_t* in, 
 // the one-pass re-tiled encoder.  kSampleGroups workgroups each write their
 // own 256 bins (slice blockIdx.x of `slices`, no atomics, so nothing needs
 // zeroing first) and clear `zero` (the fused encoding pass's kVerifySlices
-// histogram slices, added to with atomics later).
+// histogram slices, added to with atomics later) and *zero32 (when given:
+// the arrival counter of the offset scan).
 constexpr int kSampleStrideMin = 32, kSampleChunks = 128, kSampleGroups = 4;
 
 __device__ __forceinline__ int64_t sample_stride(int64_t nchunks) {
@@ -103,12 +104,14 @@ __device__ __forceinline__ int64_t sample_stride(int64_t nchunks) {
 __global__ __launch_bounds__(kHistThreads) void sample_hist_kernel(const uint16_t* in,
                                                                    int64_t nchunks,
                                                                    uint64_t* slices,
-                                                                   uint64_t* zero) {
+                                                                   uint64_t* zero,
+                                                                   int32_t* zero32) {
   __shared__ uint32_t h[kHistCopies * kHistPitch];
   for (int i = threadIdx.x; i < kHistCopies * kHistPitch; i += kHistThreads) h[i] = 0;
   for (int i = blockIdx.x * kHistThreads + threadIdx.x; i < kVerifySlices * 256;
        i += kSampleGroups * kHistThreads)
     zero[i] = 0;
+  if (zero32 && blockIdx.x == 0 && threadIdx.x == 0) *zero32 = 0;
   __syncthreads();
   uint32_t* hc = h + lane_id() * kHistPitch;
   const uint4* v = reinterpret_cast<const uint4*>(in);
@@ -703,12 +706,12 @@ namespace zs {
 // kSampleChunks of them; a partial last chunk, when numel is not a multiple
 // of 2048, is not sampled; input 16-byte aligned) into `guess`; the per-workgroup
 // sample bins go to `sample` (kSampleGroups x 256), and `zero`
-// (kVerifySlices x 256 entries) is cleared on the way.
+// (kVerifySlices x 256 entries) and *zero32 (when given) are cleared on the way.
 hipError_t launch_window_sample(hipStream_t st, const uint16_t* in, int64_t numel,
                                 bool weights_rule, uint64_t* sample, uint64_t* zero,
-                                int32_t* guess) {
+                                int32_t* guess, int32_t* zero32) {
   hipLaunchKernelGGL(sample_hist_kernel, dim3(kSampleGroups), dim3(kHistThreads), 0, st, in,
-                     numel / 2048, sample, zero);
+                     numel / 2048, sample, zero, zero32);
   if (weights_rule)
     hipLaunchKernelGGL((select_weights_kernel<uint64_t, kSampleGroups>), dim3(1), dim3(256), 0, st,
                        sample, nullptr, guess, nullptr, nullptr);

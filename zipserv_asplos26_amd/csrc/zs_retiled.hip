@@ -110,8 +110,15 @@ __device__ __forceinline__ int block256_exclusive(int v, int& total) {
   return before + incl - v;
 }
 
+// Sum of each kScanTile-record tile into eoff[tile * kScanTile].  With
+// `arrive` (a counter that is zero on entry), the workgroup that arrives last
+// also turns the tile sums into exclusive tile offsets and writes the total
+// (the work of rscan_tiles_kernel, one launch fewer), then returns the
+// counter to zero; the sums travel between workgroups through device-scope
+// stores and loads, as in splitk_finish.
 __global__ __launch_bounds__(256) void rscan_reduce_kernel(const int32_t* counts, int64_t n,
-                                                           int32_t* eoff) {
+                                                           int32_t* eoff, int32_t* arrive,
+                                                           int64_t* total_out) {
   const int64_t base = (int64_t)blockIdx.x * kScanTile;
   int s = 0;
 #pragma unroll
@@ -121,7 +128,36 @@ __global__ __launch_bounds__(256) void rscan_reduce_kernel(const int32_t* counts
   }
   int total;
   block256_exclusive(s, total);
-  if (threadIdx.x == 0) eoff[base] = total;
+  if (!arrive) {
+    if (threadIdx.x == 0) eoff[base] = total;
+    return;
+  }
+  __shared__ int last;
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(&eoff[base], total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // the store is performed before the arrival counts
+    last = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           (int)gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  const int64_t ntiles = gridDim.x;
+  int64_t carry = 0;
+  for (int64_t t0 = 0; t0 < ntiles; t0 += 256) {
+    const int64_t tile = t0 + threadIdx.x;
+    const int v = tile < ntiles ? __hip_atomic_load(&eoff[tile * kScanTile], __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT)
+                                : 0;
+    int chunk;
+    const int ex = block256_exclusive(v, chunk);
+    if (tile < ntiles) eoff[tile * kScanTile] = (int32_t)(carry + ex);
+    carry += chunk;
+  }
+  if (threadIdx.x == 0) {
+    eoff[n] = (int32_t)carry;
+    *total_out = carry;
+    __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 __global__ __launch_bounds__(1024) void rscan_tiles_kernel(int32_t* eoff, int64_t n,
@@ -175,11 +211,16 @@ __global__ __launch_bounds__(256) void rscan_write_kernel(const int32_t* counts,
   }
 }
 
+// Exclusive scan of the per-record outlier counts into eoff (n + 1 entries,
+// eoff[n] = *total).  `arrive`: a zeroed counter that lets the reduce kernel
+// scan the tile sums itself (two launches instead of three).
 static void launch_rscan(hipStream_t st, const int32_t* counts, int64_t n, int32_t* eoff,
-                         int64_t* total) {
+                         int64_t* total, int32_t* arrive = nullptr) {
   const int64_t tiles = (n + kScanTile - 1) / kScanTile;
-  hipLaunchKernelGGL(rscan_reduce_kernel, dim3((unsigned)tiles), dim3(256), 0, st, counts, n, eoff);
-  hipLaunchKernelGGL(rscan_tiles_kernel, dim3(1), dim3(1024), 0, st, eoff, n, total);
+  hipLaunchKernelGGL(rscan_reduce_kernel, dim3((unsigned)tiles), dim3(256), 0, st, counts, n, eoff,
+                     arrive, total);
+  if (!arrive)
+    hipLaunchKernelGGL(rscan_tiles_kernel, dim3(1), dim3(1024), 0, st, eoff, n, total);
   hipLaunchKernelGGL(rscan_write_kernel, dim3((unsigned)tiles), dim3(256), 0, st, counts, n, eoff);
 }
 
@@ -471,6 +512,9 @@ __global__ __launch_bounds__(256) void rcompact_kernel(const uint16_t* a, int M,
   uint8_t* buf = cbuf + (threadIdx.x >> 6) * kCompactBuf;
   const uint32_t st = (uint32_t)(top[0] - 1) & 0xFFu;
   const int64_t nrec = (int64_t)(M >> 4) * (K >> 6);
+  // the stream's slack bytes (read past the end, never selected) as zeros
+  if (blockIdx.x == 0 && threadIdx.x < ZS_STREAM_SLACK_BYTES)
+    exps[(int64_t)eoff[nrec] + threadIdx.x] = 0;
   const uint32_t* tmp32 = reinterpret_cast<const uint32_t*>(tmp);
   const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
@@ -604,7 +648,7 @@ int device_cu_count();  // zs_gemm.hip
 // window of a full histogram with a flag saying whether it differs.
 hipError_t launch_window_sample(hipStream_t st, const uint16_t* in, int64_t numel,
                                 bool weights_rule, uint64_t* sample, uint64_t* zero,
-                                int32_t* guess);
+                                int32_t* guess, int32_t* zero32);
 hipError_t launch_window_verify(hipStream_t st, bool weights_rule, const uint64_t* slices,
                                 uint64_t* hist, int32_t* top, const int32_t* guess,
                                 int32_t* differs);
@@ -2155,8 +2199,8 @@ extern "C" int zs_compress_retiled_fixed_gpu(void* stream, const uint16_t* d_inp
 // sample, the guessed window and the flag that says whether the full
 // histogram's window differs.
 constexpr int kWorkSample = kHistSlices * 256 * 8, kWorkGuess = 2 * kWorkSample,
-              kWorkDiffers = kWorkGuess + 32;
-static_assert(kWorkDiffers + 4 <= ZS_RETILED_AUTO_WORK_BYTES, "auto encoder scratch");
+              kWorkDiffers = kWorkGuess + 32, kWorkArrive = kWorkDiffers + 4;
+static_assert(kWorkArrive + 4 <= ZS_RETILED_AUTO_WORK_BYTES, "auto encoder scratch");
 
 extern "C" int zs_compress_retiled_auto_gpu(void* stream, const uint16_t* d_input, int M, int K,
                                             int rule, uint64_t* d_hist, int32_t* d_top,
@@ -2176,7 +2220,9 @@ extern "C" int zs_compress_retiled_auto_gpu(void* stream, const uint16_t* d_inpu
   uint64_t* sample = reinterpret_cast<uint64_t*>(d_work + kWorkSample);
   int32_t* guess = reinterpret_cast<int32_t*>(d_work + kWorkGuess);
   int32_t* differs = reinterpret_cast<int32_t*>(d_work + kWorkDiffers);
-  hipError_t e = launch_window_sample(st, d_input, (int64_t)M * K, weights, sample, slices, guess);
+  int32_t* arrive = reinterpret_cast<int32_t*>(d_work + kWorkArrive);  // the scan's counter
+  hipError_t e = launch_window_sample(st, d_input, (int64_t)M * K, weights, sample, slices, guess,
+                                      arrive);
   if (e != hipSuccess) return status_of(e);
   const int hist_grid = r_grid(nrec, 4);
   hipLaunchKernelGGL(rfixed_kernel<true>, dim3(hist_grid), dim3(256), 0, st, d_input, M, K, guess,
@@ -2187,7 +2233,7 @@ extern "C" int zs_compress_retiled_auto_gpu(void* stream, const uint16_t* d_inpu
   hipLaunchKernelGGL(rfixed_kernel<false>, dim3(std::min(r_grid(nrec, 4), device_cu_count() * 2)),
                      dim3(256), 0, st, d_input, M, K, d_top, d_fixed, d_counts, d_tmp, nullptr,
                      differs);
-  launch_rscan(st, d_counts, nrec, d_eoff, d_total);
+  launch_rscan(st, d_counts, nrec, d_eoff, d_total, arrive);
   return status_of(hipGetLastError());
 }
 
