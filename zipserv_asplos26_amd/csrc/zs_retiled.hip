@@ -15,6 +15,7 @@
 #include "../../include/zipserv.h"
 #include "zs_device.hpp"
 #include "zs_rdecode.hpp"
+#include "zs_window.hpp"
 
 namespace zs {
 
@@ -420,18 +421,60 @@ constexpr int kExpSlot = ZS_RETILED_EXP_SLOT_BYTES;
 // when it is zero the launch does nothing (the one-pass encoder's first pass
 // already used the right window).
 constexpr int kHistSlices = kVerifySlices;
+
+// The one-pass encoder's window check, at the start of its second launch
+// (!kHist with `slices` set): every workgroup sums the first pass's
+// kHistSlices histogram slices and applies the rule (zs_window.hpp);
+// workgroup 0 writes the histogram (`hist`, 256 x u64), the window (`top`)
+// and whether it differs from `guess` (*differs); when it does not, every
+// workgroup returns, and otherwise they encode again under it.  (One launch
+// fewer than a separate selection kernel before the re-encoding launch.)
+struct WindowCheck {
+  const uint64_t* slices;
+  uint64_t* hist;
+  int32_t* top;
+  const int32_t* guess;
+  int32_t* differs;
+  int weights_rule;
+};
+
 template <bool kHist>
 __global__ __launch_bounds__(256) void rfixed_kernel(const uint16_t* a, int M, int K,
                                                      const int32_t* top, uint8_t* fixed,
                                                      int32_t* counts, uint8_t* tmp,
-                                                     uint64_t* hist, const int32_t* redo) {
-  if (!kHist && redo && *redo == 0) return;
+                                                     uint64_t* hist, const int32_t* redo,
+                                                     WindowCheck wc) {
+  uint32_t st;
+  if constexpr (!kHist) {
+    if (wc.slices) {
+      __shared__ int64_t cnt[256];
+      __shared__ int32_t wtop[8];
+      __shared__ int32_t wdiff;
+      int64_t c = 0;
+#pragma unroll
+      for (int sl = 0; sl < kHistSlices; ++sl) c += (int64_t)wc.slices[256 * sl + threadIdx.x];
+      cnt[threadIdx.x] = c;
+      if (blockIdx.x == 0) wc.hist[threadIdx.x] = (uint64_t)c;
+      __syncthreads();
+      if (threadIdx.x < 64)
+        select_window_wave(wc.weights_rule != 0, cnt, threadIdx.x, wtop, wc.guess, &wdiff);
+      __syncthreads();
+      if (blockIdx.x == 0 && threadIdx.x < 7) wc.top[threadIdx.x] = wtop[threadIdx.x];
+      if (blockIdx.x == 0 && threadIdx.x == 0) *wc.differs = wdiff;
+      if (!wdiff) return;
+      st = (uint32_t)(wtop[0] - 1) & 0xFFu;
+    } else {
+      if (redo && *redo == 0) return;
+      st = (uint32_t)(top[0] - 1) & 0xFFu;
+    }
+  } else {
+    st = (uint32_t)(top[0] - 1) & 0xFFu;
+  }
   __shared__ uint32_t lh[kHist ? 256 : 1];
   if constexpr (kHist) {
     lh[threadIdx.x] = 0;
     __syncthreads();
   }
-  const uint32_t st = (uint32_t)(top[0] - 1) & 0xFFu;
   const int64_t nrec = (int64_t)(M >> 4) * (K >> 6);
   const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
@@ -649,9 +692,7 @@ int device_cu_count();  // zs_gemm.hip
 hipError_t launch_window_sample(hipStream_t st, const uint16_t* in, int64_t numel,
                                 bool weights_rule, uint64_t* sample, uint64_t* zero,
                                 int32_t* guess, int32_t* zero32);
-hipError_t launch_window_verify(hipStream_t st, bool weights_rule, const uint64_t* slices,
-                                uint64_t* hist, int32_t* top, const int32_t* guess,
-                                int32_t* differs);
+
 
 __global__ __launch_bounds__(kDecWaves * 64) void rdecompress_kernel(const uint8_t* fixed,
                                                                      const uint8_t* exps,
@@ -2190,7 +2231,8 @@ extern "C" int zs_compress_retiled_fixed_gpu(void* stream, const uint16_t* d_inp
   if (nrec + 1 > INT32_MAX) return ZS_E_OVERFLOW;
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(rfixed_kernel<false>, dim3(r_grid(nrec, 4)), dim3(256), 0, st, d_input, M,
-                     K, d_top_exponents, d_fixed, d_counts, d_tmp, nullptr, nullptr);
+                     K, d_top_exponents, d_fixed, d_counts, d_tmp, nullptr, nullptr,
+                     WindowCheck{});
   launch_rscan(st, d_counts, nrec, d_eoff, d_total);
   return status_of(hipGetLastError());
 }
@@ -2226,13 +2268,12 @@ extern "C" int zs_compress_retiled_auto_gpu(void* stream, const uint16_t* d_inpu
   if (e != hipSuccess) return status_of(e);
   const int hist_grid = r_grid(nrec, 4);
   hipLaunchKernelGGL(rfixed_kernel<true>, dim3(hist_grid), dim3(256), 0, st, d_input, M, K, guess,
-                     d_fixed, d_counts, d_tmp, slices, nullptr);
-  e = launch_window_verify(st, weights, slices, d_hist, d_top, guess, differs);
-  if (e != hipSuccess) return status_of(e);
-  // Usually a no-op: a small grid keeps the launch cheap.
+                     d_fixed, d_counts, d_tmp, slices, nullptr, WindowCheck{});
+  // The window check, and a second encoding only when the window differs
+  // from the guess (a small grid keeps the usual no-op launch cheap).
   hipLaunchKernelGGL(rfixed_kernel<false>, dim3(std::min(r_grid(nrec, 4), device_cu_count() * 2)),
                      dim3(256), 0, st, d_input, M, K, d_top, d_fixed, d_counts, d_tmp, nullptr,
-                     differs);
+                     nullptr, WindowCheck{slices, d_hist, d_top, guess, differs, weights ? 1 : 0});
   launch_rscan(st, d_counts, nrec, d_eoff, d_total, arrive);
   return status_of(hipGetLastError());
 }
