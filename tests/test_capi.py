@@ -57,3 +57,13 @@ def test_retiled_mm_refuses_k_past_row_blocks():
     K = (1 << 26) + 64
     assert L.zs_retiled_mm(None, fake, fake, fake, 120, fake, fake, 64, 16, K, None, 1) == \
         _lib.ZS_E_OVERFLOW
+
+
+def test_batched_encoder_argument_checks():
+    # compress_retiled_many refuses a negative lookahead before any device
+    # work, and an empty batch is an empty list
+    import pytest
+    import zipserv_asplos26_amd as zs
+    with pytest.raises(ValueError):
+        zs.compress_retiled_many([], lookahead=-1)
+    assert zs.compress_retiled_many([]) == []
