@@ -178,8 +178,13 @@ __device__ __forceinline__ void attn_v_step(AttnWave& a, int TY, const uint8_t* 
 
 // Median tile `med` (16 tokens) of the wave's range, column tile c, of K or V:
 // global tile index in the compressed 2D matrix (2 column tiles of 64).
+// (`rowbase`: a multiple of 16; median `med` of the range is the 16-row
+// band (rowbase >> 4) + med: global tile row band / 4, median band % 4)
 __device__ __forceinline__ int kv_tile(int rowbase, int med, int c) {
-  return ((rowbase >> 6) + (med >> 2)) * 2 + c;
+  return (((rowbase >> 4) + med) >> 2) * 2 + c;
+}
+__device__ __forceinline__ int kv_median(int rowbase, int med) {
+  return ((rowbase >> 4) + med) & 3;
 }
 
 // Combine buffer of kWpi > 1: per wave, 32 O values + m + l per lane.
@@ -226,8 +231,8 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
   int L = p.seqlen_k;
   if (p.seqlens) L = min(L, __builtin_amdgcn_readfirstlane(p.seqlens[b]));
   L = max(L, 0);
-  // token range of this wave (multiples of 64 from the split's start)
-  const int sub = kWpi == 1 ? p.chunk : ((p.chunk / 64 + kWpi - 1) / kWpi) * 64;
+  // token range of this wave (multiples of 16 from the split's start)
+  const int sub = kWpi == 1 ? p.chunk : ((p.chunk / 16 + kWpi - 1) / kWpi) * 16;
   const int t0 = sp * p.chunk + (kWpi == 1 ? 0 : w * sub);
   const int t1 = min(min(t0 + sub, sp * p.chunk + p.chunk), L);
   const int nmed = t1 > t0 ? (t1 - t0 + 15) >> 4 : 0;
@@ -431,8 +436,8 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
           const int j = c0 + min(l, lastc);
           const int ty = j & 3, med = j >> 2;
           const Streams& st = ty < 2 ? p.k : p.v;
-          const int gt = kv_tile(ty < 2 ? k_rowbase : v_rowbase, med, ty & 1);
-          offs = load_tile_offsets(st, gt, med & 3, true);
+          const int rb = ty < 2 ? k_rowbase : v_rowbase;
+          offs = load_tile_offsets(st, kv_tile(rb, med, ty & 1), kv_median(rb, med), true);
         }
         StageRegs R0, R1, R2, R3;
         StageMeta M0, M1, M2, M3;
@@ -443,7 +448,8 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
     const int jj_ = (J);                                                               \
     const int med_ = (c0 + jj_) >> 2;                                                  \
     stage_issue((I) < 2 ? p.k : p.v, (I) < 2 ? bmk : bmv,                              \
-                kv_tile((I) < 2 ? k_rowbase : v_rowbase, med_, (I) & 1), med_ & 3,     \
+                kv_tile((I) < 2 ? k_rowbase : v_rowbase, med_, (I) & 1),               \
+                kv_median((I) < 2 ? k_rowbase : v_rowbase, med_),                      \
                 tile_off_at(offs, jj_), R, MT);                                        \
   }
         // Clamp keeps the step type of the slot (c0 and n are multiples of 4).
@@ -853,18 +859,23 @@ static int attn_auto_splits(int batch, int heads_k, int seqlen_k, bool compresse
   // Smaller grids run four waves per item (attn_launch).  There the
   // compressed modes, whose record -> exponent-stream loads form a longer
   // latency chain, measure best at about 512 items (2048 waves; B=1 T=32k
-  // 43 -> 34 us, B=8 T=4k 43 -> 32 us) and the dense mode at about 256.
+  // 43 -> 34 us, B=8 T=4k 43 -> 32 us) and the dense mode at about 256,
+  // with splits of at least 128 tokens (32 per wave; B=1 T=4k against
+  // 256-token splits: 16.0 -> 12.8 us compressed, 11.7 -> 10.0 us dense).
   const int units = std::max(1, batch * heads_k);
   const int max_splits = std::max(1, (seqlen_k + 255) / 256);
   const int s1 = std::min(max_splits, std::max(1, (2048 + units - 1) / units));
   if ((int64_t)s1 * units >= kSharedItemsBelow) return s1;
+  const int max_shared = std::max(1, (seqlen_k + 127) / 128);
   const int items = compressed ? 512 : 256;
-  return std::min(max_splits, std::max(1, (items + units - 1) / units));
+  return std::min(max_shared, std::max(1, (items + units - 1) / units));
 }
 
+// Tokens per split: a multiple of 16 (one median, one record band), so that
+// every wave's range starts on a band of every layout.
 static int attn_chunk(int seqlen_k, int splits) {
-  const int blocks = (seqlen_k + 63) / 64;
-  return ((blocks + splits - 1) / splits) * 64;
+  const int blocks = (seqlen_k + 15) / 16;
+  return ((blocks + splits - 1) / splits) * 16;
 }
 
 static size_t attn_ws_bytes(int batch, int heads, int splits) {
@@ -1009,12 +1020,12 @@ extern "C" size_t zs_decode_attention_workspace_bytes(int batch, int num_heads, 
                                                       int seqlen_k, int num_splits) {
   if (batch <= 0 || num_heads <= 0 || head_dim != kHeadDim || seqlen_k < 0) return 0;
   // num_splits == 0 asks for the automatic choice, which never exceeds
-  // min(ceil(T/256), ceil(2048/batch)) splits, or for fused token-major
+  // min(ceil(T/128), ceil(2048/batch)) splits, or for fused token-major
   // caches min(ceil(T/16), ceil(kTmItems/batch)).
   const int splits =
       num_splits > 0
           ? num_splits
-          : std::max(std::min(std::max(1, (seqlen_k + 255) / 256), (2048 + batch - 1) / batch),
+          : std::max(std::min(std::max(1, (seqlen_k + 127) / 128), (2048 + batch - 1) / batch),
                      std::min(std::max(1, (seqlen_k + 15) / 16), (kTmItems + batch - 1) / batch));
   return attn_ws_bytes(batch, num_heads, splits);
 }
@@ -1078,7 +1089,7 @@ extern "C" int zs_decode_attention(void* stream, const uint16_t* q, const zs_kv_
   p.group = num_heads / num_heads_k;
   p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k,
                                                                  k->layout != ZS_LAYOUT_TOKEN_MAJOR);
-  p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
+  p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 15) / 16)));
   p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
   if (k->layout == ZS_LAYOUT_TOKEN_MAJOR) {
@@ -1158,7 +1169,7 @@ extern "C" int zs_decode_attention_retiled(void* stream, const uint16_t* q,
   }
   p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k,
                                                                  k->layout != ZS_LAYOUT_TOKEN_MAJOR);
-  p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
+  p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 15) / 16)));
   p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
   if (k->layout == ZS_LAYOUT_TOKEN_MAJOR) {
     const size_t sk = staging_bytes(k->layout, k->rows, k->cols);
@@ -1206,7 +1217,7 @@ extern "C" int zs_decode_attention_dense(void* stream, const uint16_t* q, const 
   p.heads_k = num_heads_k;
   p.group = num_heads / num_heads_k;
   p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k, false);
-  p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
+  p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 15) / 16)));
   p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
   return attn_launch<kModeDense>((hipStream_t)stream, p, workspace, workspace_bytes);
@@ -1242,7 +1253,7 @@ extern "C" int zs_decode_attention_dense_paged(
   p.heads_k = num_heads_k;
   p.group = num_heads / num_heads_k;
   p.splits = num_splits > 0 ? num_splits : attn_auto_splits(batch, num_heads_k, seqlen_k, false);
-  p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 63) / 64)));
+  p.splits = std::max(1, std::min(p.splits, std::max(1, (seqlen_k + 15) / 16)));
   p.chunk = attn_chunk(std::max(seqlen_k, 1), p.splits);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
   return attn_launch<kModePaged>((hipStream_t)stream, p, workspace, workspace_bytes);
