@@ -23,12 +23,42 @@ namespace zs {
 // Encoders.  One wave per record (grid-stride); lane l gathers its 2 x 8
 // elements (one 16-byte load per half) from the bf16 matrix.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ const uint16_t* rec_src(const uint16_t* a, int K, int64_t rec, int h) {
-  const int KT = K >> 6;
-  const int64_t band = rec / KT, kt = rec % KT;
+__device__ __forceinline__ const uint16_t* rec_src_at(const uint16_t* a, int K, int64_t band,
+                                                      int kt, int h) {
   const int l = lane_id();
   return a + (band * 16 + (l & 15)) * (int64_t)K + kt * 64 + 32 * h + 8 * (l >> 4);
 }
+__device__ __forceinline__ const uint16_t* rec_src(const uint16_t* a, int K, int64_t rec, int h) {
+  const int KT = K >> 6;
+  const int64_t band = rec / KT;
+  return rec_src_at(a, K, band, (int)(rec - band * KT), h);
+}
+
+// The records a wave of a grid-stride loop visits -- rec = w, w + nw, ...
+// for wave w of nw -- with their (band, K tile) advanced by addition: one
+// division per wave instead of a 64-bit division per record, all in
+// wave-uniform (scalar) registers.
+struct RecWalk {
+  int64_t rec, band, step_band;
+  int kt, step_kt, KT;
+  __device__ __forceinline__ RecWalk(int K, int64_t nw) {
+    KT = K >> 6;
+    rec = __builtin_amdgcn_readfirstlane((int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6));
+    band = rec / KT;
+    kt = (int)(rec - band * KT);
+    step_band = nw / KT;
+    step_kt = (int)(nw - step_band * KT);
+  }
+  __device__ __forceinline__ void next(int64_t nw) {
+    rec += nw;
+    band += step_band;
+    kt += step_kt;
+    if (kt >= KT) {
+      kt -= KT;
+      ++band;
+    }
+  }
+};
 
 // Plane bytes of 8 elements from their exponents (window start st).
 __device__ __forceinline__ void classify8(u32x4 v, uint32_t st, uint32_t& b1, uint32_t& b2,
@@ -54,18 +84,18 @@ __global__ __launch_bounds__(256) void rcount_kernel(const uint16_t* a, int M, i
                                                      const int32_t* top, int32_t* counts) {
   const uint32_t st = (uint32_t)(top[0] - 1) & 0xFFu;
   const int64_t nrec = (int64_t)(M >> 4) * (K >> 6);
-  const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
-  for (int64_t rec = wid; rec < nrec; rec += nw) {
+  for (RecWalk r(K, nw); r.rec < nrec; r.next(nw)) {
     int n = 0;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       uint32_t b1, b2, b3;
-      classify8(*reinterpret_cast<const u32x4*>(rec_src(a, K, rec, h)), st, b1, b2, b3);
+      classify8(*reinterpret_cast<const u32x4*>(rec_src_at(a, K, r.band, r.kt, h)), st, b1, b2,
+                b3);
       n += 8 - __builtin_popcount(b1 | b2 | b3);
     }
     n = wave_sum(n);
-    if (lane_id() == 0) counts[rec] = n;
+    if (lane_id() == 0) counts[r.rec] = n;
   }
 }
 
@@ -308,17 +338,16 @@ __global__ __launch_bounds__(256) void remit_kernel(const uint16_t* a, int M, in
                                                     uint8_t* fixed, uint8_t* exps) {
   const uint32_t st = (uint32_t)(top[0] - 1) & 0xFFu;
   const int64_t nrec = (int64_t)(M >> 4) * (K >> 6);
-  const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
-  for (int64_t rec = wid; rec < nrec; rec += nw) {
+  for (RecWalk r(K, nw); r.rec < nrec; r.next(nw)) {
     u32x4 v[2];
     uint32_t b[2][3];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      v[h] = *reinterpret_cast<const u32x4*>(rec_src(a, K, rec, h));
+      v[h] = *reinterpret_cast<const u32x4*>(rec_src_at(a, K, r.band, r.kt, h));
       classify8(v[h], st, b[h][0], b[h][1], b[h][2]);
     }
-    emit_record(fixed, exps, rec, eoff[rec], v, b);
+    emit_record(fixed, exps, r.rec, eoff[r.rec], v, b);
   }
 }
 
@@ -476,13 +505,14 @@ __global__ __launch_bounds__(256) void rfixed_kernel(const uint16_t* a, int M, i
     __syncthreads();
   }
   const int64_t nrec = (int64_t)(M >> 4) * (K >> 6);
-  const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
   uint32_t cc[7] = {0, 0, 0, 0, 0, 0, 0};  // this lane's elements with code 1..7
-  for (int64_t rec = wid; rec < nrec; rec += nw) {
+  for (RecWalk r(K, nw); r.rec < nrec; r.next(nw)) {
+    const int64_t rec = r.rec;
     u32x4 v[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) v[h] = *reinterpret_cast<const u32x4*>(rec_src(a, K, rec, h));
+    for (int h = 0; h < 2; ++h)
+      v[h] = *reinterpret_cast<const u32x4*>(rec_src_at(a, K, r.band, r.kt, h));
     const RecCodes rc = rec_codes(v, st);
     if constexpr (kHist) {
       // code bit p of element i of half h at bit 3i + h of P[p]; a code's
