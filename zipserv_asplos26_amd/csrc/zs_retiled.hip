@@ -2474,8 +2474,10 @@ static int retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exp
     // 192 workgroups.  Workgroups of 4 waves (16 per CU, twice the K tiles
     // per wave) instead of 8 for N > 1 on grids of >= 640 bands (measured:
     // 1-5 us faster at N = 8 / 16 on 10240, 14336 and 28672 rows, slower on
-    // smaller grids and mixed at N = 1).
-    const bool w4 = N > 1 && M / 16 >= 640;
+    // smaller grids) and for N = 1 on grids of >= 896 bands (14336 rows:
+    // 21.9 -> 19.6 us; 28672 rows: 0-2% faster; 10240 rows at N = 1 are
+    // 0.6 us slower with 4 waves).
+    const bool w4 = M / 16 >= (N > 1 ? 640 : 896);
     if (N > 8 && M / 16 >= 384)
       e = w4 ? launch_rgemm<2, 1, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx)
              : launch_rgemm<2, 1, 8>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
