@@ -570,11 +570,15 @@ __global__ __launch_bounds__((kWpi == 1 ? kAttnWaves : kWpi) * 64,
 // once per KV head and keeps the rows of that head,
 // flash_fwd_kernel.h:325-430), and head h's operands are the values the
 // dense kernel reads for it, in the same order, so with one wave per (batch,
-// head, split) in both the results are the same bit for bit.  Phases
-// alternate between two exchange tiles, so one barrier per phase orders both
-// the writes before the reads and the reads before the next writes to the
-// same tile.  Records are fetched four phases (one step) ahead into
-// registers, outlier bytes staged one phase ahead, as in attn_kernel.
+// head, split) in both the results are the same bit for bit.  With records
+// one step (four phases) ahead, phases alternate between two exchange tiles,
+// so one barrier per phase orders both the writes before the reads and the
+// reads before the next writes to the same tile.  With records two steps
+// ahead (grids of at most one workgroup per CU, where LDS does not limit
+// occupancy) every phase has its own tile and a wave decodes the K pair,
+// then the V pair, of a step before each barrier: two barriers per step
+// instead of four, and two independent decodes per wave between them.
+// Outlier bytes are staged one phase ahead, as in attn_kernel.
 // ---------------------------------------------------------------------------
 constexpr int kTmHeads = 8;                      // KV heads of the fused layout
 constexpr int kTmWaves = 8;                      // one wave per band / KV head
@@ -583,12 +587,19 @@ constexpr int kTmWaves = 8;                      // one wave per band / KV head
 // all start in one LDS bank (640 dwords, a multiple of the 64 banks)
 constexpr int kTmTile = 16 * kVRow + 16;
 constexpr int kTmPhase = kTmHeads * kTmTile;     // one phase's exchange tile
-constexpr int kTmLds = (int)sizeof(RTables) + kTmWaves * 2 * kExpStage + 2 * kTmPhase;
+// Exchange tiles: two (phases alternate) with the one-step ring; four (one
+// per phase) with the two-step ring, whose workgroups decode a K or V pair
+// before each barrier.
+template <int D>
+constexpr int tm_lds() {
+  return (int)sizeof(RTables) + kTmWaves * 2 * kExpStage + (D == 8 ? 4 : 2) * kTmPhase;
+}
 
 template <int D>
 __global__ __launch_bounds__(kTmWaves * 64, D == 4 ? 4 : 2) void attn_tm_kernel(AttnParams p) {
   static_assert(D % 4 == 0, "the ring holds whole steps");
-  __shared__ __attribute__((aligned(16))) uint8_t attn_smem[kTmLds];
+  constexpr bool kPair = D == 8;
+  __shared__ __attribute__((aligned(16))) uint8_t attn_smem[tm_lds<D>()];
   RTables& RT = *reinterpret_cast<RTables*>(attn_smem);
   const RExp kex = r_exp(p.k_start), vex = r_exp(p.v_start);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -697,6 +708,30 @@ __global__ __launch_bounds__(kTmWaves * 64, D == 4 ? 4 : 2) void attn_tm_kernel(
 #define ZT_CLAMP(J, I) ((J) <= lastc ? (J) : ((lastc & ~3) | (I)))
     // (a chunk of n phases, n a multiple of 4 but maybe not of D: the issue
     // clamp keeps every fetch in the chunk, and steps past n are skipped)
+#define ZT_DEC(J, I, CUR, NXT, RC, MC, RN, MN)                                             \
+  {                                                                                        \
+    const RStage cs_ = RC;                                                                 \
+    const RMeta cm_ = MC;                                                                  \
+    r_stage(NXT, RN, MN);                                                                  \
+    ZT_ISSUE(ZT_CLAMP((J) + D, I), I, RC, MC);                                             \
+    u32x4 a0_, a1_;                                                                        \
+    if (r_staged(cm_))                                                                     \
+      r_decode(RT, (I) < 2 ? kex : vex, cs_.r, (const uint8_t*)(CUR), cm_.rel, a0_, a1_);  \
+    else                                                                                   \
+      r_decode(RT, (I) < 2 ? kex : vex, cs_.r, ((I) < 2 ? p.kexp : p.vexp) + cm_.e0, 0,    \
+               a0_, a1_);                                                                  \
+    uint8_t* xt_ = xch + (I) * kTmPhase;                                                   \
+    *reinterpret_cast<u32x4*>(xt_ + xwr) = a0_;                                            \
+    *reinterpret_cast<u32x4*>(xt_ + xwr + 64) = a1_;                                       \
+  }
+#define ZT_KC(J, I)                                                                        \
+  {                                                                                        \
+    const uint8_t* xt_ = xch + (I) * kTmPhase;                                             \
+    const u32x4 k0_ = *reinterpret_cast<const u32x4*>(xt_ + krd);                          \
+    const u32x4 k1_ = *reinterpret_cast<const u32x4*>(xt_ + krd + 64);                     \
+    attn_k_step(A, (I), k0_, k1_);                                                         \
+    if ((I) == 1) attn_softmax(A, t0 + 16 * ((c0 + (J)) >> 2) + 4 * (l >> 4), t1, p.scale_log2); \
+  }
 #define ZT_STEP(J, I, CUR, NXT, RC, MC, RN, MN)                                            \
   {                                                                                        \
     const RStage cs_ = RC;                                                                 \
@@ -729,13 +764,37 @@ __global__ __launch_bounds__(kTmWaves * 64, D == 4 ? 4 : 2) void attn_tm_kernel(
     }
     r_stage(stage0, R[0], MT[0]);
     for (int j = 0; j < n; j += D) {
+      if constexpr (kPair) {
+        // per step: K pair decoded, barrier, QK^T and softmax; V pair
+        // decoded, barrier, PV.  A wave writes a tile again only after the
+        // next barrier that every wave reaches after its reads of it.
 #pragma unroll
-      for (int k = 0; k < D; ++k) {
-        if (k < 4 || j + k < n)
-          ZT_STEP(j + k, k & 3, (k & 1) ? stage1 : stage0, (k & 1) ? stage0 : stage1, R[k],
-                  MT[k], R[(k + 1) % D], MT[(k + 1) % D]);
+        for (int k = 0; k < D; k += 4) {
+          if (k == 0 || j + k < n) {
+            ZT_DEC(j + k, 0, stage0, stage1, R[k], MT[k], R[k + 1], MT[k + 1]);
+            ZT_DEC(j + k + 1, 1, stage1, stage0, R[k + 1], MT[k + 1], R[k + 2], MT[k + 2]);
+            __syncthreads();
+            ZT_KC(j + k, 0);
+            ZT_KC(j + k + 1, 1);
+            ZT_DEC(j + k + 2, 2, stage0, stage1, R[k + 2], MT[k + 2], R[k + 3], MT[k + 3]);
+            ZT_DEC(j + k + 3, 3, stage1, stage0, R[k + 3], MT[k + 3], R[(k + 4) % D],
+                   MT[(k + 4) % D]);
+            __syncthreads();
+            attn_v_step(A, 2, xch + 2 * kTmPhase + vtr);
+            attn_v_step(A, 3, xch + 3 * kTmPhase + vtr);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+          if (k < 4 || j + k < n)
+            ZT_STEP(j + k, k & 3, (k & 1) ? stage1 : stage0, (k & 1) ? stage0 : stage1, R[k],
+                    MT[k], R[(k + 1) % D], MT[(k + 1) % D]);
+        }
       }
     }
+#undef ZT_KC
+#undef ZT_DEC
 #undef ZT_STEP
 #undef ZT_CLAMP
 #undef ZT_ISSUE
@@ -772,15 +831,18 @@ __global__ __launch_bounds__(kTmWaves * 64, D == 4 ? 4 : 2) void attn_tm_kernel(
   }
 }
 
-// Merges the split partials of one (batch, head) with four waves: the split
+// Merges the split partials of one (batch, head) with W waves: the split
 // weights exp2(m_s - m) are computed once per chunk of splits into LDS, then
-// wave w takes splits 8w..8w+7 of every 32 (lane l owns dims 2l, 2l+1), so
-// each wave has eight independent partial-output loads in flight and the
-// four wave sums meet in LDS.
+// wave w takes splits 8w..8w+7 of every 8W (lane l owns dims 2l, 2l+1), so
+// each wave has eight independent partial-output loads in flight and the W
+// wave sums meet in LDS.  A wave's first eight partial loads go out before
+// the split maximum is known (they do not depend on it), so they overlap
+// its reduction.  W = 16 for more than 32 splits (two rounds of loads per
+// wave at 256 splits instead of eight with four waves), else 4.
 constexpr int kCombineChunk = 512;
-constexpr int kCombineThreads = 256;
 
-__device__ __forceinline__ float block256_reduce(float x, bool is_max, float* red) {
+template <int W>
+__device__ __forceinline__ float block_reduce(float x, bool is_max, float* red) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     const float y = __shfl_xor(x, off);
@@ -788,30 +850,41 @@ __device__ __forceinline__ float block256_reduce(float x, bool is_max, float* re
   }
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
   __syncthreads();
-  const float r = is_max ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]))
-                         : (red[0] + red[1]) + (red[2] + red[3]);
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < W; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
   __syncthreads();
   return r;
 }
 
-__global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnParams p) {
+template <int W>
+__global__ __launch_bounds__(W * 64) void attn_combine_kernel(AttnParams p) {
+  constexpr int NT = W * 64;
   __shared__ float sc[kCombineChunk];
-  __shared__ float red[4];
-  __shared__ float2 part[3][64];
+  __shared__ float red[W];
+  __shared__ float2 part[W - 1][64];
   const int bh = blockIdx.x;
   const int t = threadIdx.x, w = t >> 6, l = t & 63;
   const int S = p.splits;
   const float* ml = p.ws_ml + (int64_t)bh * S * 2;
+  const float* wo = p.ws_o + (int64_t)bh * S * kHeadDim + 2 * l;
+  float2 x[8];
+  {
+    const int n = min(S, kCombineChunk);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      x[j] = 8 * w + j < n ? *reinterpret_cast<const float2*>(wo + (int64_t)(8 * w + j) * kHeadDim)
+                           : float2{0.f, 0.f};
+  }
   float m = -INFINITY;
-  for (int s = t; s < S; s += kCombineThreads) m = fmaxf(m, ml[2 * s]);
-  m = block256_reduce(m, true, red);
+  for (int s = t; s < S; s += NT) m = fmaxf(m, ml[2 * s]);
+  m = block_reduce<W>(m, true, red);
   const float m_use = m == -INFINITY ? 0.f : m;
   float lpart = 0.f;
   float2 acc = {0.f, 0.f};
-  const float* wo = p.ws_o + (int64_t)bh * S * kHeadDim + 2 * l;
   for (int c0 = 0; c0 < S; c0 += kCombineChunk) {
     const int n = min(S - c0, kCombineChunk);
-    for (int i = t; i < n; i += kCombineThreads) {
+    for (int i = t; i < n; i += NT) {
       const float2 e = *reinterpret_cast<const float2*>(ml + 2 * (c0 + i));
       const float wgt = e.y > 0.f ? __builtin_amdgcn_exp2f(e.x - m_use) : 0.f;
       sc[i] = wgt;
@@ -819,12 +892,13 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnParam
     }
     __syncthreads();
     const float* wc = wo + (int64_t)c0 * kHeadDim;
-    for (int i0 = 8 * w; i0 < n; i0 += 32) {
-      float2 x[8];
+    for (int i0 = 8 * w; i0 < n; i0 += 8 * W) {
+      if (c0 > 0 || i0 > 8 * w) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        x[j] = i0 + j < n ? *reinterpret_cast<const float2*>(wc + (int64_t)(i0 + j) * kHeadDim)
-                          : float2{0.f, 0.f};
+        for (int j = 0; j < 8; ++j)
+          x[j] = i0 + j < n ? *reinterpret_cast<const float2*>(wc + (int64_t)(i0 + j) * kHeadDim)
+                            : float2{0.f, 0.f};
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float g = i0 + j < n ? sc[i0 + j] : 0.f;
@@ -834,12 +908,12 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnParam
     }
     __syncthreads();
   }
-  const float lsum = block256_reduce(lpart, false, red);
+  const float lsum = block_reduce<W>(lpart, false, red);
   if (w > 0) part[w - 1][l] = acc;
   __syncthreads();
   if (w == 0) {
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
+    for (int i = 0; i < W - 1; ++i) {
       acc.x += part[i][l].x;
       acc.y += part[i][l].y;
     }
@@ -849,6 +923,14 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnParam
     if (p.lse && l == 0)
       p.lse[bh] = lsum > 0.f ? (m + __log2f(lsum)) * 0.6931471805599453f : -INFINITY;
   }
+}
+
+static hipError_t launch_combine(hipStream_t st, const AttnParams& p) {
+  if (p.splits > 32)
+    hipLaunchKernelGGL(attn_combine_kernel<16>, dim3(p.batch * p.heads), dim3(16 * 64), 0, st, p);
+  else
+    hipLaunchKernelGGL(attn_combine_kernel<4>, dim3(p.batch * p.heads), dim3(4 * 64), 0, st, p);
+  return hipGetLastError();
 }
 
 // Workgroups of four waves per item take grids of fewer than this many items.
@@ -904,9 +986,7 @@ static int attn_launch(hipStream_t st, AttnParams& p, void* workspace, size_t ws
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   if (p.splits > 1) {
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(p.batch * p.heads), dim3(kCombineThreads), 0, st,
-                       p);
-    e = hipGetLastError();
+    e = launch_combine(st, p);
   }
   return e == hipSuccess ? ZS_OK : (int)e;
 }
@@ -978,8 +1058,9 @@ static int attn_tm_launch(hipStream_t st, AttnParams& p, void* workspace, size_t
     p.ws_ml = p.ws_o + (size_t)p.batch * p.heads * p.splits * kHeadDim;
   }
   // Grids of at most one workgroup per CU take the ring of two steps (eight
-  // records per wave in flight; two waves per SIMD leave it the registers),
-  // larger grids the ring of one step at four waves per SIMD.
+  // records per wave in flight; two waves per SIMD leave it the registers)
+  // and decode phase pairs between barriers, larger grids the ring of one
+  // step at four waves per SIMD.
   const int items = p.batch * p.splits;
   if (items <= device_cu_count())
     hipLaunchKernelGGL(attn_tm_kernel<8>, dim3(items), dim3(kTmWaves * 64), 0, st, p);
@@ -988,9 +1069,7 @@ static int attn_tm_launch(hipStream_t st, AttnParams& p, void* workspace, size_t
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   if (p.splits > 1) {
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(p.batch * p.heads), dim3(kCombineThreads), 0, st,
-                       p);
-    e = hipGetLastError();
+    e = launch_combine(st, p);
   }
   return e == hipSuccess ? ZS_OK : (int)e;
 }
