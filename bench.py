@@ -638,8 +638,9 @@ def bench_kv(torch, zs, dev, gen):
 def kernel_name(N, M, split_k, K):
     """Kernel that zs_retiled_mm launches for batch N (mirrors its dispatch):
     N <= 16 -> rgemm_kernel<F, 1, W, D, XD> (F bands per wave: 2 when N > 8
-    and M/16 >= 384, else 1; one 16-column block; W = 4 waves when N > 1 and
-    M/16 >= 640, else 8; records D = 4 tiles ahead with one band per wave, 3
+    and M/16 >= 384, else 1; one 16-column block; W = 4 waves when M/16 >= 640
+    (N > 1) or M/16 >= 896 (N = 1), else 8; records D = 4 tiles ahead with one
+    band per wave, 3
     with two; X staged through LDS in XD-row loads: 1 for N <= 2, 2 for
     N <= 4, 4 for N <= 8, none (0) above); N > 16 ->
     rgemm_wide_kernel<NB, 4, PH, 2> with NB = 2, 4 or 8
@@ -659,7 +660,7 @@ def kernel_name(N, M, split_k, K):
         ph = 4 if (M // 64) * split_k <= cus else 2
         return f"zs::rgemm_wide_kernel<1, 4, {ph}, 2>"
     if nb <= 1:
-        waves = 4 if (N > 1 and M // 16 >= 640) else 8
+        waves = 4 if M // 16 >= (640 if N > 1 else 896) else 8
         f = 2 if (N > 8 and M // 16 >= 384) else 1
         xd = 1 if N <= 2 else (2 if N <= 4 else (4 if N <= 8 else 0))
         return f"zs::rgemm_kernel<{f}, 1, {waves}, {4 if f == 1 else 3}, {xd}>"
