@@ -91,6 +91,17 @@ def test_attention_retiled_matches_oracle(torch_cuda, B, T, Hkv, H, splits):
     _check(_run(torch_cuda, B, T, Hkv, H, splits=splits, retiled=True))
 
 
+@pytest.mark.parametrize("retiled,layout", [(False, "by_kv_head"), (True, "by_kv_head"),
+                                            (True, "token_major")])
+def test_attention_split_merge_past_one_chunk(torch_cuda, retiled, layout):
+    # 600 splits of 32 tokens (the last 88 empty): the merge runs 16 waves
+    # per (batch, head) and walks two chunks of at most 512 splits, its first
+    # loads issued before the split maximum
+    fused_tm = retiled and layout == "token_major"
+    _check(_run(torch_cuda, 1, 16384, 8, 64, splits=600, seed=5, retiled=retiled, layout=layout),
+           exact=not fused_tm)
+
+
 @pytest.mark.parametrize("splits", [1, 0])
 def test_attention_retiled_ragged(torch_cuda, splits):
     seqlens = [300, 17, 0, 64]
