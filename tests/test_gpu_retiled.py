@@ -1,8 +1,9 @@
 """GPU parity of the CDNA4 re-tiled layout: encoders byte-identical to the
 oracle, decompress bit-exact, and ZipGEMM over the re-tiled layout identical
 (bit for bit, N <= 16 in 8-wave 16-row workgroups) or equal up to fp32
-summation order (N > 16, the 4-wave workgroups of N > 1 on >= 640 bands,
-and the 64-row workgroups of 4 <= N <= 16 on >= 224 of them) to ZipGEMM
+summation order (N > 16, the 4-wave workgroups of N > 1 on >= 640 bands and
+of N = 1 on >= 896, and the 64-row workgroups of 4 <= N <= 16 on >= 224 of
+them) to ZipGEMM
 over the canonical streams it was built from, and within 1e-2 relative
 error of the fp32-accumulated product."""
 import numpy as np
