@@ -6,8 +6,8 @@ import pytest
 
 import oracle as zo
 import zipserv_asplos26_amd as zs
-from zs_testutil import (from_torch_bf16, kv_bf16, normal_bf16, pad_by_kv_head, to_torch_bf16,
-                         upload, weights_bf16)
+from zs_testutil import (arbitrary_bf16, from_torch_bf16, kv_bf16, normal_bf16, pad_by_kv_head,
+                         to_torch_bf16, upload, weights_bf16)
 
 pytestmark = pytest.mark.gpu
 
@@ -66,6 +66,29 @@ def test_gpu_encoder_matches_oracle(torch_cuda, shape, frac, seed):
     np.testing.assert_array_equal(med.cpu().numpy(), e.tile_offsets_median)
     np.testing.assert_array_equal(tog.cpu().numpy(), e.tile_offsets_global)
     # and the device streams decode back to W
+    c = zs.make_zipserv_compressed(parts)
+    np.testing.assert_array_equal(from_torch_bf16(zs.decompress(c)), W)
+
+
+@pytest.mark.parametrize("kind", ["random_bits", "specials"])
+def test_gpu_encoder_arbitrary_bits(torch_cuda, kind):
+    # NaN payloads, infinities, subnormals and signed zeros are outliers or
+    # in-window values like any other bits: the GPU encoder's streams equal
+    # the oracle's byte for byte and decode back to the same bits
+    rng = np.random.default_rng(41)
+    W = arbitrary_bf16(rng, (192, 512), kind)
+    parts = zs.compress_zipserv(to_torch_bf16(W))
+    sm, fu, b1, b2, b3, med, tog, meta = parts
+    m = meta.tolist()
+    e = zo.compress(W, top=zo.analyze_gpu(W))
+    assert m[6] == e.start_exp and m[7] == e.sign_mantissa.size and m[8] == e.compressed_full.size
+    np.testing.assert_array_equal(sm.cpu().numpy()[: m[7]], e.sign_mantissa)
+    np.testing.assert_array_equal(from_torch_bf16(fu)[: m[8]], e.compressed_full)
+    np.testing.assert_array_equal(b1.cpu().numpy().view(np.uint64), e.bitmap1)
+    np.testing.assert_array_equal(b2.cpu().numpy().view(np.uint64), e.bitmap2)
+    np.testing.assert_array_equal(b3.cpu().numpy().view(np.uint64), e.bitmap3)
+    np.testing.assert_array_equal(med.cpu().numpy(), e.tile_offsets_median)
+    np.testing.assert_array_equal(tog.cpu().numpy(), e.tile_offsets_global)
     c = zs.make_zipserv_compressed(parts)
     np.testing.assert_array_equal(from_torch_bf16(zs.decompress(c)), W)
 

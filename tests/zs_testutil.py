@@ -17,6 +17,25 @@ def weights_bf16(rng, shape, std=0.02, outlier_frac=0.0, outlier_scale=30.0):
     return zo.f32_to_bf16(w)
 
 
+# bf16 bit patterns a codec must carry unchanged: +-0, +-Inf, quiet and
+# signalling NaNs with payloads, the smallest and largest subnormals, the
+# largest finite value
+SPECIAL_BF16 = np.array([0x0000, 0x8000, 0x7F80, 0xFF80, 0x7FC0, 0xFFC1, 0x7F81, 0x0001, 0x8001,
+                         0x007F, 0x807F, 0x7F7F, 0xFF7F], np.uint16)
+
+
+def arbitrary_bf16(rng, shape, kind):
+    """"random_bits": every 16-bit pattern equally likely (mostly outliers,
+    NaNs and Infs included); "specials": N(0, 0.02) weights with 5% of the
+    elements replaced by SPECIAL_BF16 values."""
+    if kind == "random_bits":
+        return rng.integers(0, 65536, size=shape, dtype=np.uint16)
+    W = weights_bf16(rng, shape)
+    n = W.size // 20
+    W.flat[rng.integers(0, W.size, n)] = rng.choice(SPECIAL_BF16, n)
+    return W
+
+
 def kv_bf16(rng, batch, tokens, heads, dim):
     """KV ~ N(0,1) * per-(head, channel) lognormal(0,1) scales (benchmark config 4)."""
     scales = np.exp(rng.standard_normal((1, 1, heads, dim))).astype(np.float32)
