@@ -646,7 +646,8 @@ def kernel_name(N, M, split_k, K):
     rgemm_wide_kernel<NB, 4, PH, 2> with NB = 2, 4 or 8
     column blocks, 4 row bands, 4 K phases when M/64 * split_k <= the CU
     count (2 otherwise), records 2 steps ahead; N > 32 on grids of >= 160 128-row
-    workgroups -> rgemm_wide2_kernel<NB, 8, 2> (two bands per wave);
+    workgroups, and 16 < N <= 32 on such grids of one or two slices ->
+    rgemm_wide2_kernel<NB, 8, 2> (two bands per wave);
     4 <= N <= 16 on grids of M/64 * split_k >= 7/8 of the CU count ->
     rgemm_wide_kernel<1, 4, PH, 2>; NB = 8 outside the two-band case takes 3
     K phases when the split-K slice has >= 48 K tiles."""
@@ -665,6 +666,8 @@ def kernel_name(N, M, split_k, K):
         xd = 1 if N <= 2 else (2 if N <= 4 else (4 if N <= 8 else 0))
         return f"zs::rgemm_kernel<{f}, 1, {waves}, {4 if f == 1 else 3}, {xd}>"
     nb = 2 if nb <= 2 else (4 if nb <= 4 else 8)
+    if nb == 2 and M % 128 == 0 and split_k <= 2 and (M // 128) * split_k >= 160:
+        return "zs::rgemm_wide2_kernel<2, 8, 2>"
     if nb == 8 and M % 128 == 0 and (M // 128) * split_k * ((N + 127) // 128) >= 160:
         return "zs::rgemm_wide2_kernel<8, 8, 2>"
     if nb == 4 and M % 128 == 0 and (M // 128) * split_k >= 160:

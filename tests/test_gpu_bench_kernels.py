@@ -9,11 +9,12 @@ import zipserv_asplos26_amd as zs
 pytestmark = pytest.mark.gpu
 
 # (M, K, N, split_k): N = 1 on 640 / 896 bands (8 / 4 waves), N = 8 and 16 on
-# the 16-row kernels and the 64-row one-column-block kernel, N = 32 / 64 /
-# 128 with 4 and 2 K phases, three-phase NB = 8 and both two-band kernels,
-# and the stream-K schedule
+# the 16-row kernels and the 64-row one-column-block kernel, N = 24 / 32 /
+# 64 / 128 with 4 and 2 K phases, three-phase NB = 8, the two-band kernels
+# at NB = 2 / 4 / 8, and the stream-K schedule
 CASES = [(10240, 1024, 1, 1), (14336, 1024, 1, 1), (4096, 1024, 8, 1), (14336, 1024, 8, 1),
          (6144, 1024, 16, 1), (4096, 1024, 16, 1), (4096, 1024, 32, 1), (14336, 1024, 32, 2),
+         (28672, 1024, 32, 1), (28672, 1024, 24, 4), (10240, 1024, 32, 2),
          (4096, 1024, 64, 4), (28672, 1024, 64, 1), (6144, 4096, 128, 1), (6144, 1024, 128, 1),
          (28672, 1024, 128, 1), (4096, 1024, 8, 0)]
 
