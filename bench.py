@@ -645,9 +645,9 @@ def kernel_name(N, M, split_k, K):
     N <= 4, 4 for N <= 8, none (0) above); N > 16 ->
     rgemm_wide_kernel<NB, 4, PH, 2> with NB = 2, 4 or 8
     column blocks, 4 row bands, 4 K phases when M/64 * split_k <= the CU
-    count (2 otherwise), records 2 steps ahead; N > 32 on grids of >= 160 128-row
-    workgroups, and 16 < N <= 32 on such grids of one or two slices ->
-    rgemm_wide2_kernel<NB, 8, 2> (two bands per wave);
+    count (2 otherwise), records 2 steps ahead; on grids of >= 160 128-row
+    workgroups rgemm_wide2_kernel<NB, 8, 2> (two bands per wave) instead,
+    for N > 64 at any split-K and for 16 < N <= 64 at split-K 1 or 2;
     4 <= N <= 16 on grids of M/64 * split_k >= 7/8 of the CU count ->
     rgemm_wide_kernel<1, 4, PH, 2>; NB = 8 outside the two-band case takes 3
     K phases when the split-K slice has >= 48 K tiles."""
@@ -670,7 +670,7 @@ def kernel_name(N, M, split_k, K):
         return "zs::rgemm_wide2_kernel<2, 8, 2>"
     if nb == 8 and M % 128 == 0 and (M // 128) * split_k * ((N + 127) // 128) >= 160:
         return "zs::rgemm_wide2_kernel<8, 8, 2>"
-    if nb == 4 and M % 128 == 0 and (M // 128) * split_k >= 160:
+    if nb == 4 and M % 128 == 0 and split_k <= 2 and (M // 128) * split_k >= 160:
         return "zs::rgemm_wide2_kernel<4, 8, 2>"
     ph = 4 if (nb <= 4 and (M // 64) * split_k <= cus) else 2
     if nb == 8 and ((K // 64) - 1) // split_k + 1 >= 48:

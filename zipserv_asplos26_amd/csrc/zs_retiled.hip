@@ -2456,7 +2456,9 @@ static int retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exp
     else if (nb <= 2)
       e = ph4 ? launch_rwide<2, 4, 4>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx)
               : launch_rwide<2, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
-    else if (nb <= 4 && M % 128 == 0 && (int64_t)(M / 128) * split_k >= 160)
+    else if (nb <= 4 && M % 128 == 0 && split_k <= 2 && (int64_t)(M / 128) * split_k >= 160)
+      // (with four slices one band per wave is faster: 8192 rows at N = 48 /
+      // 64, 83 -> 80 us)
       e = launch_rwide2<4, 8, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k,
                                  kb_per_split, fx);
     else if (nb <= 4)
