@@ -650,7 +650,7 @@ def kernel_name(N, M, split_k, K):
     for N > 64 at any split-K and for 16 < N <= 64 at split-K 1 or 2;
     4 <= N <= 16 on grids of M/64 * split_k >= 7/8 of the CU count ->
     rgemm_wide_kernel<1, 4, PH, 2>; NB = 8 outside the two-band case takes 3
-    K phases when the split-K slice has >= 48 K tiles."""
+    K phases when the split-K slice has >= 32 K tiles."""
     import torch
     nb = (N + 15) // 16
     cus = torch.cuda.get_device_properties(0).multi_processor_count
@@ -673,7 +673,7 @@ def kernel_name(N, M, split_k, K):
     if nb == 4 and M % 128 == 0 and split_k <= 2 and (M // 128) * split_k >= 160:
         return "zs::rgemm_wide2_kernel<4, 8, 2>"
     ph = 4 if (nb <= 4 and (M // 64) * split_k <= cus) else 2
-    if nb == 8 and ((K // 64) - 1) // split_k + 1 >= 48:
+    if nb == 8 and ((K // 64) - 1) // split_k + 1 >= 32:
         ph = 3
     return f"zs::rgemm_wide_kernel<{nb}, 4, {ph}, 2>"
 

@@ -15,7 +15,8 @@ pytestmark = pytest.mark.gpu
 CASES = [(10240, 1024, 1, 1), (14336, 1024, 1, 1), (4096, 1024, 8, 1), (14336, 1024, 8, 1),
          (6144, 1024, 16, 1), (4096, 1024, 16, 1), (4096, 1024, 32, 1), (14336, 1024, 32, 2),
          (28672, 1024, 32, 1), (28672, 1024, 24, 4), (10240, 1024, 32, 2),
-         (4096, 1024, 64, 4), (28672, 1024, 64, 1), (8192, 1024, 48, 4), (14336, 1024, 64, 2), (6144, 4096, 128, 1), (6144, 1024, 128, 1),
+         (4096, 1024, 64, 4), (28672, 1024, 64, 1), (8192, 1024, 48, 4), (14336, 1024, 64, 2), (6144, 4096, 128, 1), (6144, 1024, 128, 1), (6144, 4096, 128, 2),
+         (4096, 4096, 128, 4),
          (28672, 1024, 128, 1), (4096, 1024, 8, 0)]
 
 

@@ -2469,10 +2469,11 @@ static int retiled_mm(void* stream, const uint8_t* d_fixed, const uint8_t* d_exp
       // once the 128-row grid still has >= 160 workgroups (measured)
       e = launch_rwide2<8, 8, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k,
                                  kb_per_split, fx);
-    else if (kb_per_split >= 48)
+    else if (kb_per_split >= 32)
       // three K phases (12 waves, 3 per SIMD, B fragments read next to
-      // their MFMAs) on long slices: 2-10% faster than two phases with the
-      // early B reads; on slices of <= 32 tiles the uneven phases cost more
+      // their MFMAs) on slices of >= 32 tiles: 2-10% faster than two phases
+      // with the early B reads (4096-deep slices of 32 tiles: ~5%); on
+      // slices of 16 tiles the uneven phases cost about what they gain
       e = launch_rwide<8, 4, 3>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
     else
       e = launch_rwide<8, 4, 2>(st, d_fixed, d_exps, d_eoff, se, B, out, M, N, K, split_k, kb_per_split, fx);
