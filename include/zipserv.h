@@ -232,6 +232,17 @@ int zs_compress_retiled_auto_gpu(void* stream, const uint16_t* d_input, int M, i
                                  uint64_t* d_hist, int32_t* d_top, uint8_t* d_work,
                                  uint8_t* d_fixed, int32_t* d_counts, int32_t* d_eoff,
                                  int64_t* d_total, uint8_t* d_tmp);
+/* zs_compress_retiled_auto_gpu with the guess taken from d_guess (7 int32
+ * window exponents in device memory, e.g. d_top of the previous matrix of a
+ * model's weights, which share one window) instead of a sample of the input:
+ * one small launch instead of the sample and its selection.  The outputs are
+ * the same bytes whatever d_guess holds (a wrong guess costs the second
+ * encoding).  d_guess must not alias d_top.  No counterpart in the
+ * reference (no GPU encoder of weights there). */
+int zs_compress_retiled_guess_gpu(void* stream, const uint16_t* d_input, int M, int K, int rule,
+                                  const int32_t* d_guess, uint64_t* d_hist, int32_t* d_top,
+                                  uint8_t* d_work, uint8_t* d_fixed, int32_t* d_counts,
+                                  int32_t* d_eoff, int64_t* d_total, uint8_t* d_tmp);
 int zs_compress_retiled_exps_gpu(void* stream, const uint16_t* d_input, int M, int K,
                                  const int32_t* d_top_exponents, const int32_t* d_eoff,
                                  const uint8_t* d_tmp, uint8_t* d_exps);

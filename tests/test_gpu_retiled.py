@@ -547,6 +547,62 @@ def test_explicit_window_encoder_bytes(torch_cuda, first):
     np.testing.assert_array_equal(from_torch_bf16(zs.decompress_retiled(r)), W)
 
 
+@pytest.mark.parametrize("rule", ["kv", "weights"])
+def test_guess_encoder_equals_sampled_guess(torch_cuda, rule):
+    # zs_compress_retiled_guess_gpu with a wrong guess (a window no element
+    # falls in) and with the right one writes what zs_compress_retiled_auto_gpu
+    # writes; a null guess, or one aliasing d_top, is refused
+    torch = torch_cuda
+    import zipserv_asplos26_amd._lib as zl
+    L = zs.lib()
+    rng = np.random.default_rng(97)
+    W = weights_bf16(rng, (512, 1024), outlier_frac=0.02)
+    x = to_torch_bf16(W)
+    rows, cols = W.shape
+    nrec = rows // 16 * (cols // 64)
+    rl = zl.ZS_WINDOW_KV if rule == "kv" else zl.ZS_WINDOW_WEIGHTS
+    st = torch.cuda.current_stream().cuda_stream
+
+    def bufs():
+        return dict(hist=torch.empty(256, dtype=torch.int64, device="cuda"),
+                    top=torch.empty(7, dtype=torch.int32, device="cuda"),
+                    work=torch.empty(zl.ZS_RETILED_AUTO_WORK_BYTES, dtype=torch.uint8, device="cuda"),
+                    fixed=torch.empty(nrec * 1408, dtype=torch.uint8, device="cuda"),
+                    cnt=torch.empty(nrec, dtype=torch.int32, device="cuda"),
+                    eoff=torch.empty(nrec + 1, dtype=torch.int32, device="cuda"),
+                    total=torch.empty(1, dtype=torch.int64, device="cuda"),
+                    tmp=torch.empty(nrec * zl.ZS_RETILED_EXP_SLOT_BYTES, dtype=torch.uint8,
+                                    device="cuda"))
+
+    def args(b):
+        return [b[k].data_ptr() for k in ("hist", "top", "work", "fixed", "cnt", "eoff", "total", "tmp")]
+    ref = bufs()
+    assert L.zs_compress_retiled_auto_gpu(st, x.data_ptr(), rows, cols, rl, *args(ref)) == 0
+    right = ref["top"].clone()
+    wrong = torch.arange(200, 207, dtype=torch.int32, device="cuda")
+    for guess in (wrong, right):
+        b = bufs()
+        assert L.zs_compress_retiled_guess_gpu(st, x.data_ptr(), rows, cols, rl, guess.data_ptr(),
+                                               *args(b)) == 0
+        torch.cuda.synchronize()
+        for k in ("hist", "top", "fixed", "cnt", "eoff", "total"):
+            assert torch.equal(b[k], ref[k]), k
+        tot = int(ref["total"].item())
+        # slots hold the outlier bytes of each record (the rest is unspecified)
+        exps_a = torch.empty(tot + 64, dtype=torch.uint8, device="cuda")
+        exps_b = torch.empty(tot + 64, dtype=torch.uint8, device="cuda")
+        for bb, e in ((ref, exps_a), (b, exps_b)):
+            assert L.zs_compress_retiled_exps_gpu(st, x.data_ptr(), rows, cols, bb["top"].data_ptr(),
+                                                  bb["eoff"].data_ptr(), bb["tmp"].data_ptr(),
+                                                  e.data_ptr()) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(exps_a, exps_b)
+    b = bufs()
+    assert L.zs_compress_retiled_guess_gpu(st, x.data_ptr(), rows, cols, rl, None, *args(b)) == zl.ZS_E_INVAL
+    assert L.zs_compress_retiled_guess_gpu(st, x.data_ptr(), rows, cols, rl, b["top"].data_ptr(),
+                                           *args(b)) == zl.ZS_E_INVAL
+
+
 @pytest.mark.parametrize("window,lookahead", [("kv", 2), ("weights", 0), ("explicit", 9)])
 def test_batched_encoder_equals_one_call_per_matrix(torch_cuda, window, lookahead):
     # compress_retiled_many (outlier totals read back asynchronously, the

@@ -67,6 +67,8 @@ SIGNATURES = {
                                                 _p]),
     "zs_compress_retiled_auto_gpu": (C.c_int, [_p, _p, C.c_int, C.c_int, C.c_int, _p, _p, _p, _p, _p,
                                                _p, _p, _p]),
+    "zs_compress_retiled_guess_gpu": (C.c_int, [_p, _p, C.c_int, C.c_int, C.c_int, _p, _p, _p, _p,
+                                                _p, _p, _p, _p, _p]),
     "zs_compress_retiled_exps_gpu": (C.c_int, [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p]),
     "zs_retile_triple_bitmap_count_gpu": (
         C.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, C.c_int, C.c_int, _p, _p, _p]),

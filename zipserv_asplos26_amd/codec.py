@@ -490,12 +490,14 @@ def _retiled_alloc(rows, cols, total, dev):
     return fixed, exps, nrec
 
 
-def _retiled_encode(input, window):
+def _retiled_encode(input, window, guess=None):
     """First phase of the re-tiled GPU encoder on the current stream: the
     window, the fixed parts, the per-record outlier counts and offsets, and
     the outlier bytes in per-record slots; the outlier total and the window
     land in one int64 [5] tensor (`meta`) that the host reads to size the
-    exponent stream.  Returns the state _retiled_finish takes."""
+    exponent stream.  Under a window rule, `guess` (int32 [7] on the device,
+    e.g. the previous matrix's window) replaces the sampled guess; the bytes
+    are the same either way.  Returns the state _retiled_finish takes."""
     torch = _torch()
     _check_cuda(input, "input", torch.bfloat16)
     if input.dim() != 2:
@@ -522,10 +524,18 @@ def _retiled_encode(input, window):
         rule = _lib.ZS_WINDOW_KV if window == "kv" else _lib.ZS_WINDOW_WEIGHTS
         work = torch.empty(_lib.ZS_RETILED_AUTO_WORK_BYTES, dtype=torch.uint8, device=dev)
         # 64-bit bins: the re-tiled layout takes matrices past 2^31 elements.
-        check("zs_compress_retiled_auto_gpu",
-              L.zs_compress_retiled_auto_gpu(st, _dptr(input), rows, cols, rule, _dptr(counts),
-                                             _dptr(top), _dptr(work), _dptr(fixed), _dptr(cnt),
-                                             _dptr(eoff), _dptr(total), _dptr(tmp)))
+        if guess is not None:
+            _check_cuda(guess, "guess", torch.int32)
+            check("zs_compress_retiled_guess_gpu",
+                  L.zs_compress_retiled_guess_gpu(st, _dptr(input), rows, cols, rule, _dptr(guess),
+                                                  _dptr(counts), _dptr(top), _dptr(work),
+                                                  _dptr(fixed), _dptr(cnt), _dptr(eoff),
+                                                  _dptr(total), _dptr(tmp)))
+        else:
+            check("zs_compress_retiled_auto_gpu",
+                  L.zs_compress_retiled_auto_gpu(st, _dptr(input), rows, cols, rule, _dptr(counts),
+                                                 _dptr(top), _dptr(work), _dptr(fixed), _dptr(cnt),
+                                                 _dptr(eoff), _dptr(total), _dptr(tmp)))
     else:
         _device_window(input, window, top, counts)
         check("zs_compress_retiled_fixed_gpu",
@@ -581,11 +591,16 @@ def compress_retiled_many(inputs, window="kv", layout="by_kv_head", lookahead=2)
     `lookahead` matrices are queued behind it.  Same bytes as one call per
     matrix (a model's weights are compressed this way, layer by layer).  At
     most lookahead + 1 matrices hold their outlier slots (256 bytes per 1024
-    elements, an eighth of the bf16 bytes) at once."""
+    elements, an eighth of the bf16 bytes) at once.  Under a window rule each
+    matrix after the first takes the previous one's window as its guess
+    (zs_compress_retiled_guess_gpu: no sample of its input; a model's
+    matrices share one window, and a wrong guess only costs a second
+    encoding pass)."""
     torch = _torch()
     if lookahead < 0:
         raise ValueError("lookahead must be >= 0")
     out, pending = [], []
+    prev_top = None  # kept referenced until the next matrix's encoder is queued
 
     def finish_oldest():
         s, host, done = pending.pop(0)
@@ -593,7 +608,10 @@ def compress_retiled_many(inputs, window="kv", layout="by_kv_head", lookahead=2)
         out.append(_retiled_finish(s, host, None, None, layout))
 
     for x in inputs:
-        s = _retiled_encode(x, window)
+        rule = isinstance(window, str)
+        same_dev = prev_top is not None and prev_top.device == x.device
+        s = _retiled_encode(x, window, guess=prev_top if rule and same_dev else None)
+        prev_top = s["top"]
         host = torch.empty(5, dtype=torch.int64, pin_memory=True)
         host.copy_(s["meta"], non_blocking=True)
         done = torch.cuda.Event()

@@ -2274,10 +2274,15 @@ constexpr int kWorkSample = kHistSlices * 256 * 8, kWorkGuess = 2 * kWorkSample,
               kWorkDiffers = kWorkGuess + 32, kWorkArrive = kWorkDiffers + 4;
 static_assert(kWorkArrive + 4 <= ZS_RETILED_AUTO_WORK_BYTES, "auto encoder scratch");
 
-extern "C" int zs_compress_retiled_auto_gpu(void* stream, const uint16_t* d_input, int M, int K,
-                                            int rule, uint64_t* d_hist, int32_t* d_top,
-                                            uint8_t* d_work, uint8_t* d_fixed, int32_t* d_counts,
-                                            int32_t* d_eoff, int64_t* d_total, uint8_t* d_tmp) {
+__global__ void zero_i32_kernel(int32_t* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+static int retiled_auto(void* stream, const uint16_t* d_input, int M, int K, int rule,
+                        const int32_t* d_guess, uint64_t* d_hist, int32_t* d_top, uint8_t* d_work,
+                        uint8_t* d_fixed, int32_t* d_counts, int32_t* d_eoff, int64_t* d_total,
+                        uint8_t* d_tmp) {
   if (!shape_ok(M, K) || !d_input || !d_hist || !d_top || !d_work || !d_fixed || !d_counts ||
       !d_eoff || !d_total || !d_tmp || (rule != ZS_WINDOW_KV && rule != ZS_WINDOW_WEIGHTS))
     return ZS_E_INVAL;
@@ -2293,9 +2298,17 @@ extern "C" int zs_compress_retiled_auto_gpu(void* stream, const uint16_t* d_inpu
   int32_t* guess = reinterpret_cast<int32_t*>(d_work + kWorkGuess);
   int32_t* differs = reinterpret_cast<int32_t*>(d_work + kWorkDiffers);
   int32_t* arrive = reinterpret_cast<int32_t*>(d_work + kWorkArrive);  // the scan's counter
-  hipError_t e = launch_window_sample(st, d_input, (int64_t)M * K, weights, sample, slices, guess,
-                                      arrive);
-  if (e != hipSuccess) return status_of(e);
+  if (d_guess) {
+    // the caller's window as the guess: only the histogram slices and the
+    // scan's counter need clearing (one fill over the start of d_work)
+    hipLaunchKernelGGL(zero_i32_kernel, dim3((kWorkArrive / 4 + 1 + 255) / 256), dim3(256), 0, st,
+                       reinterpret_cast<int32_t*>(d_work), (int64_t)(kWorkArrive / 4 + 1));
+    guess = const_cast<int32_t*>(d_guess);
+  } else {
+    const hipError_t e = launch_window_sample(st, d_input, (int64_t)M * K, weights, sample, slices,
+                                              guess, arrive);
+    if (e != hipSuccess) return status_of(e);
+  }
   const int hist_grid = r_grid(nrec, 4);
   hipLaunchKernelGGL(rfixed_kernel<true>, dim3(hist_grid), dim3(256), 0, st, d_input, M, K, guess,
                      d_fixed, d_counts, d_tmp, slices, nullptr, WindowCheck{});
@@ -2306,6 +2319,24 @@ extern "C" int zs_compress_retiled_auto_gpu(void* stream, const uint16_t* d_inpu
                      nullptr, WindowCheck{slices, d_hist, d_top, guess, differs, weights ? 1 : 0});
   launch_rscan(st, d_counts, nrec, d_eoff, d_total, arrive);
   return status_of(hipGetLastError());
+}
+
+extern "C" int zs_compress_retiled_auto_gpu(void* stream, const uint16_t* d_input, int M, int K,
+                                            int rule, uint64_t* d_hist, int32_t* d_top,
+                                            uint8_t* d_work, uint8_t* d_fixed, int32_t* d_counts,
+                                            int32_t* d_eoff, int64_t* d_total, uint8_t* d_tmp) {
+  return retiled_auto(stream, d_input, M, K, rule, nullptr, d_hist, d_top, d_work, d_fixed,
+                      d_counts, d_eoff, d_total, d_tmp);
+}
+
+extern "C" int zs_compress_retiled_guess_gpu(void* stream, const uint16_t* d_input, int M, int K,
+                                             int rule, const int32_t* d_guess, uint64_t* d_hist,
+                                             int32_t* d_top, uint8_t* d_work, uint8_t* d_fixed,
+                                             int32_t* d_counts, int32_t* d_eoff, int64_t* d_total,
+                                             uint8_t* d_tmp) {
+  if (!d_guess || d_guess == d_top) return ZS_E_INVAL;
+  return retiled_auto(stream, d_input, M, K, rule, d_guess, d_hist, d_top, d_work, d_fixed,
+                      d_counts, d_eoff, d_total, d_tmp);
 }
 
 extern "C" int zs_compress_retiled_exps_gpu(void* stream, const uint16_t* d_input, int M, int K,
@@ -2576,11 +2607,6 @@ constexpr int64_t kScratchBytes = kScratchSlabBytes + 4 * kScratchCounters;
 constexpr int kScratchMaxDevices = 64;
 
 __device__ __align__(256) uint8_t scratch[kScratchBytes];
-
-__global__ void zero_i32_kernel(int32_t* p, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
-}
 
 // Per-device address of `scratch`, looked up (and its counters cleared on
 // `st`) by the first call on that device.  0 / a hipError_t status.
