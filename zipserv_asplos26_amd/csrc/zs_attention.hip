@@ -1030,10 +1030,11 @@ static bool tm_fused(int heads_k, int cols) { return heads_k == kTmHeads && cols
 // Splits of the fused token-major kernel: one 8-wave workgroup per (batch,
 // split), about kTmItems of them (two per CU), at least kTmMinTokens
 // tokens and at most kTmMaxSplits splits per sequence (the combine reads
-// every split's partial of every head); an explicit count is used as given
-// (at most one split per 16 tokens).  The chunk is a multiple of 16 tokens
-// (a step).  Measured over B = 1 / 8 / 32, T = 4k..32k: the best of 16..512
-// splits in every case.
+// every split's partial of every head), or one per CU when two per CU would
+// leave chunks under 128 tokens; an explicit count is used as given (at
+// most one split per 16 tokens).  The chunk is a multiple of 16 tokens (a
+// step).  Measured over B = 1..32, T = 2k..32k, each count timed after a
+// warm-up in both orders: within 3% of the best of 8..256 splits.
 constexpr int kTmItems = 512;
 constexpr int kTmMinTokens = 32;
 constexpr int kTmMaxSplits = 256;
@@ -1042,8 +1043,13 @@ static int tm_splits(int batch, int seqlen_k, int num_splits) {
   const int steps = std::max(1, (seqlen_k + 15) / 16);
   if (num_splits > 0) return std::min(num_splits, steps);
   const int max_splits = std::max(1, (seqlen_k + kTmMinTokens - 1) / kTmMinTokens);
-  return std::min(std::min(max_splits, kTmMaxSplits),
-                  std::max(1, (kTmItems + batch - 1) / batch));
+  int s = std::min(std::min(max_splits, kTmMaxSplits), std::max(1, (kTmItems + batch - 1) / batch));
+  // More than one workgroup per CU with chunks under 128 tokens: one round
+  // of them (the two-step ring with phase pairs) is faster (B = 8, T = 2k /
+  // 4k: 28.0 -> 24.0 / 35.9 -> 34.2 us; B = 4, T = 4k: 26.0 -> 24.5 us).
+  if ((int64_t)batch * s > device_cu_count() && seqlen_k < 128 * s)
+    s = std::max(1, (device_cu_count() + batch - 1) / batch);
+  return s;
 }
 
 static int tm_chunk(int seqlen_k, int splits) {
