@@ -250,7 +250,7 @@ __device__ __forceinline__ u32x4 decode_row(const Streams& s, const DecodeTables
 // Returns the two MFMA A operands.
 struct HalfDec {
   uint32_t b1, b2, b3, ind;
-  int n, excl, incl;
+  int n, excl;
 };
 
 __device__ __forceinline__ void decode_median_pair(const DecodeTables& T, const uint4* e1,
@@ -270,10 +270,15 @@ __device__ __forceinline__ void decode_median_pair(const DecodeTables& T, const 
   for (int h = 0; h < 2; ++h) {
     d[h].ind = d[h].b1 | d[h].b2 | d[h].b3;
     d[h].n = __builtin_popcount(d[h].ind);
-    d[h].incl = wave_inclusive_scan(d[h].n);
-    d[h].excl = d[h].incl - d[h].n;
   }
-  const int tot0 = __builtin_amdgcn_readlane(d[0].incl, 63);
+  // Both halves' in-window counts go through one wave scan, 16 bits each (a
+  // half holds at most 512 of them).
+  const int nn = d[0].n | (d[1].n << 16);
+  const int incl = wave_inclusive_scan(nn);
+  const int excl = incl - nn;
+  const int tot0 = __builtin_amdgcn_readlane(incl, 63) & 0xFFFF;
+  d[0].excl = excl & 0xFFFF;
+  d[1].excl = excl >> 16;
   u32x4 o[2];
   int fo[2];
 #pragma unroll

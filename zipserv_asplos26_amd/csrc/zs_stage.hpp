@@ -102,28 +102,29 @@ __device__ __forceinline__ void stage_issue(const Streams& s, const uint8_t* bm_
   // Every lane issues exactly two 16-byte loads (addresses clamped to valid
   // data when the lane has nothing to fetch) so the number of loads in flight
   // is the same on every path and the waits stay precise.
+  // Lane roles by select, not by branch: lanes 24..56 take FULL chunk l - 24
+  // when it exists and the outliers fit, lanes 57..63 SM chunk 64 when the
+  // median tile has one; every other lane re-reads its bitmap chunk.
   r.sm = *reinterpret_cast<const u32x4*>(s.sm + a0 + (l < nch ? 16 * l : 0));
+  const int fi = l - 24;
+  const bool full_lane = fi >= 0 && fi < kFullChunks && fi < nfc && nfc <= kFullChunks;
+  const bool sm_lane = fi >= kFullChunks && nch > 64;
   const uint8_t* mp = bm_lane + 512 * g + 128 * m + 16 * (l & 7);
-  if (l >= 24) {
-    if (l < 24 + kFullChunks) {
-      if (l - 24 < nfc && nfc <= kFullChunks)
-        mp = reinterpret_cast<const uint8_t*>(s.full + fa0 + 8 * (l - 24));
-    } else if (l == 24 + kFullChunks && nch > 64) {
-      mp = s.sm + a0 + 1024;
-    }
-  }
+  mp = full_lane ? reinterpret_cast<const uint8_t*>(s.full + fa0) + 16 * fi
+                 : (sm_lane ? s.sm + a0 + 1024 : mp);
   r.misc = *reinterpret_cast<const u32x4*>(mp);
 }
 
+// Every lane writes its misc chunk: lanes 0..23 the bitmap planes, 24..56 the
+// FULL chunks, 57..63 the same SM chunk 64 (identical data when it exists;
+// otherwise bytes past the median tile's SM bytes, which no decode selects).
+// FULL chunks past the tile's outliers hold bitmap bytes, also never selected.
 __device__ __forceinline__ void stage_write(uint8_t* st, const StageRegs& r) {
   const int l = lane_id();
   *reinterpret_cast<u32x4*>(st + kStSm + 16 * l) = r.sm;
-  if (l < 24)
-    *reinterpret_cast<u32x4*>(st + kStBm + 16 * l) = r.misc;
-  else if (l < 24 + kFullChunks)
-    *reinterpret_cast<u32x4*>(st + kStFull + 16 * (l - 24)) = r.misc;
-  else if (l == 24 + kFullChunks)
-    *reinterpret_cast<u32x4*>(st + kStSm + 1024) = r.misc;
+  const int dst = l < 24 ? kStBm + 16 * l
+                         : (l < 24 + kFullChunks ? kStFull + 16 * (l - 24) : kStSm + 1024);
+  *reinterpret_cast<u32x4*>(st + dst) = r.misc;
 }
 
 }  // namespace zs
