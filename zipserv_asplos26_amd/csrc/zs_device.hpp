@@ -299,10 +299,11 @@ __device__ __forceinline__ void decode_median_pair(const DecodeTables& T, const 
       merge_outliers4(T, d[h].ind, __builtin_amdgcn_alignbyte(q1, q0, fsh),
                       __builtin_amdgcn_alignbyte(q2, q1, fsh), o[h]);
     }
+    // Rows with more than four outliers (fewer than four in-window elements;
+    // rare) patch the rest one by one; one wave-wide test skips it all.
+    if (__builtin_amdgcn_ballot_w64(d[0].n < 4 || d[1].n < 4))
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      // Rows with more than four outliers (fewer than four in-window
-      // elements; rare) patch the rest one by one.
       if (d[h].n < 4) {
         uint32_t rest = (~d[h].ind) & 0xFFu;
         rest &= rest - 1;

@@ -102,9 +102,9 @@ __device__ __forceinline__ void stage_issue(const Streams& s, const uint8_t* bm_
   // Every lane issues exactly two 16-byte loads (addresses clamped to valid
   // data when the lane has nothing to fetch) so the number of loads in flight
   // is the same on every path and the waits stay precise.
-  // Lane roles by select, not by branch: lanes 24..56 take FULL chunk l - 24
-  // when it exists and the outliers fit, lanes 57..63 SM chunk 64 when the
-  // median tile has one; every other lane re-reads its bitmap chunk.
+  // Lane roles: lanes 24..56 take FULL chunk l - 24 when it exists and the
+  // outliers fit, lanes 57..63 SM chunk 64 when the median tile has one;
+  // every other lane re-reads its bitmap chunk.
   r.sm = *reinterpret_cast<const u32x4*>(s.sm + a0 + (l < nch ? 16 * l : 0));
   const int fi = l - 24;
   const bool full_lane = fi >= 0 && fi < kFullChunks && fi < nfc && nfc <= kFullChunks;
