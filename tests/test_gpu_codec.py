@@ -276,6 +276,35 @@ def test_zipgemm_64row_unit_vectors_exact(torch_cuda, M, split_k):
         np.testing.assert_array_equal(Y[i], W[:, k])
 
 
+@pytest.mark.parametrize("M,N,split_k,shift", [(128, 15, 1, 4), (128, 15, 2, 4), (10240, 15, 1, 4),
+                                               (10240, 30, 1, 4), (12352, 15, 3, 4), (128, 15, 1, None),
+                                               (10240, 30, 2, None)])
+def test_zipgemm_outlier_dominated_unit_vectors_exact(torch_cuda, M, N, split_k, shift):
+    """Median tiles with more than 264 outliers (33 staged FULL chunks) take
+    their FULL values from global memory instead of the LDS stage.  The window
+    moved `shift` exponents up from the analysed one leaves 262-361 outliers
+    per median tile (both paths in one matrix at M = 10240); None: a window
+    far below every exponent, all 1024 elements outliers.  16-row kernel at
+    one slice and N <= 16, 64-row kernel with split-K and at N = 30."""
+    rng = np.random.default_rng(M + N + split_k)
+    K = 256
+    W = weights_bf16(rng, (M, K), outlier_frac=0.01)
+    e0 = zo.compress(W)
+    E0 = e0.start_exp + 1
+    lo = 10 if shift is None else E0 + shift
+    e = zo.compress(W, top=list(range(lo, lo + 7)))
+    ex = (W.astype(np.int64) >> 7) & 0xFF
+    per_tile = ((ex < lo) | (ex > lo + 6)).reshape(M // 16, 16, K // 64, 64).sum(axis=(1, 3))
+    assert per_tile.max() > 264
+    ks = ([0, 7, 8, 31, 32, 63, 64, 65, 100, 127, 128, 191, 192, 200, 255] * 2)[:N]
+    X = np.zeros((N, K), np.uint16)
+    for i, k in enumerate(ks):
+        X[i, k] = 0x3F80
+    Y = from_torch_bf16(zs.zipgemm(upload(e), to_torch_bf16(X), split_k=split_k))
+    for i, k in enumerate(ks):
+        np.testing.assert_array_equal(Y[i], W[:, k])
+
+
 def test_zipgemm_rejects_bad_args(torch_cuda):
     rng = np.random.default_rng(0)
     W = weights_bf16(rng, (64, 128))
